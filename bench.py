@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""bench.py - throughput of the gfx950 quantized expert path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload: Q4 rowwise GEMV at batch 1 at
+both expert shapes, down [2048 x 768] and gate [768 x 2048].  Weights are
+W ~ N(0, 0.02^2) quantized per row on the device with the exporter's rule,
+x ~ N(0, 1).  A step is one pass over a rotating pool of distinct matrices
+(>= 1 GiB per shape, far beyond the 256 MB Infinity Cache) in one batched
+launch per shape, inputs resident in HBM.  `value` is algorithmic GB/s:
+weights + scales + x + y of every GEMV, each counted once.
+
+Other workloads: q8_gemv (configs[0], [768 x 2048]).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "moe.cc_amd"))
+
+import moehip as M  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q8/Q4 expert GEMV GB/s (% HBM peak); decode tok/s at 30B-A3B shape"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(dtype: int, N: int, K: int) -> int:
+    """Algorithmic bytes of one batch-1 GEMV: weights + scales + x + y."""
+    wbytes = N * K if dtype == 2 else N * (K // 2)
+    return wbytes + 4 * N + 4 * K + 4 * N
+
+
+class Pool:
+    """`count` distinct quantized matrices [N x K] in one device allocation,
+    plus a shared x and one output row per matrix, and the job table."""
+
+    def __init__(self, dtype: int, N: int, K: int, count: int, seed: int):
+        self.dtype, self.N, self.K, self.count = dtype, N, K, count
+        rb = K if dtype == 2 else K // 2
+        self.q = M.DeviceBuffer(count * N * rb)
+        self.s = M.DeviceBuffer(count * N * 4)
+        self.x = M.DeviceBuffer(K * 4)
+        self.y = M.DeviceBuffer(count * N * 4)
+        chunk = max(1, min(count, (512 << 20) // (N * K * 4)))
+        tmp = M.DeviceBuffer(chunk * N * K * 4)
+        L = M.lib()
+        for c0 in range(0, count, chunk):
+            n = min(chunk, count - c0)
+            M.check(L.moe_fill_normal_dev(tmp.ptr, n * N * K, seed + c0, 0.0, 0.02), "fill")
+            M.check(L.moe_quantize_rows_dev(dtype, tmp.ptr, n * N, K, self.q.ptr + c0 * N * rb,
+                                            self.s.ptr + c0 * N * 4), "quantize")
+        tmp.free()
+        M.check(L.moe_fill_normal_dev(self.x.ptr, K, seed + 999983, 0.0, 1.0), "fill x")
+        jobs = (M.QJob * count)()
+        for i in range(count):
+            jobs[i] = M.QJob(self.q.ptr + i * N * rb, self.s.ptr + i * N * 4, self.x.ptr,
+                             self.y.ptr + i * N * 4)
+        self.jobs = M.DeviceBuffer(ctypes.sizeof(jobs))
+        M.check(L.moe_memcpy_h2d(self.jobs.ptr, ctypes.addressof(jobs), ctypes.sizeof(jobs)))
+        M.synchronize()
+        self.bytes_per_launch = count * gemv_bytes(dtype, N, K)
+        self.weight_bytes = count * N * rb
+
+    def launch(self):
+        M.check(M.lib().moe_matmul_q_batched_dev(self.dtype, self.jobs.ptr, self.count, 1,
+                                                 self.N, self.K), "batched gemv")
+
+
+def kernel_name(dtype, N, K):
+    return M.gemv_variant(dtype, 1, N, K)
+
+
+def cpu_baseline(shapes, budget_s: float):
+    """Reference kernels.c (oracle/_ref, built from the reference sources) or
+    the oracle restatement, single thread on this host, batch-1 GEMVs over a
+    small rotating pool of each shape."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    kind = "reference" if os.path.exists(O.REF_KERNELS_LIB) else "port"
+    fn = O.ref_kernels().matmul_adaptive if kind == "reference" else O.orc().orc_matmul_adaptive
+    pool = 6
+    tot_bytes, tot_s, calls = 0, 0.0, 0
+    per = budget_s / len(shapes)
+    for dtype, N, K in shapes:
+        mats = []
+        for i in range(pool):
+            W = O.normal(N * K, 4242 + i, 0.0, 0.02).reshape(N, K)
+            q, s = (O.quant_q8 if dtype == 2 else O.quant_q4)(W)
+            mats.append((q, s, O.QW(q.ctypes.data, s.ctypes.data, N, K, dtype)))
+        x = O.normal(K, 77, 0.0, 1.0)
+        y = np.empty(N, np.float32)
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            q, s, qw = mats[n % pool]
+            fn(x.ctypes.data, None, ctypes.addressof(qw), y.ctypes.data, 1, N, K)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= per:
+                break
+        tot_bytes += n * gemv_bytes(dtype, N, K)
+        tot_s += el
+        calls += n
+    return {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{calls} batch-1 GEMVs over {pool} matrices per shape "
+                      f"{[f'{N}x{K}' for _, N, K in shapes]}, {tot_s:.1f} s, 1 thread of "
+                      f"{os.cpu_count()} host cores"}
+
+
+def run_gemv(args, dtype, shapes, workload):
+    M.init(0)
+    pools = []
+    for i, (N, K) in enumerate(shapes):
+        rb = K if dtype == 2 else K // 2
+        count = int(np.ceil(args.pool_gib * (1 << 30) / (N * rb)))
+        log(f"[bench] building pool {N}x{K} dtype {dtype}: {count} matrices")
+        pools.append(Pool(dtype, N, K, count, seed=1000 * (i + 1)))
+    evs = {i: [(M.Event(), M.Event()) for _ in range(args.steps)] for i in range(len(pools))}
+    for _ in range(args.warmup):
+        for p in pools:
+            p.launch()
+    M.synchronize()
+    t_start, t_end = M.Event(), M.Event()
+    wall0 = time.perf_counter()
+    t_start.record()
+    for s in range(args.steps):
+        for i, p in enumerate(pools):
+            a, b = evs[i][s]
+            a.record()
+            p.launch()
+            b.record()
+    t_end.record()
+    M.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_ms(t_end)
+    per_kernel = []
+    for i, p in enumerate(pools):
+        ms = [a.elapsed_ms(b) for a, b in evs[i]]
+        avg = float(np.mean(ms))
+        per_kernel.append({"kernel": f"qgemv_{kernel_name(dtype, p.N, p.K)}",
+                           "shape": f"{p.N}x{p.K}", "matrices_per_launch": p.count,
+                           "avg_launch_us": round(avg * 1e3, 2),
+                           "algorithmic_bytes_per_launch": p.bytes_per_launch,
+                           "achieved_GBs": round(p.bytes_per_launch / (avg * 1e-3) / 1e9, 1)})
+    bytes_step = sum(p.bytes_per_launch for p in pools)
+    ms_step = total_ms / args.steps
+    value = bytes_step / (ms_step * 1e-3) / 1e9
+    dom = max(per_kernel, key=lambda k: k["avg_launch_us"])
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": workload, "batch": 1,
+                   "shapes": [f"{p.N}x{p.K}" for p in pools],
+                   "pool_bytes_per_shape": [p.weight_bytes for p in pools],
+                   "weights": "N(0,0.02^2) rowwise-quantized on device (export.py rule)",
+                   "x": "N(0,1) fp32"},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": dom["kernel"]},
+        "kernels": per_kernel,
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline([(dtype, N, K) for (N, K) in shapes], args.cpu_seconds)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="q4_gemv", choices=["q4_gemv", "q8_gemv"])
+    ap.add_argument("--pool-gib", type=float, default=1.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the expert path on a single MI355X "
+              "(multi-GPU sharding is a design note, not implemented); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.workload == "q4_gemv":
+        out = run_gemv(args, 3, [(2048, 768), (768, 2048)],
+                       "q4_rowwise_gemv_batch1 down[2048x768]+gate[768x2048] (BASELINE configs[1])")
+    else:
+        out = run_gemv(args, 2, [(768, 2048)],
+                       "q8_rowwise_gemv_batch1 gate[768x2048] (BASELINE configs[0])")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,182 @@
+/*
+ * moehip.h - C ABI of libmoehip.so, the gfx950 implementation of moe.cc's
+ * quantized expert path.
+ *
+ * Two layers:
+ *   1. The drop-in: matmul_adaptive() with the exact signature of the
+ *      reference (kernels.h:16-17) and the QuantizedWeight layout of
+ *      model.h:26-31.  A program built against the reference's kernels.o
+ *      links against this library unchanged; it takes host pointers and is
+ *      synchronous, like the reference.
+ *   2. A device-resident API (moe_*) on plain device pointers: GEMVs, the
+ *      MoE block of one layer (test_model_trace.c:460-517) and the
+ *      weight upload from the reference's QwenLayerWeights (model.h:34-58).
+ *
+ * All moe_* functions return 0 on success and a nonzero moe_status on
+ * failure, with a message in moe_last_error().  Device work is queued on the
+ * library's stream (moe_get_stream) and is asynchronous unless stated.
+ * No torch types appear anywhere in this interface.
+ */
+#ifndef MOEHIP_H
+#define MOEHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference-compatible types (layouts identical to model.h) ---- */
+#ifndef QUANTIZED_WEIGHT_DEFINED
+/* model.h:26-31.  dtype 2 = Q8 (int8 [rows x cols]); 3 = Q4 (uint8
+ * [rows x cols/2], low nibble = even column, value = q + 8). */
+typedef struct {
+  const int8_t* q;
+  const float* s;
+  int rows, cols;
+  int dtype;
+} QuantizedWeight;
+#define QUANTIZED_WEIGHT_DEFINED
+#endif
+
+#ifndef MOEHIP_NO_MODEL_TYPES
+/* model.h:9-23 */
+typedef struct {
+  int d_model;
+  int n_layers;
+  int head_dim;
+  int n_q;
+  int n_kv;
+  int d_ff;
+  int n_experts;
+  int top_k;
+  int vocab_size;
+  int causal;
+  float rope_theta;
+  float rms_eps;
+} QwenConfig;
+
+/* model.h:34-58 */
+typedef struct {
+  const float* Wq; const float* bq;
+  const float* Wk; const float* bk;
+  const float* Wv; const float* bv;
+  const float* Wo; const float* bo;
+  const float* q_norm;
+  const float* k_norm;
+  const float* rms1_w;
+  const float* rms2_w;
+  const float* router_w;
+  const float* router_b;
+  const float** Wg; const float** bg;
+  const float** Wu; const float** bu;
+  const float** Wd; const float** bd;
+  QuantizedWeight* Wg_q;
+  QuantizedWeight* Wu_q;
+  QuantizedWeight* Wd_q;
+  int experts_quantized;
+} QwenLayerWeights;
+#endif
+
+/* ==== 1. drop-in ==================================================== */
+
+/* Replaces kernels.c:149-181 (declared at kernels.h:16-17).
+ *   W_q_ptr == NULL : C = A * W_fp32^T, fp32, k ascending (kernels.c:153-165)
+ *   dtype 2 / 3     : rowwise Q8 / Q4 (kernels.c:51-74 / 96-128)
+ *   other dtype     : C is zero-filled (kernels.c:172-179)
+ * A [M x K], W [N x K] (Q4: N x K/2 bytes, rows K/2 bytes apart), C [M x N],
+ * all host memory.  Results are bit-identical to the reference.  Weights are
+ * uploaded on first use and cached by host address (the reference never
+ * mutates them; call moe_weight_cache_clear() after changing a weight in
+ * place).  Errors from the GPU runtime abort the process with a message:
+ * there is no CPU fallback. */
+void matmul_adaptive(const float* A, const float* W_fp32, const void* W_q_ptr,
+                     float* C, int M, int N, int K);
+
+/* ==== 2. device-resident API ======================================== */
+
+typedef int moe_status;
+enum {
+  MOE_OK = 0,
+  MOE_ERR_HIP = 1,        /* a HIP runtime call failed */
+  MOE_ERR_ARG = 2,        /* invalid argument (shape, pointer, dtype) */
+  MOE_ERR_NOMEM = 3,
+  MOE_ERR_UNSUPPORTED = 4
+};
+
+/* Initialises the library on `device` (creates its stream).  Called lazily
+ * with device 0 by every entry point if not called first. */
+moe_status moe_init(int device);
+const char* moe_last_error(void);
+const char* moe_version(void);
+/* hipStream_t the library queues work on */
+void* moe_get_stream(void);
+moe_status moe_synchronize(void);
+/* drops every cached upload made by matmul_adaptive */
+moe_status moe_weight_cache_clear(void);
+
+moe_status moe_malloc(void** dptr, size_t bytes);
+moe_status moe_free(void* dptr);
+/* synchronous copies (hipMemcpy on the library stream, then wait) */
+moe_status moe_memcpy_h2d(void* dst, const void* src, size_t bytes);
+moe_status moe_memcpy_d2h(void* dst, const void* src, size_t bytes);
+moe_status moe_memcpy_d2d(void* dst, const void* src, size_t bytes);
+moe_status moe_memset(void* dptr, int value, size_t bytes);
+
+/* Events on the library stream, for timing (milliseconds). */
+moe_status moe_event_create(void** ev);
+moe_status moe_event_record(void* ev);
+moe_status moe_event_elapsed_ms(void* start, void* stop, float* ms);
+moe_status moe_event_destroy(void* ev);
+
+/* kernels.c:51-74 on device pointers: C[M x N] = Q8(A[M x K], Wq[N x K], s[N]) */
+moe_status moe_matmul_q8_dev(const float* A, const int8_t* Wq, const float* s, float* C,
+                             int M, int N, int K);
+/* kernels.c:96-128 on device pointers; Wq rows are K/2 bytes apart */
+moe_status moe_matmul_q4_dev(const float* A, const uint8_t* Wq, const float* s, float* C,
+                             int M, int N, int K);
+/* kernels.c:153-165 on device pointers: fp32, k ascending, unfused */
+moe_status moe_matmul_f32_dev(const float* A, const float* W, float* C, int M, int N, int K);
+/* kernels.c:149-181 with W_q->q / W_q->s (and W_fp32) device pointers;
+ * W_q itself is a host struct */
+moe_status moe_matmul_adaptive_dev(const float* A, const float* W_fp32,
+                                   const QuantizedWeight* W_q, float* C, int M, int N, int K);
+
+/* Many independent products of one shape in one launch (the expert-GEMV
+ * building block).  jobs_dev: device array of njobs moe_qjob; every W must be
+ * 16-byte aligned with rows packed (K bytes for Q8, K/2 for Q4). */
+typedef struct {
+  const void* W;
+  const float* S;
+  const float* A;
+  float* C;
+} moe_qjob;
+moe_status moe_matmul_q_batched_dev(int dtype, const moe_qjob* jobs_dev, int njobs,
+                                    int M, int N, int K);
+
+/* test_model_trace.c:229-236 and :500 on device arrays of n floats:
+ * h = (g / (1 + expf(-g))) * u  (u may be NULL: h = silu(g)).  expf is
+ * bit-identical to the host glibc expf, so h matches the reference exactly. */
+moe_status moe_silu_mul_dev(const float* g, const float* u, float* h, size_t n);
+/* y = expf(x), bit-identical to glibc expf (test_model_trace.c:233, :485). */
+moe_status moe_expf_dev(const float* x, float* y, size_t n);
+/* Verification hook: y[i] = expf(bits_as_float(start_bits + i)), so that all
+ * 2^32 inputs can be checked against the host libm without uploading them. */
+moe_status moe_expf_bits_dev(uint32_t start_bits, float* y, size_t n);
+
+/* Synthetic data: out[i] ~ N(mean, std^2), counter-based (seed, i) -> value. */
+moe_status moe_fill_normal_dev(float* out, size_t n, uint64_t seed, float mean, float stdv);
+/* export.py:23-36 rowwise quantization on device.  W fp32 [N x K];
+ * dtype 2: q int8 [N x K], s = max(amax,1e-8)/127, q = round-half-even(w/s);
+ * dtype 3: q uint8 [N x K/2], s = max(amax,1e-8)/7, q = clamp(rne(w/s),-8,7)+8,
+ *          low nibble = even column.  Bit-identical to the exporter's fp32 ops. */
+moe_status moe_quantize_rows_dev(int dtype, const float* W, long long N, int K, void* q, float* s);
+
+/* Name of the kernel variant the GEMV entry points use for a shape. */
+const char* moe_gemv_variant(int dtype, int M, int N, int K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOEHIP_H */

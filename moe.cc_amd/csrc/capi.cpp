@@ -1,0 +1,346 @@
+// capi.cpp - the C ABI of libmoehip.so (declared in include/moehip.h).
+//
+// Library state: one device, one stream (default priority), a cache of
+// weights uploaded by the drop-in matmul_adaptive, a thread-local last-error
+// message.  Every entry point is thread-compatible; the cache is guarded by a
+// mutex.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/moehip.h"
+#include "moe_internal.h"
+#include "moe_lib.h"
+
+namespace moe {
+
+namespace {
+thread_local std::string g_err;
+std::mutex g_mu;
+bool g_ready = false;
+int g_device = -1;
+hipStream_t g_stream = nullptr;
+
+struct CacheKey {
+  const void* host;
+  size_t bytes;
+  bool operator==(const CacheKey& o) const { return host == o.host && bytes == o.bytes; }
+};
+struct CacheKeyHash {
+  size_t operator()(const CacheKey& k) const {
+    return std::hash<const void*>()(k.host) ^ (std::hash<size_t>()(k.bytes) * 1315423911u);
+  }
+};
+std::unordered_map<CacheKey, void*, CacheKeyHash> g_cache;
+
+// staging buffers of the drop-in (grown on demand)
+void* g_stage_a = nullptr;
+size_t g_stage_a_bytes = 0;
+void* g_stage_c = nullptr;
+size_t g_stage_c_bytes = 0;
+}  // namespace
+
+moe_status set_error(moe_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return st;
+}
+
+moe_status check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MOE_OK;
+  return set_error(MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+moe_status ensure_init() {
+  if (g_ready) return MOE_OK;
+  return moe_init(0);
+}
+
+hipStream_t stream() { return g_stream; }
+
+namespace {
+
+moe_status grow(void** buf, size_t* cap, size_t need) {
+  if (need <= *cap) return MOE_OK;
+  if (*buf) (void)hipFree(*buf);
+  *buf = nullptr;
+  *cap = 0;
+  moe_status st = check_hip(hipMalloc(buf, need), "hipMalloc(staging)");
+  if (st == MOE_OK) *cap = need;
+  return st;
+}
+
+// Device copy of a host weight, uploaded once per (address, size).
+moe_status cached_upload(const void* host, size_t bytes, const void** dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  CacheKey key{host, bytes};
+  auto it = g_cache.find(key);
+  if (it != g_cache.end()) {
+    *dev = it->second;
+    return MOE_OK;
+  }
+  void* d = nullptr;
+  moe_status st = check_hip(hipMalloc(&d, bytes ? bytes : 1), "hipMalloc(weight)");
+  if (st) return st;
+  st = check_hip(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, g_stream), "upload weight");
+  if (st == MOE_OK) st = check_hip(hipStreamSynchronize(g_stream), "upload weight sync");
+  if (st) {
+    (void)hipFree(d);
+    return st;
+  }
+  g_cache[key] = d;
+  *dev = d;
+  return MOE_OK;
+}
+
+[[noreturn]] void die(const char* where) {
+  std::fprintf(stderr, "libmoehip: %s failed: %s\n", where, g_err.c_str());
+  std::fflush(stderr);
+  std::abort();
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+moe_status moe_init(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ready) {
+    if (device == g_device) return MOE_OK;
+    return set_error(MOE_ERR_UNSUPPORTED, "moe_init: already initialised on device %d", g_device);
+  }
+  int n = 0;
+  moe_status st = check_hip(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  if (st) return st;
+  if (device < 0 || device >= n)
+    return set_error(MOE_ERR_ARG, "moe_init: device %d not present (%d visible)", device, n);
+  st = check_hip(hipSetDevice(device), "hipSetDevice");
+  if (st) return st;
+  st = check_hip(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
+  if (st) return st;
+  g_device = device;
+  g_ready = true;
+  return MOE_OK;
+}
+
+const char* moe_last_error(void) { return g_err.c_str(); }
+const char* moe_version(void) { return "moehip 0.1 (gfx950)"; }
+
+void* moe_get_stream(void) {
+  if (ensure_init()) return nullptr;
+  return (void*)g_stream;
+}
+
+moe_status moe_synchronize(void) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  return check_hip(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
+moe_status moe_weight_cache_clear(void) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  st = check_hip(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& kv : g_cache) (void)hipFree(kv.second);
+  g_cache.clear();
+  return st;
+}
+
+moe_status moe_malloc(void** dptr, size_t bytes) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (!dptr) return set_error(MOE_ERR_ARG, "moe_malloc: null out pointer");
+  return check_hip(hipMalloc(dptr, bytes ? bytes : 1), "hipMalloc");
+}
+
+moe_status moe_free(void* dptr) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  return check_hip(hipFree(dptr), "hipFree");
+}
+
+static moe_status copy_sync(void* dst, const void* src, size_t bytes, hipMemcpyKind kind,
+                            const char* what) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  st = check_hip(hipMemcpyAsync(dst, src, bytes, kind, g_stream), what);
+  if (st) return st;
+  return check_hip(hipStreamSynchronize(g_stream), what);
+}
+
+moe_status moe_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyHostToDevice, "memcpy h2d");
+}
+moe_status moe_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToHost, "memcpy d2h");
+}
+moe_status moe_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToDevice, "memcpy d2d");
+}
+moe_status moe_memset(void* dptr, int value, size_t bytes) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  return check_hip(hipMemsetAsync(dptr, value, bytes, g_stream), "hipMemsetAsync");
+}
+
+moe_status moe_event_create(void** ev) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  return check_hip(hipEventCreate((hipEvent_t*)ev), "hipEventCreate");
+}
+moe_status moe_event_record(void* ev) {
+  return check_hip(hipEventRecord((hipEvent_t)ev, g_stream), "hipEventRecord");
+}
+moe_status moe_event_elapsed_ms(void* start, void* stop, float* ms) {
+  moe_status st = check_hip(hipEventSynchronize((hipEvent_t)stop), "hipEventSynchronize");
+  if (st) return st;
+  return check_hip(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop),
+                   "hipEventElapsedTime");
+}
+moe_status moe_event_destroy(void* ev) {
+  return check_hip(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+}
+
+static moe_status qgemv_dev(int dtype, const float* A, const void* Wq, const float* s, float* C,
+                            int M, int N, int K) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (M < 0 || N < 0) return set_error(MOE_ERR_ARG, "matmul: negative M or N");
+  if (K < 0) K = 0;  // the reference's loops run zero times: dot = 0
+  if (M == 0 || N == 0) return MOE_OK;
+  if (!A || !Wq || !s || !C) return set_error(MOE_ERR_ARG, "matmul: null pointer");
+  QShape sh;
+  sh.dtype = dtype;
+  sh.M = M;
+  sh.N = N;
+  sh.K = K;
+  sh.lda = K;
+  sh.ldc = N;
+  sh.rs = dtype == 3 ? K / 2 : K;
+  QJob one{(const uint8_t*)Wq, s, A, C};
+  return check_hip(launch_qgemv(sh, nullptr, one, 1, g_stream), "qgemv launch");
+}
+
+moe_status moe_matmul_q8_dev(const float* A, const int8_t* Wq, const float* s, float* C, int M,
+                             int N, int K) {
+  return qgemv_dev(2, A, Wq, s, C, M, N, K);
+}
+
+moe_status moe_matmul_q4_dev(const float* A, const uint8_t* Wq, const float* s, float* C, int M,
+                             int N, int K) {
+  return qgemv_dev(3, A, Wq, s, C, M, N, K);
+}
+
+moe_status moe_matmul_f32_dev(const float* A, const float* W, float* C, int M, int N, int K) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (M < 0 || N < 0) return set_error(MOE_ERR_ARG, "matmul_f32: negative M or N");
+  if (K < 0) K = 0;
+  if (M == 0 || N == 0) return MOE_OK;
+  if (!A || !W || !C) return set_error(MOE_ERR_ARG, "matmul_f32: null pointer");
+  return check_hip(launch_f32gemv(A, W, C, M, N, K, K, K, N, g_stream), "f32gemv launch");
+}
+
+moe_status moe_matmul_adaptive_dev(const float* A, const float* W_fp32, const QuantizedWeight* W_q,
+                                   float* C, int M, int N, int K) {
+  if (!W_q) return moe_matmul_f32_dev(A, W_fp32, C, M, N, K);
+  if (W_q->dtype == 2) return qgemv_dev(2, A, W_q->q, W_q->s, C, M, N, K);
+  if (W_q->dtype == 3) return qgemv_dev(3, A, W_q->q, W_q->s, C, M, N, K);
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (M <= 0 || N <= 0) return MOE_OK;
+  return check_hip(launch_zero(C, (size_t)M * (size_t)N, g_stream), "zero fill");
+}
+
+moe_status moe_matmul_q_batched_dev(int dtype, const moe_qjob* jobs_dev, int njobs, int M, int N,
+                                    int K) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (dtype != 2 && dtype != 3) return set_error(MOE_ERR_ARG, "batched: dtype %d", dtype);
+  if (M < 0 || N < 0 || K < 0 || njobs < 0) return set_error(MOE_ERR_ARG, "batched: bad shape");
+  if (dtype == 3 && (K & 1)) return set_error(MOE_ERR_ARG, "batched: Q4 needs even K");
+  const long long rb = dtype == 3 ? K / 2 : K;
+  if (rb % 16 != 0) return set_error(MOE_ERR_ARG, "batched: row bytes must be a multiple of 16");
+  if (njobs == 0 || M == 0 || N == 0) return MOE_OK;
+  QShape sh;
+  sh.dtype = dtype;
+  sh.M = M;
+  sh.N = N;
+  sh.K = K;
+  sh.lda = K;
+  sh.ldc = N;
+  sh.rs = rb;
+  static_assert(sizeof(moe_qjob) == sizeof(QJob), "job layout");
+  QJob none{nullptr, nullptr, nullptr, nullptr};
+  return check_hip(launch_qgemv(sh, (const QJob*)jobs_dev, none, njobs, g_stream),
+                   "batched qgemv launch");
+}
+
+const char* moe_gemv_variant(int dtype, int M, int N, int K) {
+  QShape sh;
+  sh.dtype = dtype;
+  sh.M = M;
+  sh.N = N;
+  sh.K = K;
+  sh.lda = K;
+  sh.ldc = N;
+  sh.rs = dtype == 3 ? K / 2 : K;
+  return qgemv_variant_name(sh, nullptr);
+}
+
+void matmul_adaptive(const float* A, const float* W_fp32, const void* W_q_ptr, float* C, int M,
+                     int N, int K) {
+  if (ensure_init()) die("matmul_adaptive init");
+  if (M <= 0 || N <= 0) return;
+  if (K < 0) K = 0;
+  const QuantizedWeight* wq = (const QuantizedWeight*)W_q_ptr;
+  const size_t a_bytes = (size_t)M * (size_t)K * sizeof(float);
+  const size_t c_bytes = (size_t)M * (size_t)N * sizeof(float);
+  if (grow(&g_stage_c, &g_stage_c_bytes, c_bytes)) die("matmul_adaptive staging");
+  float* dC = (float*)g_stage_c;
+  moe_status st = MOE_OK;
+  if (wq && wq->dtype != 2 && wq->dtype != 3) {
+    st = check_hip(launch_zero(dC, (size_t)M * (size_t)N, g_stream), "zero fill");
+  } else {
+    if (grow(&g_stage_a, &g_stage_a_bytes, a_bytes)) die("matmul_adaptive staging");
+    float* dA = (float*)g_stage_a;
+    if (a_bytes)
+      st = check_hip(hipMemcpyAsync(dA, A, a_bytes, hipMemcpyHostToDevice, g_stream), "upload A");
+    if (st) die("matmul_adaptive");
+    if (!wq) {
+      const void* dW = nullptr;
+      st = cached_upload(W_fp32, (size_t)N * (size_t)K * sizeof(float), &dW);
+      if (!st) st = moe_matmul_f32_dev(dA, (const float*)dW, dC, M, N, K);
+    } else {
+      // Q4 rows are K/2 bytes apart but a row reads ceil(K/2) bytes
+      // (kernels.c:103,108), so an odd K reads one byte past N*(K/2).
+      const size_t q_bytes = wq->dtype == 2 ? (size_t)N * (size_t)K
+                                            : (size_t)N * (size_t)(K / 2) + (size_t)(K & 1);
+      const void* dq = nullptr;
+      const void* ds = nullptr;
+      st = cached_upload(wq->q, q_bytes, &dq);
+      if (!st) st = cached_upload(wq->s, (size_t)N * sizeof(float), &ds);
+      if (!st) st = qgemv_dev(wq->dtype, dA, dq, (const float*)ds, dC, M, N, K);
+    }
+  }
+  if (st) die("matmul_adaptive");
+  st = check_hip(hipMemcpyAsync(C, dC, c_bytes, hipMemcpyDeviceToHost, g_stream), "download C");
+  if (!st) st = check_hip(hipStreamSynchronize(g_stream), "matmul_adaptive sync");
+  if (st) die("matmul_adaptive");
+}
+
+}  // extern "C"

@@ -1,0 +1,140 @@
+// moe_device.h - device-side arithmetic shared by the gfx950 kernels.
+//
+// Everything here exists to make GPU results bit-identical to moe.cc's CPU
+// path (kernels.c, test_model_trace.c) compiled by gcc -O2 for x86-64:
+//   * activation truncation with x86 cvttss2si semantics,
+//   * exact integer dot products through int8 "limbs" and v_dot4_i32_i8,
+//   * an expf that reproduces glibc 2.35's expf bit for bit,
+//   * fp32 glue evaluated with separate roundings (the library is compiled
+//     with -ffp-contract=off, so a*b+c is never fused).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kWave = 64;
+
+// (int32_t)v as gcc compiles it for x86-64 (cvttss2si): truncation toward
+// zero; NaN and values whose truncation leaves int32 give INT32_MIN.  The GPU
+// conversion instruction saturates instead, so the out-of-range case is
+// handled explicitly.  Used for kernels.c:66 and kernels.c:115-116.
+__device__ __forceinline__ int32_t f2i_trunc_x86(float v) {
+  return (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;
+}
+
+// Number of signed int8 limbs needed so that sum_l limb_l * 256^l == a:
+//   1 limb: [-128, 127]; 2 limbs: [-32896, 32639]; otherwise 4 limbs, which
+//   represent every int32 modulo 2^32 (all the dot product needs, since the
+//   reference accumulates in wrapping int32).
+__device__ __forceinline__ int limbs_needed(int32_t a) {
+  if (a >= -128 && a <= 127) return 1;
+  if (a >= -32896 && a <= 32639) return 2;
+  return 4;
+}
+
+// Splits a into 4 signed bytes (least significant first) with
+// a == b0 + 256 b1 + 65536 b2 + 2^24 b3 (mod 2^32).  Returned as the raw
+// byte values (0..255) ready to be packed into a dword.
+__device__ __forceinline__ void split_limbs(int32_t a, uint32_t b[4]) {
+  uint32_t r = (uint32_t)a;
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    int32_t lo = (int32_t)(int8_t)(r & 0xFFu);
+    b[l] = (uint32_t)lo & 0xFFu;
+    r = (uint32_t)((int32_t)(r - (uint32_t)lo) >> 8);
+  }
+}
+
+__device__ __forceinline__ uint32_t pack4(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Combines per-limb partial sums: sum_l acc[l] << 8l, modulo 2^32.
+template <int NL>
+__device__ __forceinline__ uint32_t combine_limbs(const int32_t* acc) {
+  uint32_t r = (uint32_t)acc[0];
+  if (NL > 1) r += (uint32_t)acc[1] << 8;
+  if (NL > 2) r += (uint32_t)acc[2] << 16;
+  if (NL > 3) r += (uint32_t)acc[3] << 24;
+  return r;
+}
+
+// Wrapping uint32 sum over the lanes of a group of W consecutive lanes
+// (W a power of two <= 64); every lane of the group receives the total.
+template <int W>
+__device__ __forceinline__ uint32_t group_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, W);
+  return v;
+}
+
+// kernels.c:71 / kernels.c:125 epilogue: ((float)dot / div) * scale, each
+// operation rounded on its own (IEEE division).
+__device__ __forceinline__ float qdot_epilogue(uint32_t dot, float div, float scale) {
+  float f = (float)(int32_t)dot;
+  f = f / div;
+  return f * scale;
+}
+
+// ---------------------------------------------------------------------------
+// expf, bit-identical to glibc 2.35 expf on x86-64 with FMA (the variant the
+// host's ifunc selects).  Method: the published ARM Optimized Routines expf
+// (also glibc's sysdeps/ieee754/flt-32/e_expf.c): x*32/ln2 = k + r, a 32-entry
+// table of 2^(i/32) and a cubic in r, evaluated in double, with the fused
+// multiply-adds a compiler contracts in that source under -mfma.  The table
+// entries are the nearest doubles to 2^(i/32), minus i << 47.  Equality with
+// the host expf on all 2^32 inputs is checked by tests/test_gpu_expf.py.
+// ---------------------------------------------------------------------------
+__constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float expf_glibc(float x) {
+  constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  constexpr double kShift = 0x1.8p+52;
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  const uint32_t ux = __float_as_uint(x);
+  const uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {                      // |x| >= 88 or x is NaN/inf
+    if (ux == 0xff800000u) return 0.0f;        // expf(-inf)
+    if (abstop >= 0x7f8u) return x + x;        // +inf or NaN
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+  }
+  const double xd = (double)x;
+  double kd = __builtin_fma(kInvLn2N, xd, kShift);
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd = kd - kShift;
+  const double r = __builtin_fma(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki % 32];
+  t += ki << 47;
+  const double s = __longlong_as_double((long long)t);
+  const double z = __builtin_fma(kC0, r, kC1);
+  const double r2 = r * r;
+  double y = __builtin_fma(kC2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// test_model_trace.c:233 then :500: h = (g / (1 + expf(-g))) * u
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float den = 1.0f + expf_glibc(-g);
+  const float sg = g / den;
+  return sg * u;
+}
+
+}  // namespace moe

@@ -1,0 +1,43 @@
+// moe_internal.h - host-side interfaces between the C ABI (capi.cpp) and the
+// kernel translation units.  Not installed; the public ABI is include/moehip.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moe {
+
+// One matrix-times-vectors product of the quantized path:
+//   C[m, n] = epilogue(sum_k trunc(A[m, k] * mult) * w[n, k])
+// W rows are `rs` bytes apart (int8 values for Q8, nibble pairs for Q4).
+struct QJob {
+  const uint8_t* W;
+  const float* S;
+  const float* A;
+  float* C;
+};
+
+struct QShape {
+  int dtype;        // 2 = Q8, 3 = Q4 (the reference's TensorBin dtypes)
+  int M, N, K;      // tokens, output rows, logical input length
+  int lda, ldc;     // row strides (elements) of A and C
+  long long rs;     // weight row stride in bytes
+};
+
+// Launches C = A * W^T for `njobs` jobs of one shape.  `jobs_dev` is a device
+// array of jobs, or nullptr to use `one` (a single job passed by value).
+hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                        hipStream_t stream);
+
+// fp32 path of matmul_adaptive (kernels.c:153-165): sequential k, one
+// rounding per multiply and per add.  W row-major [N][ldw].
+hipError_t launch_f32gemv(const float* A, const float* W, float* C, int M, int N, int K,
+                          int lda, int ldw, int ldc, hipStream_t stream);
+
+// Zero-fill used for unsupported dtypes (kernels.c:172-179).
+hipError_t launch_zero(float* C, size_t n, hipStream_t stream);
+
+// Which kernel variant launch_qgemv picks for a shape (for tests/profiles).
+const char* qgemv_variant_name(const QShape& sh, const void* w_base);
+
+}  // namespace moe

@@ -1,0 +1,73 @@
+// pointwise.hip - elementwise ops of the MoE path on device pointers:
+//   h = silu(g) * u     (test_model_trace.c:229-236 then :500)
+//   y = expf(x)         (glibc-exact, moe_device.h)
+#include "moe_device.h"
+#include "moe_internal.h"
+#include "moe_lib.h"
+
+namespace moe {
+namespace {
+
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                float* __restrict__ h, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float gv = g[i];
+    const float den = 1.0f + expf_glibc(-gv);
+    const float sg = gv / den;
+    h[i] = u ? sg * u[i] : sg;
+  }
+}
+
+__global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    y[i] = expf_glibc(x[i]);
+}
+
+__global__ void expf_bits_kernel(uint32_t start, float* __restrict__ y, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    y[i] = expf_glibc(__uint_as_float(start + (uint32_t)i));
+}
+
+unsigned grid_for(size_t n) {
+  size_t b = (n + 255) / 256;
+  return (unsigned)(b < 65536 ? (b ? b : 1) : 65536);
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+moe_status moe_silu_mul_dev(const float* g, const float* u, float* h, size_t n) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (n == 0) return MOE_OK;
+  if (!g || !h) return set_error(MOE_ERR_ARG, "silu_mul: null pointer");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(256), 0, stream(), g, u, h, n);
+  return check_hip(hipGetLastError(), "silu_mul launch");
+}
+
+moe_status moe_expf_dev(const float* x, float* y, size_t n) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (n == 0) return MOE_OK;
+  if (!x || !y) return set_error(MOE_ERR_ARG, "expf: null pointer");
+  hipLaunchKernelGGL(expf_kernel, dim3(grid_for(n)), dim3(256), 0, stream(), x, y, n);
+  return check_hip(hipGetLastError(), "expf launch");
+}
+
+moe_status moe_expf_bits_dev(uint32_t start_bits, float* y, size_t n) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (n == 0) return MOE_OK;
+  if (!y) return set_error(MOE_ERR_ARG, "expf_bits: null pointer");
+  hipLaunchKernelGGL(expf_bits_kernel, dim3(grid_for(n)), dim3(256), 0, stream(), start_bits, y, n);
+  return check_hip(hipGetLastError(), "expf_bits launch");
+}
+
+}  // extern "C"

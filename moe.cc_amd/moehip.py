@@ -1,0 +1,212 @@
+"""moehip - Python host binding of libmoehip.so (ctypes; no torch).
+
+Mirrors the reference's call surface for the quantized expert path:
+``matmul_adaptive`` (kernels.h:16-17) with its host-pointer semantics, the
+device-pointer GEMVs, and the MoE block of one layer
+(test_model_trace.c:460-517).  Arrays are numpy; device memory is held by
+:class:`DeviceBuffer`.  There is no CPU fallback: if the library is missing or
+the GPU runtime fails, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoehip.so")
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class MoeError(RuntimeError):
+    pass
+
+
+class QuantizedWeight(ctypes.Structure):
+    """model.h:26-31 layout: {q, s, rows, cols, dtype}."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("s", ctypes.c_void_p),
+        ("rows", ctypes.c_int),
+        ("cols", ctypes.c_int),
+        ("dtype", ctypes.c_int),
+    ]
+
+
+class QJob(ctypes.Structure):
+    _fields_ = [
+        ("W", ctypes.c_void_p),
+        ("S", ctypes.c_void_p),
+        ("A", ctypes.c_void_p),
+        ("C", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "matmul_adaptive": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "moe_init": (_I, [_I]),
+    "moe_last_error": (ctypes.c_char_p, []),
+    "moe_version": (ctypes.c_char_p, []),
+    "moe_get_stream": (_P, []),
+    "moe_synchronize": (_I, []),
+    "moe_weight_cache_clear": (_I, []),
+    "moe_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "moe_free": (_I, [_P]),
+    "moe_memcpy_h2d": (_I, [_P, _P, _SZ]),
+    "moe_memcpy_d2h": (_I, [_P, _P, _SZ]),
+    "moe_memcpy_d2d": (_I, [_P, _P, _SZ]),
+    "moe_memset": (_I, [_P, _I, _SZ]),
+    "moe_event_create": (_I, [ctypes.POINTER(_P)]),
+    "moe_event_record": (_I, [_P]),
+    "moe_event_elapsed_ms": (_I, [_P, _P, ctypes.POINTER(ctypes.c_float)]),
+    "moe_event_destroy": (_I, [_P]),
+    "moe_matmul_q8_dev": (_I, [_P, _P, _P, _P, _I, _I, _I]),
+    "moe_matmul_q4_dev": (_I, [_P, _P, _P, _P, _I, _I, _I]),
+    "moe_matmul_f32_dev": (_I, [_P, _P, _P, _I, _I, _I]),
+    "moe_matmul_adaptive_dev": (_I, [_P, _P, ctypes.POINTER(QuantizedWeight), _P, _I, _I, _I]),
+    "moe_matmul_q_batched_dev": (_I, [_I, _P, _I, _I, _I, _I]),
+    "moe_gemv_variant": (ctypes.c_char_p, [_I, _I, _I, _I]),
+    "moe_silu_mul_dev": (_I, [_P, _P, _P, _SZ]),
+    "moe_expf_dev": (_I, [_P, _P, _SZ]),
+    "moe_expf_bits_dev": (_I, [ctypes.c_uint32, _P, _SZ]),
+    "moe_fill_normal_dev": (_I, [_P, _SZ, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+    "moe_quantize_rows_dev": (_I, [_I, _P, ctypes.c_longlong, _I, _P, _P]),
+}
+
+
+def exported_symbols():
+    """Names the C ABI (include/moehip.h) exports."""
+    return list(_SIGS)
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libmoehip.so (built in-tree by ``make -C moe.cc_amd``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MoeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        msg = lib().moe_last_error().decode(errors="replace")
+        raise MoeError(f"{what}: status {status}: {msg}")
+
+
+def init(device: int = 0) -> None:
+    check(lib().moe_init(device), "moe_init")
+
+
+def synchronize() -> None:
+    check(lib().moe_synchronize(), "moe_synchronize")
+
+
+class DeviceBuffer:
+    """Owned device allocation of `nbytes` bytes."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _P()
+        check(lib().moe_malloc(ctypes.byref(p), max(self.nbytes, 1)), "moe_malloc")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise MoeError("upload past the end of the buffer")
+        check(lib().moe_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes), "h2d")
+
+    def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise MoeError("download past the end of the buffer")
+        check(lib().moe_memcpy_d2h(out.ctypes.data, self.ptr + offset, out.nbytes), "d2h")
+        return out
+
+    def zero(self) -> None:
+        check(lib().moe_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib().moe_free(self.ptr), "moe_free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.moe_free(self.ptr)
+        except Exception:
+            pass
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def matmul_adaptive(A: np.ndarray, W_fp32: Optional[np.ndarray], W_q: Optional[dict],
+                    N: int, K: int) -> np.ndarray:
+    """The drop-in entry point on host arrays (kernels.c:149-181).
+
+    ``W_q`` is None for the fp32 path, else a dict with ``q`` (int8 / uint8
+    array), ``s`` (fp32 [N]) and ``dtype`` (2 = Q8, 3 = Q4).  Returns C [M, N].
+    The host arrays must stay alive while the library caches their upload.
+    """
+    A = _f32(A)
+    M = A.shape[0] if A.ndim == 2 else 1
+    C = np.empty((M, N), dtype=np.float32)
+    if W_q is None:
+        Wf = _f32(W_fp32)
+        lib().matmul_adaptive(A.ctypes.data, Wf.ctypes.data, None, C.ctypes.data, M, N, K)
+    else:
+        qw = QuantizedWeight(W_q["q"].ctypes.data, W_q["s"].ctypes.data, N,
+                             K, int(W_q["dtype"]))
+        lib().matmul_adaptive(A.ctypes.data, None, ctypes.addressof(qw), C.ctypes.data, M, N, K)
+    return C
+
+
+def gemv_variant(dtype: int, M: int, N: int, K: int) -> str:
+    return lib().moe_gemv_variant(dtype, M, N, K).decode()
+
+
+class Event:
+    def __init__(self):
+        p = _P()
+        check(lib().moe_event_create(ctypes.byref(p)), "event_create")
+        self.ptr = p.value
+
+    def record(self) -> None:
+        check(lib().moe_event_record(self.ptr), "event_record")
+
+    def elapsed_ms(self, stop: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().moe_event_elapsed_ms(self.ptr, stop.ptr, ctypes.byref(ms)), "elapsed")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.moe_event_destroy(self.ptr)
+        except Exception:
+            pass

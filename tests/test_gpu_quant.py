@@ -1,0 +1,25 @@
+"""Device rowwise quantizer (export.py:23-36) equals the oracle's restatement
+bit for bit (scales and packed bytes)."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype,N,K", [(2, 768, 2048), (3, 2048, 768), (2, 5, 33), (3, 7, 10)])
+def test_quantize_rows(moehip, dtype, N, K):
+    W = O.normal(N * K, 31 * N + K, 0.0, 0.02).reshape(N, K)
+    W[0, :] = 0.0  # zero row: scale clamps at 1e-8
+    if N > 2:
+        W[1, 3] = 1e-3  # a single large entry
+    q_want, s_want = (O.quant_q8 if dtype == 2 else O.quant_q4)(W)
+    dW = moehip.DeviceBuffer.from_array(W)
+    dq = moehip.DeviceBuffer(q_want.nbytes)
+    ds = moehip.DeviceBuffer(s_want.nbytes)
+    moehip.check(moehip.lib().moe_quantize_rows_dev(dtype, dW.ptr, N, K, dq.ptr, ds.ptr), "quantize")
+    q = dq.download(q_want.shape, q_want.dtype)
+    s = ds.download(s_want.shape, np.float32)
+    np.testing.assert_array_equal(s.view(np.uint32), s_want.view(np.uint32))
+    np.testing.assert_array_equal(q, q_want)
