@@ -87,10 +87,12 @@ typedef struct {
  *   other dtype     : C is zero-filled (kernels.c:172-179)
  * A [M x K], W [N x K] (Q4: N x K/2 bytes, rows K/2 bytes apart), C [M x N],
  * all host memory.  Results are bit-identical to the reference.  Weights are
- * uploaded on first use and cached by host address (the reference never
- * mutates them; call moe_weight_cache_clear() after changing a weight in
- * place).  Errors from the GPU runtime abort the process with a message:
- * there is no CPU fallback. */
+ * uploaded on first use and cached by (host address, size); by default each
+ * call re-hashes the host bytes and re-uploads them if they changed, so freed
+ * and reused host memory is safe.  moe_weight_cache_mode(1) skips the hash
+ * for callers whose weights never change (the reference's loader).  Errors
+ * from the GPU runtime abort the process with a message: there is no CPU
+ * fallback. */
 void matmul_adaptive(const float* A, const float* W_fp32, const void* W_q_ptr,
                      float* C, int M, int N, int K);
 
@@ -115,6 +117,9 @@ void* moe_get_stream(void);
 moe_status moe_synchronize(void);
 /* drops every cached upload made by matmul_adaptive */
 moe_status moe_weight_cache_clear(void);
+/* 0 (default): verify cached weights by content on every call;
+ * 1: trust that a host address keeps its bytes (no hashing) */
+moe_status moe_weight_cache_mode(int trust_addresses);
 
 moe_status moe_malloc(void** dptr, size_t bytes);
 moe_status moe_free(void* dptr);

@@ -37,7 +37,14 @@ struct CacheKeyHash {
     return std::hash<const void*>()(k.host) ^ (std::hash<size_t>()(k.bytes) * 1315423911u);
   }
 };
-std::unordered_map<CacheKey, void*, CacheKeyHash> g_cache;
+struct CacheEntry {
+  void* dev;
+  uint64_t digest;
+};
+std::unordered_map<CacheKey, CacheEntry, CacheKeyHash> g_cache;
+// 0: re-hash the host bytes on every call and re-upload when they changed
+//    (safe when callers free and reuse host memory); 1: trust the address.
+int g_trust_addresses = 0;
 
 // staging buffers of the drop-in (grown on demand)
 void* g_stage_a = nullptr;
@@ -80,25 +87,54 @@ moe_status grow(void** buf, size_t* cap, size_t need) {
   return st;
 }
 
-// Device copy of a host weight, uploaded once per (address, size).
+// 64-bit digest of a host buffer: four interleaved multiply-xorshift lanes
+// over 8-byte words, tail bytes folded in one at a time.
+uint64_t digest(const void* p, size_t n) {
+  const unsigned char* b = (const unsigned char*)p;
+  uint64_t h[4] = {0x9E3779B97F4A7C15ull, 0xC2B2AE3D27D4EB4Full, 0x165667B19E3779F9ull,
+                   0x27D4EB2F165667C5ull};
+  size_t i = 0;
+  for (; i + 32 <= n; i += 32) {
+    for (int l = 0; l < 4; ++l) {
+      uint64_t w;
+      std::memcpy(&w, b + i + 8 * l, 8);
+      h[l] = (h[l] ^ w) * 0xFF51AFD7ED558CCDull;
+      h[l] ^= h[l] >> 29;
+    }
+  }
+  uint64_t r = h[0] ^ (h[1] * 31) ^ (h[2] * 131) ^ (h[3] * 1313) ^ (uint64_t)n;
+  for (; i < n; ++i) r = (r ^ b[i]) * 0x100000001B3ull;
+  r ^= r >> 33;
+  return r * 0xC4CEB9FE1A85EC53ull;
+}
+
+// Device copy of a host weight, uploaded once per (address, size) and
+// re-uploaded when its bytes change (unless addresses are trusted).
 moe_status cached_upload(const void* host, size_t bytes, const void** dev) {
   std::lock_guard<std::mutex> lk(g_mu);
   CacheKey key{host, bytes};
+  const uint64_t dg = g_trust_addresses ? 0 : digest(host, bytes);
   auto it = g_cache.find(key);
-  if (it != g_cache.end()) {
-    *dev = it->second;
+  if (it != g_cache.end() && (g_trust_addresses || it->second.digest == dg)) {
+    *dev = it->second.dev;
     return MOE_OK;
   }
   void* d = nullptr;
-  moe_status st = check_hip(hipMalloc(&d, bytes ? bytes : 1), "hipMalloc(weight)");
-  if (st) return st;
+  moe_status st = MOE_OK;
+  if (it != g_cache.end()) {
+    d = it->second.dev;  // same size: refill in place
+  } else {
+    st = check_hip(hipMalloc(&d, bytes ? bytes : 1), "hipMalloc(weight)");
+    if (st) return st;
+  }
   st = check_hip(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, g_stream), "upload weight");
   if (st == MOE_OK) st = check_hip(hipStreamSynchronize(g_stream), "upload weight sync");
   if (st) {
+    if (it != g_cache.end()) g_cache.erase(it);
     (void)hipFree(d);
     return st;
   }
-  g_cache[key] = d;
+  g_cache[key] = CacheEntry{d, dg};
   *dev = d;
   return MOE_OK;
 }
@@ -155,9 +191,15 @@ moe_status moe_weight_cache_clear(void) {
   if (st) return st;
   st = check_hip(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
   std::lock_guard<std::mutex> lk(g_mu);
-  for (auto& kv : g_cache) (void)hipFree(kv.second);
+  for (auto& kv : g_cache) (void)hipFree(kv.second.dev);
   g_cache.clear();
   return st;
+}
+
+moe_status moe_weight_cache_mode(int trust_addresses) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_trust_addresses = trust_addresses ? 1 : 0;
+  return MOE_OK;
 }
 
 moe_status moe_malloc(void** dptr, size_t bytes) {

@@ -5,262 +5,206 @@
 //   dot  = sum_k a_k * w[n,k]               wrapping int32, any order (exact)
 //   C    = ((float)dot / 127.0f) * s[n]     (7.0f for Q4)
 //
-// Design (decode is HBM-bound; one weight byte feeds one multiply-add):
-//   * The truncated activations of the block's tokens are built once per
-//     block in LDS as packed signed-int8 "limbs" (a = sum_l b_l 256^l), so the
-//     integer dot runs on v_dot4_i32_i8: 1, 2 or 4 dot4 per weight dword
-//     depending on the activation range (chosen per block at run time).
-//   * Q4 weights are used as unsigned nibbles u = q + 8 in [0, 15]:
-//     sum a*(u-8) = sum a*u - 8*sum a; the even/odd nibbles of a dword are
-//     split with two masks and meet activations pre-split into even and odd
-//     columns.
-//   * A lane owns C consecutive dwords of a row per pass (dwordx4 or dwordx3
-//     global loads, coalesced across the LPR lanes that share a row), a wave
-//     keeps UR rows of loads in flight, and a row's partial sums are reduced
-//     across its lanes with cross-lane shuffles.
-//   * Shapes whose row bytes are not one of the tiled sizes, unaligned rows
-//     and odd-K Q4 go to a plain one-wave-per-row kernel with the same
-//     arithmetic.
+// Two launches per call:
+//   1. act_pack: every activation row -> packed limb table (moe_qtile.h),
+//      once, into a workspace;
+//   2. qgemv_tiled: each block owns a chunk of rows of one job; its waves
+//      load their slice of the activation table into registers once, then
+//      stream rows with double-buffered dwordx4 loads (LPR lanes per row, a
+//      row = LPR*P*16 bytes), dot on v_dot4_i32_i8 and reduce across the
+//      row's lanes with DPP.  No LDS, no block barriers in the main loop.
+// Shapes without a tiled geometry (row bytes not LPR*P*16, unaligned rows,
+// odd-K Q4) and Q4 activations that need 4 limbs use a one-wave-per-row
+// kernel with plain int32 arithmetic on the fp32 activations.
 #include "moe_device.h"
 #include "moe_internal.h"
+#include "moe_qtile.h"
 
 namespace moe {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / kWave;
+constexpr int kBlock = kTileBlock;
+constexpr int kWaves = kTileWaves;
 
-template <int C>
-__device__ __forceinline__ void load_chunk(const uint8_t* p, uint32_t* out) {
-  if constexpr (C == 4) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
-    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
-  } else {
-    static_assert(C == 3, "chunk of 3 or 4 dwords");
-    const uint3 v = *reinterpret_cast<const uint3*>(p);
-    out[0] = v.x; out[1] = v.y; out[2] = v.z;
-  }
+struct TiledArgs {
+  QShape sh;
+  const QJob* jobs;     // device array, or nullptr -> `one`
+  QJob one;
+  const uint8_t* tabs;  // packed activations, [job][m] tables of tab_bytes
+  size_t tab_bytes;
+  int blocks_per_job;
+  int rows_per_block;
+};
+
+__device__ __forceinline__ QJob get_job(const TiledArgs& a, int j) {
+  return a.jobs ? a.jobs[j] : a.one;
 }
 
-// Builds the limb tables for tokens m0..m0+MT-1 in LDS and returns the number
-// of limbs (1, 2 or 4) the block needs.  KD = weight dwords per row.
-//   Q8: act[(m*4 + l)*KD + d] packs limb l of a[4d .. 4d+3]
-//   Q4: act[(m*4 + l)*KD + d]        packs limb l of a[8d], a[8d+2], a[8d+4], a[8d+6]
-//       act[(m*4 + l)*KD + KD/2 + d] packs limb l of a[8d+1], ..., a[8d+7]
-//       (here KD counts both halves: KD = 2 * weight dwords per row)
-//   asum[m] = sum_k a_k (wrapping), used by the Q4 offset correction.
-template <bool Q4, int MT>
-__device__ int build_act_lds(const float* __restrict__ A, int lda, int M, int m0, int K, int KD,
-                             uint32_t* act, uint32_t* asum) {
-  const float mult = Q4 ? 7.0f : 127.0f;
-  const int tid = threadIdx.x;
-  int need2 = 0, need4 = 0;
-  if (tid < MT) asum[tid] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const bool valid = (m0 + m) < M;
-    const float* a = A + (size_t)(valid ? (m0 + m) : 0) * lda;
-    uint32_t* base = act + (size_t)m * 4 * KD;
-    if constexpr (!Q4) {
-      for (int d = tid; d < KD; d += kBlock) {
-        uint32_t b[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int k = 4 * d + i;
-          const int32_t v = (valid && k < K) ? f2i_trunc_x86(a[k] * mult) : 0;
-          const int nl = limbs_needed(v);
-          need2 |= nl >= 2;
-          need4 |= nl >= 4;
-          split_limbs(v, b[i]);
-        }
-#pragma unroll
-        for (int l = 0; l < 4; ++l) base[l * KD + d] = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
-      }
-    } else {
-      const int KH = KD / 2;
-      uint32_t part = 0;
-      for (int d = tid; d < KH; d += kBlock) {
-        uint32_t b[8][4];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int k = 8 * d + i;
-          const int32_t v = (valid && k < K) ? f2i_trunc_x86(a[k] * mult) : 0;
-          const int nl = limbs_needed(v);
-          need2 |= nl >= 2;
-          need4 |= nl >= 4;
-          part += (uint32_t)v;
-          split_limbs(v, b[i]);
-        }
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-          base[l * KD + d] = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
-          base[l * KD + KH + d] = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
-        }
-      }
-      atomicAdd(&asum[m], part);
-    }
-  }
-  const int any4 = __syncthreads_or(need4);
-  const int any2 = __syncthreads_or(need2);
-  return any4 ? 4 : (any2 ? 2 : 1);
+template <bool Q4>
+__global__ __launch_bounds__(kBlock) void act_pack_kernel(QShape sh, const QJob* __restrict__ jobs,
+                                                          QJob one, uint8_t* __restrict__ tabs,
+                                                          size_t tab_bytes) {
+  __shared__ int scratch[2];
+  const int j = blockIdx.x, m = blockIdx.y;
+  const QJob job = jobs ? jobs[j] : one;
+  pack_act_row<Q4>(job.A + (size_t)m * sh.lda, sh.K, tabs + ((size_t)j * sh.M + m) * tab_bytes,
+                   scratch);
 }
 
-// Tiled body.  Geometry: LPR lanes share a row; a lane loads P chunks of C
-// dwords at dword offsets (p*LPR + r)*C of the row; WR = 64/LPR rows per wave
-// at once; UR such row groups per wave; the block covers
-// kWaves*UR*WR consecutive rows.
-template <bool Q4, int C, int P, int LPR, int UR, int MT, int NL>
-__device__ __forceinline__ void qgemv_body(const QJob& job, const QShape& sh, int row0, int m0,
-                                           const uint32_t* act, const uint32_t* asum, int KD) {
-  constexpr int WR = kWave / LPR;
-  constexpr int DW = P * C;
+// Plain exact path for the rows [r0, r1) of one job and tokens [m0, m1):
+// one wave per row, int32 multiply-add on the fly.
+template <bool Q4>
+__device__ void generic_rows(const QShape& sh, const QJob& job, int r0, int r1, int m0, int m1) {
   const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  const int g = lane / LPR, r = lane % LPR;
-
-  uint32_t w[UR][DW];
-  int rows[UR];
-#pragma unroll
-  for (int u = 0; u < UR; ++u) {
-    rows[u] = row0 + (wave * UR + u) * WR + g;
-    if (rows[u] < sh.N) {
-      const uint8_t* wr = job.W + (size_t)rows[u] * (size_t)sh.rs;
-#pragma unroll
-      for (int p = 0; p < P; ++p) load_chunk<C>(wr + (size_t)((p * LPR + r) * C) * 4, &w[u][p * C]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < DW; ++i) w[u][i] = 0;
+  for (int row = r0 + (int)(threadIdx.x / kWave); row < r1; row += blockDim.x / kWave) {
+    const uint8_t* wr = job.W + (size_t)row * (size_t)sh.rs;
+    const float sc = job.S[row];
+    for (int m = m0; m < m1; ++m) {
+      const float* a = job.A + (size_t)m * sh.lda;
+      uint32_t acc = 0;
+      if constexpr (!Q4) {
+        for (int k = lane; k < sh.K; k += kWave) {
+          const int32_t ai = f2i_trunc_x86(a[k] * 127.0f);
+          acc += (uint32_t)ai * (uint32_t)(int32_t)(int8_t)wr[k];
+        }
+      } else {
+        for (int j = lane; 2 * j < sh.K; j += kWave) {
+          const uint32_t byte = wr[j];
+          const int k = 2 * j;
+          const int32_t lo = (int32_t)(byte & 0x0Fu) - 8;
+          const int32_t hi = (int32_t)((byte >> 4) & 0x0Fu) - 8;
+          acc += (uint32_t)f2i_trunc_x86(a[k] * 7.0f) * (uint32_t)lo;
+          if (k + 1 < sh.K) acc += (uint32_t)f2i_trunc_x86(a[k + 1] * 7.0f) * (uint32_t)hi;
+        }
+      }
+      acc = group_sum_dpp<kWave>(acc);
+      if (lane == 0) job.C[(size_t)m * sh.ldc + row] = qdot_epilogue(acc, Q4 ? 7.0f : 127.0f, sc);
     }
   }
+}
 
-  uint32_t dot[UR][MT];
+// Rows [r0, r1) of one job against MTI token tables starting at token m0.
+// Each wave walks row groups gi = wave, wave + 4, ...; the loads of the next
+// group are issued before the current one is reduced.
+template <bool Q4, class G, int NL, int MTI>
+__device__ __forceinline__ void tiled_rows(const QShape& sh, const QJob& job,
+                                           const uint8_t* const* tab, int r0, int r1, int m0) {
+  ActRegs<Q4, G, NL> ar[MTI];
+  uint32_t asum[MTI];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const uint32_t* am = act + (size_t)m * 4 * KD;
-    if constexpr (!Q4) {
-      uint32_t av[NL][DW];
-#pragma unroll
-      for (int l = 0; l < NL; ++l)
-#pragma unroll
-        for (int p = 0; p < P; ++p)
-#pragma unroll
-          for (int c = 0; c < C; ++c) av[l][p * C + c] = am[l * KD + (p * LPR + r) * C + c];
-#pragma unroll
-      for (int u = 0; u < UR; ++u) {
-        int32_t acc[NL];
-#pragma unroll
-        for (int l = 0; l < NL; ++l) {
-          acc[l] = 0;
-#pragma unroll
-          for (int i = 0; i < DW; ++i) acc[l] = dot4(w[u][i], av[l][i], acc[l]);
-        }
-        dot[u][m] = combine_limbs<NL>(acc);
-      }
-    } else {
-      const int KH = KD / 2;
-      uint32_t ev[NL][DW], ov[NL][DW];
-#pragma unroll
-      for (int l = 0; l < NL; ++l)
-#pragma unroll
-        for (int p = 0; p < P; ++p)
-#pragma unroll
-          for (int c = 0; c < C; ++c) {
-            const int d = (p * LPR + r) * C + c;
-            ev[l][p * C + c] = am[l * KD + d];
-            ov[l][p * C + c] = am[l * KD + KH + d];
-          }
-#pragma unroll
-      for (int u = 0; u < UR; ++u) {
-        int32_t acc[NL];
-#pragma unroll
-        for (int l = 0; l < NL; ++l) acc[l] = 0;
-#pragma unroll
-        for (int i = 0; i < DW; ++i) {
-          const uint32_t lo = w[u][i] & 0x0F0F0F0Fu;
-          const uint32_t hi = (w[u][i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-          for (int l = 0; l < NL; ++l) {
-            acc[l] = dot4(lo, ev[l][i], acc[l]);
-            acc[l] = dot4(hi, ov[l][i], acc[l]);
-          }
-        }
-        dot[u][m] = combine_limbs<NL>(acc);
-      }
-    }
+  for (int t = 0; t < MTI; ++t) {
+    load_act_regs<Q4, G, NL>(tab[t], sh.K, ar[t]);
+    asum[t] = Q4 ? act_asum(tab[t]) : 0u;
   }
-
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / G::LPR, r = lane % G::LPR;
+  const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
   const float div = Q4 ? 7.0f : 127.0f;
+
+  auto row_of = [&](int gi) { return r0 + gi * G::WR + g; };
+  auto load = [&](int gi, uint32_t (&w)[G::DW]) {
+    const int row = row_of(gi);
+    if (row < r1) {
+      load_row_regs<G>(job.W + (size_t)row * (size_t)sh.rs, w);
+    } else {
 #pragma unroll
-  for (int u = 0; u < UR; ++u) {
-    float sc = 0.0f;
-    if (r == 0 && rows[u] < sh.N) sc = job.S[rows[u]];
+      for (int i = 0; i < G::DW; ++i) w[i] = 0;
+    }
+  };
+  auto finish = [&](int gi, const uint32_t (&w)[G::DW]) {
+    const int row = row_of(gi);
+    uint32_t tot[MTI];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      uint32_t v = group_sum_u32<LPR>(dot[u][m]);
-      if (Q4) v -= 8u * asum[m];
-      if (r == 0 && rows[u] < sh.N && (m0 + m) < sh.M)
-        job.C[(size_t)(m0 + m) * sh.ldc + rows[u]] = qdot_epilogue(v, div, sc);
+    for (int t = 0; t < MTI; ++t) tot[t] = group_sum_dpp<G::LPR>(lane_dot<Q4, G, NL>(w, ar[t]));
+    if (r == 0 && row < r1) {
+      const float sc = job.S[row];
+#pragma unroll
+      for (int t = 0; t < MTI; ++t) {
+        const int m = m0 + t;
+        if (m < sh.M) {
+          const uint32_t v = Q4 ? tot[t] - 8u * asum[t] : tot[t];
+          job.C[(size_t)m * sh.ldc + row] = qdot_epilogue(v, div, sc);
+        }
+      }
+    }
+  };
+
+  uint32_t wa[G::DW], wb[G::DW];
+  int gi = wave;
+  if (gi < ngroups) load(gi, wa);
+  while (gi < ngroups) {
+    int gn = gi + kWaves;
+    if (gn < ngroups) load(gn, wb);
+    finish(gi, wa);
+    gi = gn;
+    if (gi >= ngroups) break;
+    gn = gi + kWaves;
+    if (gn < ngroups) load(gn, wa);
+    finish(gi, wb);
+    gi = gn;
+  }
+}
+
+// Token slots per weight pass so that activation registers stay <= ~96.
+template <bool Q4, class G, int NL>
+constexpr int mti_for() {
+  constexpr int per = NL * G::DW * (Q4 ? 2 : 1);
+  constexpr int n = 96 / per;
+  return n >= 4 ? 4 : (n >= 2 ? 2 : (n >= 1 ? 1 : 0));
+}
+
+template <bool Q4, class G, int NL, int MT>
+__device__ __forceinline__ void tiled_tokens(const TiledArgs& a, const QJob& job, int job_id, int r0,
+                                             int r1, int mbase) {
+  constexpr int MTI0 = mti_for<Q4, G, NL>();
+  if constexpr (MTI0 == 0) {
+    generic_rows<Q4>(a.sh, job, r0, r1, mbase, mbase + MT < a.sh.M ? mbase + MT : a.sh.M);
+  } else {
+    constexpr int MTI = MTI0 < MT ? MTI0 : MT;
+#pragma unroll
+    for (int m0 = 0; m0 < MT; m0 += MTI) {
+      if (mbase + m0 >= a.sh.M) break;
+      const uint8_t* tab[MTI];
+#pragma unroll
+      for (int t = 0; t < MTI; ++t) {
+        const int m = mbase + m0 + t < a.sh.M ? mbase + m0 + t : a.sh.M - 1;
+        tab[t] = a.tabs + ((size_t)job_id * a.sh.M + m) * a.tab_bytes;
+      }
+      tiled_rows<Q4, G, NL, MTI>(a.sh, job, tab, r0, r1, mbase + m0);
     }
   }
 }
 
-template <bool Q4, int C, int P, int LPR, int UR, int MT>
-__global__ __launch_bounds__(kBlock) void qgemv_tiled(QShape sh, const QJob* __restrict__ jobs,
-                                                      QJob one, int blocks_per_job) {
-  extern __shared__ uint32_t smem[];
-  constexpr int WR = kWave / LPR;
-  constexpr int RB = kWaves * UR * WR;
-  const int job_id = blockIdx.x / blocks_per_job;
-  const int row0 = (blockIdx.x % blocks_per_job) * RB;
-  const QJob job = jobs ? jobs[job_id] : one;
-  const int m0 = blockIdx.y * MT;
-  const int KD = (LPR * C * P) * (Q4 ? 2 : 1);  // LDS dwords per (token, limb)
-  uint32_t* act = smem;
-  uint32_t* asum = smem + (size_t)MT * 4 * KD;
-  const int nl = build_act_lds<Q4, MT>(job.A, sh.lda, sh.M, m0, sh.K, KD, act, asum);
+template <bool Q4, class G, int MT>
+__global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
+  const int job_id = blockIdx.x / a.blocks_per_job;
+  const int r0 = (blockIdx.x % a.blocks_per_job) * a.rows_per_block;
+  const int r1 = r0 + a.rows_per_block < a.sh.N ? r0 + a.rows_per_block : a.sh.N;
+  const QJob job = get_job(a, job_id);
+  const int mbase = blockIdx.y * MT;
+  int nl = 1;
+  for (int t = 0; t < MT && mbase + t < a.sh.M; ++t) {
+    const int v = act_nl(a.tabs + ((size_t)job_id * a.sh.M + mbase + t) * a.tab_bytes);
+    nl = v > nl ? v : nl;
+  }
   if (nl == 1)
-    qgemv_body<Q4, C, P, LPR, UR, MT, 1>(job, sh, row0, m0, act, asum, KD);
+    tiled_tokens<Q4, G, 1, MT>(a, job, job_id, r0, r1, mbase);
   else if (nl == 2)
-    qgemv_body<Q4, C, P, LPR, UR, MT, 2>(job, sh, row0, m0, act, asum, KD);
+    tiled_tokens<Q4, G, 2, MT>(a, job, job_id, r0, r1, mbase);
   else
-    qgemv_body<Q4, C, P, LPR, UR, MT, 4>(job, sh, row0, m0, act, asum, KD);
+    tiled_tokens<Q4, G, 4, MT>(a, job, job_id, r0, r1, mbase);
 }
 
-// Any shape: one wave per output row, activations truncated on the fly,
-// plain wrapping int32 multiply-add.  Q4 follows the reference's byte
-// addressing exactly (row start n*rs, byte k/2, odd-K guard).
 template <bool Q4>
 __global__ __launch_bounds__(kBlock) void qgemv_generic(QShape sh, const QJob* __restrict__ jobs,
                                                         QJob one, int blocks_per_job) {
   const int job_id = blockIdx.x / blocks_per_job;
-  const int row = (blockIdx.x % blocks_per_job) * kWaves + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
+  const int r0 = (blockIdx.x % blocks_per_job) * kWaves;
+  const int r1 = r0 + kWaves < sh.N ? r0 + kWaves : sh.N;
   const QJob job = jobs ? jobs[job_id] : one;
-  if (row >= sh.N) return;
-  const uint8_t* wr = job.W + (size_t)row * (size_t)sh.rs;
-  const float sc = job.S[row];
-  for (int m = blockIdx.y; m < sh.M; m += gridDim.y) {
-    const float* a = job.A + (size_t)m * sh.lda;
-    uint32_t acc = 0;
-    if constexpr (!Q4) {
-      for (int k = lane; k < sh.K; k += kWave) {
-        const int32_t ai = f2i_trunc_x86(a[k] * 127.0f);
-        acc += (uint32_t)ai * (uint32_t)(int32_t)(int8_t)wr[k];
-      }
-    } else {
-      for (int j = lane; 2 * j < sh.K; j += kWave) {
-        const uint32_t byte = wr[j];
-        const int k = 2 * j;
-        const int32_t lo = (int32_t)(byte & 0x0Fu) - 8;
-        const int32_t hi = (int32_t)((byte >> 4) & 0x0Fu) - 8;
-        acc += (uint32_t)f2i_trunc_x86(a[k] * 7.0f) * (uint32_t)lo;
-        if (k + 1 < sh.K) acc += (uint32_t)f2i_trunc_x86(a[k + 1] * 7.0f) * (uint32_t)hi;
-      }
-    }
-    acc = group_sum_u32<kWave>(acc);
-    if (lane == 0) job.C[(size_t)m * sh.ldc + row] = qdot_epilogue(acc, Q4 ? 7.0f : 127.0f, sc);
-  }
+  const int m0 = blockIdx.y * 16;
+  const int m1 = m0 + 16 < sh.M ? m0 + 16 : sh.M;
+  generic_rows<Q4>(sh, job, r0, r1, m0, m1);
 }
 
 // fp32 path: one thread per output, k ascending, unfused multiply then add.
@@ -287,34 +231,34 @@ __global__ void zero_fill(float* p, size_t n) {
 }
 
 // ---- host-side variant selection ----
-using KernelFn = void (*)(QShape, const QJob*, QJob, int);
+using TiledFn = void (*)(TiledArgs);
 
 struct Variant {
-  KernelFn fn;
-  int rows_per_block;
+  TiledFn fn;
+  int wr;      // rows per wave group
   int mt;
-  int kd;          // LDS dwords per (token, limb)
   const char* name;
 };
 
-template <bool Q4, int C, int P, int LPR, int UR, int MT>
+template <bool Q4, class G, int MT>
 Variant make_variant(const char* name) {
-  constexpr int WR = kWave / LPR;
-  return Variant{qgemv_tiled<Q4, C, P, LPR, UR, MT>, kWaves * UR * WR, MT,
-                 LPR * C * P * (Q4 ? 2 : 1), name};
+  return Variant{qgemv_tiled<Q4, G, MT>, G::WR, MT, name};
 }
 
-// Row byte counts with a tiled kernel: lanes-per-row x chunk x passes x 4.
+// Row byte counts with a tiled geometry: LPR lanes x P dwordx4 x 16 bytes.
 template <bool Q4, int MT>
 bool pick_tiled(long long rb, Variant* v) {
   switch (rb) {
-    case 384:  *v = make_variant<Q4, 3, 1, 32, 2, MT>("tiled_c3p1l32"); return true;
-    case 512:  *v = make_variant<Q4, 4, 1, 32, 2, MT>("tiled_c4p1l32"); return true;
-    case 768:  *v = make_variant<Q4, 3, 1, 64, 4, MT>("tiled_c3p1l64"); return true;
-    case 1024: *v = make_variant<Q4, 4, 1, 64, 4, MT>("tiled_c4p1l64"); return true;
-    case 1536: *v = make_variant<Q4, 3, 2, 64, 4, MT>("tiled_c3p2l64"); return true;
-    case 2048: *v = make_variant<Q4, 4, 2, 64, 4, MT>("tiled_c4p2l64"); return true;
-    case 4096: *v = make_variant<Q4, 4, 4, 64, 2, MT>("tiled_c4p4l64"); return true;
+    case 192:  *v = make_variant<Q4, TileGeom<3, 4>, MT>("tiled_p3l4"); return true;
+    case 256:  *v = make_variant<Q4, TileGeom<4, 4>, MT>("tiled_p4l4"); return true;
+    case 384:  *v = make_variant<Q4, TileGeom<3, 8>, MT>("tiled_p3l8"); return true;
+    case 512:  *v = make_variant<Q4, TileGeom<4, 8>, MT>("tiled_p4l8"); return true;
+    case 768:  *v = make_variant<Q4, TileGeom<3, 16>, MT>("tiled_p3l16"); return true;
+    case 1024: *v = make_variant<Q4, TileGeom<4, 16>, MT>("tiled_p4l16"); return true;
+    case 1536: *v = make_variant<Q4, TileGeom<3, 32>, MT>("tiled_p3l32"); return true;
+    case 2048: *v = make_variant<Q4, TileGeom<4, 32>, MT>("tiled_p4l32"); return true;
+    case 3072: *v = make_variant<Q4, TileGeom<3, 64>, MT>("tiled_p3l64"); return true;
+    case 4096: *v = make_variant<Q4, TileGeom<4, 64>, MT>("tiled_p4l64"); return true;
     default: return false;
   }
 }
@@ -322,13 +266,38 @@ bool pick_tiled(long long rb, Variant* v) {
 bool select_tiled(const QShape& sh, const void* w_base, Variant* v) {
   const bool q4 = sh.dtype == 3;
   if (q4 && (sh.K & 1)) return false;
+  if (sh.K <= 0) return false;
   const long long rb = q4 ? sh.K / 2 : sh.K;
   if (sh.rs != rb) return false;
   if (w_base && ((uintptr_t)w_base % 16) != 0) return false;
-  if (sh.rs % 16 != 0) return false;
-  const int mt = sh.M == 1 ? 1 : 4;
-  if (q4) return mt == 1 ? pick_tiled<true, 1>(rb, v) : pick_tiled<true, 4>(rb, v);
-  return mt == 1 ? pick_tiled<false, 1>(rb, v) : pick_tiled<false, 4>(rb, v);
+  const int mt = sh.M == 1 ? 1 : (sh.M == 2 ? 2 : 4);
+  if (q4) {
+    if (mt == 1) return pick_tiled<true, 1>(rb, v);
+    if (mt == 2) return pick_tiled<true, 2>(rb, v);
+    return pick_tiled<true, 4>(rb, v);
+  }
+  if (mt == 1) return pick_tiled<false, 1>(rb, v);
+  if (mt == 2) return pick_tiled<false, 2>(rb, v);
+  return pick_tiled<false, 4>(rb, v);
+}
+
+// Workspace for packed activation tables (grown on demand; freed never).
+uint8_t* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+hipError_t ensure_ws(size_t need) {
+  if (need <= g_ws_bytes) return hipSuccess;
+  if (g_ws) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    (void)hipFree(g_ws);
+  }
+  g_ws = nullptr;
+  g_ws_bytes = 0;
+  size_t cap = need < ((size_t)1 << 20) ? ((size_t)1 << 20) : need + need / 2;
+  hipError_t e = hipMalloc(&g_ws, cap);
+  if (e == hipSuccess) g_ws_bytes = cap;
+  return e;
 }
 
 }  // namespace
@@ -341,19 +310,43 @@ const char* qgemv_variant_name(const QShape& sh, const void* w_base) {
 
 hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
                         hipStream_t stream) {
-  if (sh.M <= 0 || sh.N <= 0 || sh.K <= 0 || njobs <= 0) return hipSuccess;
+  if (sh.M <= 0 || sh.N <= 0 || njobs <= 0) return hipSuccess;
   if (sh.dtype != 2 && sh.dtype != 3) return hipErrorInvalidValue;
   Variant v;
   // With a device job array the host cannot see the pointers; callers of the
-  // batched entry point guarantee 16-byte aligned rows (checked in capi.cpp).
+  // batched entry point guarantee 16-byte aligned packed rows (capi.cpp).
   if (select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) {
-    const int bpj = (sh.N + v.rows_per_block - 1) / v.rows_per_block;
-    const size_t lds = ((size_t)v.mt * 4 * v.kd + 4) * sizeof(uint32_t);
-    dim3 grid((unsigned)((long long)bpj * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
-    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), lds, stream, sh, jobs_dev, one, bpj);
+    const size_t tb = act_table_bytes(sh.K);
+    hipError_t e = ensure_ws(tb * (size_t)njobs * (size_t)sh.M);
+    if (e != hipSuccess) return e;
+    if (sh.dtype == 3)
+      hipLaunchKernelGGL(act_pack_kernel<true>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
+                         jobs_dev, one, g_ws, tb);
+    else
+      hipLaunchKernelGGL(act_pack_kernel<false>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
+                         jobs_dev, one, g_ws, tb);
+    // rows per block: a multiple of (waves x rows per wave group), large
+    // enough to amortise the activation loads, small enough for >= ~2048 blocks
+    const int unit = kWaves * v.wr;
+    const long long total_rows = (long long)sh.N * njobs;
+    long long rpb = (total_rows + 2047) / 2048;
+    rpb = (rpb + unit - 1) / unit * unit;
+    if (rpb < unit) rpb = unit;
+    if (rpb > 8 * unit) rpb = 8 * unit;
+    if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
+    TiledArgs a;
+    a.sh = sh;
+    a.jobs = jobs_dev;
+    a.one = one;
+    a.tabs = g_ws;
+    a.tab_bytes = tb;
+    a.rows_per_block = (int)rpb;
+    a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
+    dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
+    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
   } else {
     const int bpj = (sh.N + kWaves - 1) / kWaves;
-    dim3 grid((unsigned)((long long)bpj * njobs), (unsigned)(sh.M < 64 ? sh.M : 64));
+    dim3 grid((unsigned)((long long)bpj * njobs), (unsigned)((sh.M + 15) / 16));
     if (sh.dtype == 3)
       hipLaunchKernelGGL(qgemv_generic<true>, grid, dim3(kBlock), 0, stream, sh, jobs_dev, one, bpj);
     else

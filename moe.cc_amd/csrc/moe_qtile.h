@@ -1,0 +1,180 @@
+// moe_qtile.h - quantized row-tile machinery shared by the GEMV and the MoE
+// kernels: packed activation tables and exact integer row dots.
+//
+// Arithmetic contract (kernels.c:51-74, 96-128):
+//   a_k = (int32)(x_k * 127.0f)  (Q8)   or  (int32)(x_k * 7.0f)  (Q4)
+//   dot = sum_k a_k * w_k   in wrapping int32 (order-free, exact)
+//
+// Packed activation table ("act table") of one activation row, built once
+// by pack_act_row and then read by every wave that needs the row:
+//   header (16 B): nl (limbs needed: 1, 2 or 4), asum (sum_k a_k, wrapping)
+//   4 limb planes of K bytes each (a = sum_l b_l 256^l, b_l signed int8):
+//     Q8: plane dword d = limb of a[4d .. 4d+3]
+//     Q4: plane dword d        (d < K/8)  = limb of a[8d], a[8d+2], a[8d+4], a[8d+6]
+//         plane dword K/8 + d            = limb of a[8d+1], a[8d+3], a[8d+5], a[8d+7]
+// so that one weight dword meets its activations in one (Q8) or two (Q4,
+// even/odd nibbles) v_dot4_i32_i8 per limb.  Q4 weights enter as unsigned
+// nibbles u = w + 8 and the offset is removed once per row: sum a*w =
+// sum a*u - 8*asum.
+#pragma once
+#include "moe_device.h"
+
+namespace moe {
+
+constexpr int kTileBlock = 256;
+constexpr int kTileWaves = kTileBlock / kWave;
+
+__host__ __device__ constexpr size_t act_table_bytes(int K) {
+  return 16 + 4 * (((size_t)K + 15) / 16) * 16;
+}
+__device__ __forceinline__ int act_nl(const uint8_t* tab) {
+  return *reinterpret_cast<const int*>(tab);
+}
+__device__ __forceinline__ uint32_t act_asum(const uint8_t* tab) {
+  return *reinterpret_cast<const uint32_t*>(tab + 4);
+}
+__device__ __forceinline__ const uint32_t* act_plane(const uint8_t* tab, int K, int l) {
+  return reinterpret_cast<const uint32_t*>(tab + 16 + (size_t)l * (((size_t)K + 15) / 16) * 16);
+}
+
+// Packs one activation row into its table.  Called by a whole block (any
+// size); contains barriers.  `scratch` is 2 ints of LDS.
+template <bool Q4>
+__device__ void pack_act_row(const float* __restrict__ x, int K, uint8_t* __restrict__ tab,
+                             int* scratch) {
+  const float mult = Q4 ? 7.0f : 127.0f;
+  const size_t plane = (((size_t)K + 15) / 16) * 16;
+  uint32_t* p0 = reinterpret_cast<uint32_t*>(tab + 16);
+  if (threadIdx.x == 0) { scratch[0] = 1; scratch[1] = 0; }
+  __syncthreads();
+  int nl = 1;
+  uint32_t part = 0;
+  const int nd = Q4 ? (K + 7) / 8 : (K + 3) / 4;
+  for (int d = threadIdx.x; d < nd; d += blockDim.x) {
+    constexpr int V = Q4 ? 8 : 4;
+    uint32_t b[V][4];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int k = V * d + i;
+      const int32_t v = k < K ? f2i_trunc_x86(x[k] * mult) : 0;
+      const int n = limbs_needed(v);
+      nl = n > nl ? n : nl;
+      part += (uint32_t)v;
+      split_limbs(v, b[i]);
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      uint32_t* pl = p0 + (size_t)l * (plane / 4);
+      if constexpr (!Q4) {
+        pl[d] = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+      } else {
+        const int KW = (K + 7) / 8;
+        pl[d] = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
+        pl[KW + d] = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
+      }
+    }
+  }
+  atomicMax(&scratch[0], nl);
+  atomicAdd(reinterpret_cast<unsigned*>(&scratch[1]), part);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    reinterpret_cast<int*>(tab)[0] = scratch[0];
+    reinterpret_cast<uint32_t*>(tab)[1] = (uint32_t)scratch[1];
+  }
+}
+
+// ---- cross-lane integer sums with DPP ----
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+
+// Sum over groups of W consecutive lanes (W = 4, 8, 16, 32, 64).  For W <= 16
+// every lane of the group gets the total; for W = 32 / 64 lane 0 of the group
+// is guaranteed to have it.
+template <int W>
+__device__ __forceinline__ uint32_t group_sum_dpp(uint32_t v) {
+  v += dpp_u32<0xB1>(v);                 // quad_perm [1,0,3,2]
+  v += dpp_u32<0x4E>(v);                 // quad_perm [2,3,0,1]
+  if (W >= 8) v += dpp_u32<0x141>(v);    // row_half_mirror
+  if (W >= 16) v += dpp_u32<0x140>(v);   // row_mirror
+  if (W >= 32) v += (uint32_t)__shfl_xor((int)v, 16, kWave);
+  if (W >= 64) v += (uint32_t)__shfl_xor((int)v, 32, kWave);
+  return v;
+}
+
+// Geometry of one tiled configuration: a row of ROW_BYTES = LPR*P*16 bytes is
+// read by LPR consecutive lanes, each with P dwordx4 loads at byte offsets
+// (p*LPR + r)*16; a wave covers WR = 64/LPR rows at once.
+template <int P_, int LPR_>
+struct TileGeom {
+  static constexpr int P = P_, LPR = LPR_;
+  static constexpr int WR = kWave / LPR;
+  static constexpr int DW = P * 4;                 // weight dwords per lane per row
+  static constexpr int ROW_BYTES = LPR * P * 16;
+};
+
+template <class G>
+__device__ __forceinline__ void load_row_regs(const uint8_t* row, uint32_t (&w)[G::DW]) {
+  const int r = (threadIdx.x % kWave) % G::LPR;
+#pragma unroll
+  for (int p = 0; p < G::P; ++p) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + (size_t)(p * G::LPR + r) * 16);
+    w[4 * p + 0] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+  }
+}
+
+// This lane's activation dwords for its weight chunk: Q8 -> a[l][i] (i <
+// DW); Q4 -> even dwords in a[l][i], odd in a[l][DW + i].
+template <bool Q4, class G, int NL>
+struct ActRegs {
+  uint32_t a[NL][Q4 ? 2 * G::DW : G::DW];
+};
+
+template <bool Q4, class G, int NL>
+__device__ __forceinline__ void load_act_regs(const uint8_t* tab, int K, ActRegs<Q4, G, NL>& ar) {
+  const int r = (threadIdx.x % kWave) % G::LPR;
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const uint32_t* pl = act_plane(tab, K, l);
+#pragma unroll
+    for (int p = 0; p < G::P; ++p) {
+      const int d = (p * G::LPR + r) * 4;   // first weight dword of the chunk
+      const uint4 e = *reinterpret_cast<const uint4*>(pl + d);
+      ar.a[l][4 * p + 0] = e.x; ar.a[l][4 * p + 1] = e.y;
+      ar.a[l][4 * p + 2] = e.z; ar.a[l][4 * p + 3] = e.w;
+      if constexpr (Q4) {
+        const uint4 o = *reinterpret_cast<const uint4*>(pl + (K + 7) / 8 + d);
+        ar.a[l][G::DW + 4 * p + 0] = o.x; ar.a[l][G::DW + 4 * p + 1] = o.y;
+        ar.a[l][G::DW + 4 * p + 2] = o.z; ar.a[l][G::DW + 4 * p + 3] = o.w;
+      }
+    }
+  }
+}
+
+// This lane's partial dot of one weight row chunk with one activation row.
+template <bool Q4, class G, int NL>
+__device__ __forceinline__ uint32_t lane_dot(const uint32_t (&w)[G::DW],
+                                             const ActRegs<Q4, G, NL>& ar) {
+  int32_t acc[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) acc[l] = 0;
+#pragma unroll
+  for (int i = 0; i < G::DW; ++i) {
+    if constexpr (!Q4) {
+#pragma unroll
+      for (int l = 0; l < NL; ++l) acc[l] = dot4(w[i], ar.a[l][i], acc[l]);
+    } else {
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu;
+      const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        acc[l] = dot4(lo, ar.a[l][i], acc[l]);
+        acc[l] = dot4(hi, ar.a[l][G::DW + i], acc[l]);
+      }
+    }
+  }
+  return combine_limbs<NL>(acc);
+}
+
+}  // namespace moe

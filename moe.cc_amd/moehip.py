@@ -58,6 +58,7 @@ _SIGS = {
     "moe_get_stream": (_P, []),
     "moe_synchronize": (_I, []),
     "moe_weight_cache_clear": (_I, []),
+    "moe_weight_cache_mode": (_I, [_I]),
     "moe_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
     "moe_free": (_I, [_P]),
     "moe_memcpy_h2d": (_I, [_P, _P, _SZ]),
