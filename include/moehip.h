@@ -178,6 +178,41 @@ moe_status moe_fill_normal_dev(float* out, size_t n, uint64_t seed, float mean, 
  *          low nibble = even column.  Bit-identical to the exporter's fp32 ops. */
 moe_status moe_quantize_rows_dev(int dtype, const float* W, long long N, int K, void* q, float* s);
 
+/* ---- the MoE block of one layer (test_model_trace.c:460-517) ---- */
+typedef struct moe_layer moe_layer;
+
+/* Uploads one layer from the reference's structures (model.h:9-58, bound by
+ * load_all_weights model.h:220-305): router_w/router_b, rms2_w and the E
+ * quantized gate/up/down experts.  Host pointers; copied. */
+moe_status moe_layer_create(const QwenConfig* cfg, const QwenLayerWeights* lw, moe_layer** out);
+/* Same from contiguous arrays: router_w [E x D], router_b [E] or NULL,
+ * rms2_w [D] or NULL, gq/uq [E x d_ff x rb_g] bytes (rb_g = D for Q8, D/2
+ * for Q4), gs/us [E x d_ff], dq [E x D x rb_d] (rb_d = d_ff or d_ff/2),
+ * ds [E x D].  src_on_device: the arrays are device pointers (copied). */
+moe_status moe_layer_create_raw(int dtype, int D, int d_ff, int E, int top_k,
+                                const float* router_w, const float* router_b, const float* rms2_w,
+                                const void* gq, const float* gs, const void* uq, const float* us,
+                                const void* dq, const float* ds, int src_on_device,
+                                moe_layer** out);
+moe_status moe_layer_destroy(moe_layer* layer);
+/* test_model_trace.c:463-517 on device arrays:
+ *   out[t] = x_resid[t] + sum_j p[t,j] * down_e(silu(gate_e x) * up_e x),
+ *   e = idx[t,j], the top_k experts of logits = x_norm Wr^T (+ b), p their
+ *   softmax; x_resid may be NULL (no residual).  x_norm, x_resid, out:
+ *   [T x D]; idx_out / p_out ([T x top_k], int32 / fp32) may be NULL.
+ *   Bit-identical to the reference on the same inputs. */
+moe_status moe_layer_forward(moe_layer* layer, const float* x_norm, const float* x_resid, int T,
+                             float* out, int32_t* idx_out, float* p_out);
+/* test_model_trace.c:460-517 including norm2: out = x + MoE(rmsnorm(x, rms2_w)) */
+moe_status moe_block_forward(moe_layer* layer, const float* x, int T, float* out, float eps);
+/* test_model_trace.c:241-255 on device arrays: y = (x / sqrt(mean(x^2)+eps)) * w
+ * (w may be NULL), sequential sum of squares as in the reference */
+moe_status moe_rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps);
+/* Device pointers of the last forward's router logits [T x E], SwiGLU
+ * outputs h [T*top_k x d_ff] and expert outputs y [T*top_k x D] (for tests). */
+moe_status moe_layer_debug_buffers(moe_layer* layer, const float** logits, const float** h,
+                                   const float** y);
+
 /* Name of the kernel variant the GEMV entry points use for a shape. */
 const char* moe_gemv_variant(int dtype, int M, int N, int K);
 

@@ -51,129 +51,29 @@ __global__ __launch_bounds__(kBlock) void act_pack_kernel(QShape sh, const QJob*
                    scratch);
 }
 
-// Plain exact path for the rows [r0, r1) of one job and tokens [m0, m1):
-// one wave per row, int32 multiply-add on the fly.
-template <bool Q4>
-__device__ void generic_rows(const QShape& sh, const QJob& job, int r0, int r1, int m0, int m1) {
-  const int lane = threadIdx.x % kWave;
-  for (int row = r0 + (int)(threadIdx.x / kWave); row < r1; row += blockDim.x / kWave) {
-    const uint8_t* wr = job.W + (size_t)row * (size_t)sh.rs;
-    const float sc = job.S[row];
-    for (int m = m0; m < m1; ++m) {
-      const float* a = job.A + (size_t)m * sh.lda;
-      uint32_t acc = 0;
-      if constexpr (!Q4) {
-        for (int k = lane; k < sh.K; k += kWave) {
-          const int32_t ai = f2i_trunc_x86(a[k] * 127.0f);
-          acc += (uint32_t)ai * (uint32_t)(int32_t)(int8_t)wr[k];
-        }
-      } else {
-        for (int j = lane; 2 * j < sh.K; j += kWave) {
-          const uint32_t byte = wr[j];
-          const int k = 2 * j;
-          const int32_t lo = (int32_t)(byte & 0x0Fu) - 8;
-          const int32_t hi = (int32_t)((byte >> 4) & 0x0Fu) - 8;
-          acc += (uint32_t)f2i_trunc_x86(a[k] * 7.0f) * (uint32_t)lo;
-          if (k + 1 < sh.K) acc += (uint32_t)f2i_trunc_x86(a[k + 1] * 7.0f) * (uint32_t)hi;
-        }
-      }
-      acc = group_sum_dpp<kWave>(acc);
-      if (lane == 0) job.C[(size_t)m * sh.ldc + row] = qdot_epilogue(acc, Q4 ? 7.0f : 127.0f, sc);
-    }
-  }
-}
-
-// Rows [r0, r1) of one job against MTI token tables starting at token m0.
-// Each wave walks row groups gi = wave, wave + 4, ...; the loads of the next
-// group are issued before the current one is reduced.
-template <bool Q4, class G, int NL, int MTI>
-__device__ __forceinline__ void tiled_rows(const QShape& sh, const QJob& job,
-                                           const uint8_t* const* tab, int r0, int r1, int m0) {
-  ActRegs<Q4, G, NL> ar[MTI];
-  uint32_t asum[MTI];
+// Epilogue of the plain GEMV: C[m, row] = ((float)dot / div) * S[row].
+struct GemvEpiMaker {
+  const float* S;
+  float* C;
+  int M, ldc, mbase;
+  float div;
+  template <int MTI>
+  struct Epi {
+    const float* S;
+    float* C;
+    int M, ldc, m0;
+    float div;
+    template <class Tot>
+    __device__ void operator()(int row, const Tot& tot) const {
+      const float sc = S[row];
 #pragma unroll
-  for (int t = 0; t < MTI; ++t) {
-    load_act_regs<Q4, G, NL>(tab[t], sh.K, ar[t]);
-    asum[t] = Q4 ? act_asum(tab[t]) : 0u;
-  }
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int g = lane / G::LPR, r = lane % G::LPR;
-  const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
-  const float div = Q4 ? 7.0f : 127.0f;
-
-  auto row_of = [&](int gi) { return r0 + gi * G::WR + g; };
-  auto load = [&](int gi, uint32_t (&w)[G::DW]) {
-    const int row = row_of(gi);
-    if (row < r1) {
-      load_row_regs<G>(job.W + (size_t)row * (size_t)sh.rs, w);
-    } else {
-#pragma unroll
-      for (int i = 0; i < G::DW; ++i) w[i] = 0;
+      for (int t = 0; t < MTI; ++t)
+        if (m0 + t < M) C[(size_t)(m0 + t) * ldc + row] = qdot_epilogue(tot[0][t], div, sc);
     }
   };
-  auto finish = [&](int gi, const uint32_t (&w)[G::DW]) {
-    const int row = row_of(gi);
-    uint32_t tot[MTI];
-#pragma unroll
-    for (int t = 0; t < MTI; ++t) tot[t] = group_sum_dpp<G::LPR>(lane_dot<Q4, G, NL>(w, ar[t]));
-    if (r == 0 && row < r1) {
-      const float sc = job.S[row];
-#pragma unroll
-      for (int t = 0; t < MTI; ++t) {
-        const int m = m0 + t;
-        if (m < sh.M) {
-          const uint32_t v = Q4 ? tot[t] - 8u * asum[t] : tot[t];
-          job.C[(size_t)m * sh.ldc + row] = qdot_epilogue(v, div, sc);
-        }
-      }
-    }
-  };
-
-  uint32_t wa[G::DW], wb[G::DW];
-  int gi = wave;
-  if (gi < ngroups) load(gi, wa);
-  while (gi < ngroups) {
-    int gn = gi + kWaves;
-    if (gn < ngroups) load(gn, wb);
-    finish(gi, wa);
-    gi = gn;
-    if (gi >= ngroups) break;
-    gn = gi + kWaves;
-    if (gn < ngroups) load(gn, wa);
-    finish(gi, wb);
-    gi = gn;
-  }
-}
-
-// Token slots per weight pass so that activation registers stay <= ~96.
-template <bool Q4, class G, int NL>
-constexpr int mti_for() {
-  constexpr int per = NL * G::DW * (Q4 ? 2 : 1);
-  constexpr int n = 96 / per;
-  return n >= 4 ? 4 : (n >= 2 ? 2 : (n >= 1 ? 1 : 0));
-}
-
-template <bool Q4, class G, int NL, int MT>
-__device__ __forceinline__ void tiled_tokens(const TiledArgs& a, const QJob& job, int job_id, int r0,
-                                             int r1, int mbase) {
-  constexpr int MTI0 = mti_for<Q4, G, NL>();
-  if constexpr (MTI0 == 0) {
-    generic_rows<Q4>(a.sh, job, r0, r1, mbase, mbase + MT < a.sh.M ? mbase + MT : a.sh.M);
-  } else {
-    constexpr int MTI = MTI0 < MT ? MTI0 : MT;
-#pragma unroll
-    for (int m0 = 0; m0 < MT; m0 += MTI) {
-      if (mbase + m0 >= a.sh.M) break;
-      const uint8_t* tab[MTI];
-#pragma unroll
-      for (int t = 0; t < MTI; ++t) {
-        const int m = mbase + m0 + t < a.sh.M ? mbase + m0 + t : a.sh.M - 1;
-        tab[t] = a.tabs + ((size_t)job_id * a.sh.M + m) * a.tab_bytes;
-      }
-      tiled_rows<Q4, G, NL, MTI>(a.sh, job, tab, r0, r1, mbase + m0);
-    }
-  }
-}
+  template <int MTI>
+  __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{S, C, M, ldc, mbase + t0, div}; }
+};
 
 template <bool Q4, class G, int MT>
 __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
@@ -182,17 +82,18 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
   const int r1 = r0 + a.rows_per_block < a.sh.N ? r0 + a.rows_per_block : a.sh.N;
   const QJob job = get_job(a, job_id);
   const int mbase = blockIdx.y * MT;
-  int nl = 1;
-  for (int t = 0; t < MT && mbase + t < a.sh.M; ++t) {
-    const int v = act_nl(a.tabs + ((size_t)job_id * a.sh.M + mbase + t) * a.tab_bytes);
-    nl = v > nl ? v : nl;
+  const int ntok = a.sh.M - mbase < MT ? a.sh.M - mbase : MT;
+  const uint8_t* tabs[MT];
+  const float* xs[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = mbase + (t < ntok ? t : ntok - 1);
+    tabs[t] = a.tabs + ((size_t)job_id * a.sh.M + m) * a.tab_bytes;
+    xs[t] = job.A + (size_t)m * a.sh.lda;
   }
-  if (nl == 1)
-    tiled_tokens<Q4, G, 1, MT>(a, job, job_id, r0, r1, mbase);
-  else if (nl == 2)
-    tiled_tokens<Q4, G, 2, MT>(a, job, job_id, r0, r1, mbase);
-  else
-    tiled_tokens<Q4, G, 4, MT>(a, job, job_id, r0, r1, mbase);
+  const uint8_t* W[1] = {job.W};
+  GemvEpiMaker mk{job.S, job.C, a.sh.M, a.sh.ldc, mbase, Q4 ? 7.0f : 127.0f};
+  stream_tokens<Q4, G, 1, MT>(W, a.sh.rs, a.sh.K, tabs, xs, ntok, r0, r1, mk);
 }
 
 template <bool Q4>
@@ -204,7 +105,12 @@ __global__ __launch_bounds__(kBlock) void qgemv_generic(QShape sh, const QJob* _
   const QJob job = jobs ? jobs[job_id] : one;
   const int m0 = blockIdx.y * 16;
   const int m1 = m0 + 16 < sh.M ? m0 + 16 : sh.M;
-  generic_rows<Q4>(sh, job, r0, r1, m0, m1);
+  const uint8_t* W[1] = {job.W};
+  for (int m = m0; m < m1; ++m) {
+    GemvEpiMaker mk{job.S, job.C, sh.M, sh.ldc, m, Q4 ? 7.0f : 127.0f};
+    auto epi = mk.at<1>(0);
+    generic_rows_fp32<Q4, 1>(W, sh.rs, sh.K, job.A + (size_t)m * sh.lda, r0, r1, epi);
+  }
 }
 
 // fp32 path: one thread per output, k ascending, unfused multiply then add.

@@ -17,6 +17,8 @@
 // nibbles u = w + 8 and the offset is removed once per row: sum a*w =
 // sum a*u - 8*asum.
 #pragma once
+#include <type_traits>
+
 #include "moe_device.h"
 
 namespace moe {
@@ -175,6 +177,149 @@ __device__ __forceinline__ uint32_t lane_dot(const uint32_t (&w)[G::DW],
     }
   }
   return combine_limbs<NL>(acc);
+}
+
+// Streams rows [r0, r1) of NM matrices (W[mat], row stride rs) against MTI
+// packed activation tables; each wave walks row groups gi = wave, wave+4, ...
+// with the loads of the next group issued before the current one is reduced.
+// For each valid row, lane 0 of its lane group calls
+//     epi(row, tot)   with tot[mat][t] = exact int32 dot (Q4 offset removed).
+template <bool Q4, class G, int NL, int MTI, int NM, class Epi>
+__device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long rs, int K,
+                                            const uint8_t* const* tab, int r0, int r1,
+                                            Epi& epi) {
+  ActRegs<Q4, G, NL> ar[MTI];
+  uint32_t asum[MTI];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / G::LPR, r = lane % G::LPR;
+  const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
+  auto load = [&](int gi, uint32_t (&w)[NM][G::DW]) {
+    const int row = r0 + gi * G::WR + g;
+#pragma unroll
+    for (int mat = 0; mat < NM; ++mat) {
+      if (row < r1) {
+        load_row_regs<G>(W[mat] + (size_t)row * (size_t)rs, w[mat]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < G::DW; ++i) w[mat][i] = 0;
+      }
+    }
+  };
+  auto finish = [&](int gi, const uint32_t (&w)[NM][G::DW]) {
+    const int row = r0 + gi * G::WR + g;
+    uint32_t tot[NM][MTI];
+#pragma unroll
+    for (int mat = 0; mat < NM; ++mat)
+#pragma unroll
+      for (int t = 0; t < MTI; ++t) {
+        const uint32_t v = group_sum_dpp<G::LPR>(lane_dot<Q4, G, NL>(w[mat], ar[t]));
+        tot[mat][t] = Q4 ? v - 8u * asum[t] : v;
+      }
+    if (r == 0 && row < r1) epi(row, tot);
+  };
+
+  uint32_t wa[NM][G::DW], wb[NM][G::DW];
+  int gi = wave;
+  if (gi < ngroups) load(gi, wa);  // weights first: their latency is the longer one
+#pragma unroll
+  for (int t = 0; t < MTI; ++t) {
+    load_act_regs<Q4, G, NL>(tab[t], K, ar[t]);
+    asum[t] = Q4 ? act_asum(tab[t]) : 0u;
+  }
+  while (gi < ngroups) {
+    int gn = gi + kTileWaves;
+    if (gn < ngroups) load(gn, wb);
+    finish(gi, wa);
+    gi = gn;
+    if (gi >= ngroups) break;
+    gn = gi + kTileWaves;
+    if (gn < ngroups) load(gn, wa);
+    finish(gi, wb);
+    gi = gn;
+  }
+}
+
+// Token slots per weight pass so that activation registers stay within a
+// budget (96 dwords for one matrix, 64 for two); 0 = does not fit.
+template <bool Q4, class G, int NL, int NM>
+constexpr int mti_for() {
+  constexpr int per = NL * G::DW * (Q4 ? 2 : 1);
+  constexpr int n = (NM == 1 ? 96 : 64) / per;
+  return n >= 4 ? 4 : (n >= 2 ? 2 : (n >= 1 ? 1 : 0));
+}
+
+// Exact fallback on fp32 activations: one wave per row, wrapping int32
+// multiply-add with the reference's byte addressing (row start n*rs, byte
+// k/2 for Q4, odd-K guard).  Calls epi(row, tot) like stream_rows with one
+// token slot.
+template <bool Q4, int NM, class Epi>
+__device__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K, const float* x,
+                                  int r0, int r1, Epi& epi) {
+  const int lane = threadIdx.x % kWave;
+  for (int row = r0 + (int)(threadIdx.x / kWave); row < r1; row += blockDim.x / kWave) {
+    uint32_t tot[NM][1];
+#pragma unroll
+    for (int mat = 0; mat < NM; ++mat) {
+      const uint8_t* wr = W[mat] + (size_t)row * (size_t)rs;
+      uint32_t acc = 0;
+      if constexpr (!Q4) {
+        for (int k = lane; k < K; k += kWave)
+          acc += (uint32_t)f2i_trunc_x86(x[k] * 127.0f) * (uint32_t)(int32_t)(int8_t)wr[k];
+      } else {
+        for (int j = lane; 2 * j < K; j += kWave) {
+          const uint32_t byte = wr[j];
+          const int k = 2 * j;
+          acc += (uint32_t)f2i_trunc_x86(x[k] * 7.0f) * (uint32_t)((int32_t)(byte & 0x0Fu) - 8);
+          if (k + 1 < K)
+            acc += (uint32_t)f2i_trunc_x86(x[k + 1] * 7.0f) *
+                   (uint32_t)((int32_t)((byte >> 4) & 0x0Fu) - 8);
+        }
+      }
+      tot[mat][0] = group_sum_dpp<kWave>(acc);
+    }
+    if (lane == 0) epi(row, tot);
+  }
+}
+
+// All tokens of a block against rows [r0, r1): picks the limb count from the
+// tables' headers (uniform), then walks token chunks of the largest size that
+// fits in registers.  make_epi(t0) returns the epilogue for token slots
+// t0 .. t0+MTI-1 (an object with a templated operator()(row, tot)).
+// xs[t] are the fp32 activation rows, used only by the exact fallback.
+template <bool Q4, class G, int NM, int MT, class MakeEpi>
+__device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
+                              const uint8_t* const* tabs, const float* const* xs, int ntok, int r0,
+                              int r1, MakeEpi& make_epi) {
+  int nl = 1;
+  for (int t = 0; t < ntok; ++t) {
+    const int v = act_nl(tabs[t]);
+    nl = v > nl ? v : nl;
+  }
+  auto run = [&](auto nl_tag) {
+    constexpr int NL = decltype(nl_tag)::value;
+    constexpr int M0 = mti_for<Q4, G, NL, NM>();
+    if constexpr (M0 == 0) {
+      for (int t = 0; t < ntok; ++t) {
+        auto epi = make_epi.template at<1>(t);
+        generic_rows_fp32<Q4, NM>(W, rs, K, xs[t], r0, r1, epi);
+      }
+    } else {
+      constexpr int MTI = M0 < MT ? M0 : MT;
+      for (int t0 = 0; t0 < ntok; t0 += MTI) {
+        const uint8_t* tb[MTI];
+#pragma unroll
+        for (int t = 0; t < MTI; ++t) tb[t] = tabs[t0 + t < ntok ? t0 + t : ntok - 1];
+        auto epi = make_epi.template at<MTI>(t0);
+        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi);
+      }
+    }
+  };
+  if (nl == 1)
+    run(std::integral_constant<int, 1>());
+  else if (nl == 2)
+    run(std::integral_constant<int, 2>());
+  else
+    run(std::integral_constant<int, 4>());
 }
 
 }  // namespace moe

@@ -80,6 +80,15 @@ _SIGS = {
     "moe_expf_bits_dev": (_I, [ctypes.c_uint32, _P, _SZ]),
     "moe_fill_normal_dev": (_I, [_P, _SZ, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
     "moe_quantize_rows_dev": (_I, [_I, _P, ctypes.c_longlong, _I, _P, _P]),
+    "moe_layer_create": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "moe_layer_create_raw": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                                  ctypes.POINTER(_P)]),
+    "moe_layer_destroy": (_I, [_P]),
+    "moe_layer_forward": (_I, [_P, _P, _P, _I, _P, _P, _P]),
+    "moe_block_forward": (_I, [_P, _P, _I, _P, ctypes.c_float]),
+    "moe_rmsnorm_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
+    "moe_layer_debug_buffers": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P),
+                                     ctypes.POINTER(_P)]),
 }
 
 
@@ -209,5 +218,80 @@ class Event:
         try:
             if self.ptr and _lib is not None:
                 _lib.moe_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class MoeLayer:
+    """Device-resident MoE block of one layer (test_model_trace.c:460-517)."""
+
+    def __init__(self, handle, dtype, D, d_ff, E, top_k):
+        self.h, self.dtype, self.D, self.d_ff, self.E, self.top_k = handle, dtype, D, d_ff, E, top_k
+
+    @classmethod
+    def from_arrays(cls, dtype, router_w, router_b, gq, gs, uq, us, dq, ds, rms2_w=None,
+                    top_k=8):
+        """Host arrays: router_w [E, D], gq/uq [E, d_ff, rb_g], dq [E, D, rb_d], scales fp32."""
+        router_w = _f32(router_w)
+        E, D = router_w.shape
+        d_ff = gq.shape[1]
+        keep = [router_w, np.ascontiguousarray(gq), _f32(gs), np.ascontiguousarray(uq), _f32(us),
+                np.ascontiguousarray(dq), _f32(ds)]
+        rb = None if router_b is None else _f32(router_b)
+        rw2 = None if rms2_w is None else _f32(rms2_w)
+        h = _P()
+        check(lib().moe_layer_create_raw(
+            dtype, D, d_ff, E, top_k, keep[0].ctypes.data,
+            None if rb is None else rb.ctypes.data, None if rw2 is None else rw2.ctypes.data,
+            keep[1].ctypes.data, keep[2].ctypes.data, keep[3].ctypes.data, keep[4].ctypes.data,
+            keep[5].ctypes.data, keep[6].ctypes.data, 0, ctypes.byref(h)), "moe_layer_create_raw")
+        return cls(h.value, dtype, D, d_ff, E, top_k)
+
+    def forward_dev(self, x_norm_ptr, x_resid_ptr, T, out_ptr, idx_ptr=None, p_ptr=None):
+        check(lib().moe_layer_forward(self.h, x_norm_ptr, x_resid_ptr, T, out_ptr, idx_ptr, p_ptr),
+              "moe_layer_forward")
+
+    def forward(self, x_norm: np.ndarray, x_resid: Optional[np.ndarray]):
+        """Host-array convenience: returns (out [T, D], idx [T, k], p [T, k])."""
+        x_norm = _f32(x_norm)
+        T = x_norm.shape[0]
+        dx = DeviceBuffer.from_array(x_norm)
+        dr = DeviceBuffer.from_array(_f32(x_resid)) if x_resid is not None else None
+        do = DeviceBuffer(x_norm.nbytes)
+        di = DeviceBuffer(T * self.top_k * 4)
+        dp = DeviceBuffer(T * self.top_k * 4)
+        self.forward_dev(dx.ptr, None if dr is None else dr.ptr, T, do.ptr, di.ptr, dp.ptr)
+        return (do.download((T, self.D), np.float32), di.download((T, self.top_k), np.int32),
+                dp.download((T, self.top_k), np.float32))
+
+    def block_forward(self, x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+        x = _f32(x)
+        dx = DeviceBuffer.from_array(x)
+        do = DeviceBuffer(x.nbytes)
+        check(lib().moe_block_forward(self.h, dx.ptr, x.shape[0], do.ptr, eps), "moe_block_forward")
+        return do.download(x.shape, np.float32)
+
+    def debug(self, T):
+        lg, hh, yy = _P(), _P(), _P()
+        check(lib().moe_layer_debug_buffers(self.h, ctypes.byref(lg), ctypes.byref(hh),
+                                            ctypes.byref(yy)))
+        out = {}
+        for name, ptr, shape in (("logits", lg.value, (T, self.E)),
+                                 ("h", hh.value, (T * self.top_k, self.d_ff)),
+                                 ("y", yy.value, (T * self.top_k, self.D))):
+            a = np.empty(shape, np.float32)
+            check(lib().moe_memcpy_d2h(a.ctypes.data, ptr, a.nbytes))
+            out[name] = a
+        return out
+
+    def close(self):
+        if self.h:
+            check(lib().moe_layer_destroy(self.h), "moe_layer_destroy")
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and _lib is not None:
+                _lib.moe_layer_destroy(self.h)
         except Exception:
             pass

@@ -1,0 +1,157 @@
+"""GPU parity of the MoE block (test_model_trace.c:460-517) through the C ABI.
+
+Bar: bit-exact outputs, top-k indices and gates.  The router sums in the
+reference's order, the expert dots are exact integers, expf matches glibc and
+every fp32 step is a separately rounded IEEE operation, so nothing is left to
+tolerance.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def random_experts(dtype, E, D, dff, seed):
+    """Fast synthetic experts: uniform weight bytes, small normal scales."""
+    rg = D if dtype == 2 else D // 2
+    rd = dff if dtype == 2 else dff // 2
+
+    def qbytes(n, s):
+        u = O.uniform_u32(n, s)
+        if dtype == 2:
+            return ((u % 255).astype(np.int64) - 127).astype(np.int8)
+        return (u & 0xFF).astype(np.uint8)
+
+    gq = qbytes(E * dff * rg, seed).reshape(E, dff, rg)
+    uq = qbytes(E * dff * rg, seed + 1).reshape(E, dff, rg)
+    dq = qbytes(E * D * rd, seed + 2).reshape(E, D, rd)
+    gs = np.abs(O.normal(E * dff, seed + 3, 0.0, 2e-4)).reshape(E, dff)
+    us = np.abs(O.normal(E * dff, seed + 4, 0.0, 2e-4)).reshape(E, dff)
+    ds = np.abs(O.normal(E * D, seed + 5, 0.0, 2e-4)).reshape(E, D)
+    return O.ExpertSet(dtype, gq, gs, uq, us, dq, ds, D, dff)
+
+
+def make_layer(moehip, dtype, ex, rw, rb=None, rms2=None, top_k=8):
+    return moehip.MoeLayer.from_arrays(dtype, rw, rb, ex.gq, ex.gs, ex.uq, ex.us, ex.dq, ex.ds,
+                                       rms2_w=rms2, top_k=top_k)
+
+
+@pytest.mark.parametrize("tag", ["q8", "q4"])
+def test_golden_small_layers(moehip, tag):
+    with np.load(os.path.join(GOLD, "ref_small.npz")) as z:
+        pre = f"layer_{tag}_"
+        dtype, T, D, dff, E = (int(v) for v in z[pre + "dims"])
+        ex = O.ExpertSet(dtype, z[pre + "gq"], z[pre + "gs"], z[pre + "uq"], z[pre + "us"],
+                         z[pre + "dq"], z[pre + "ds"], D, dff)
+        x, rw, rms2, want = z[pre + "x"], z[pre + "rw"], z[pre + "rms2"], z[pre + "out"]
+        rb = z[pre + "rb"] if (pre + "rb") in z.files else None
+    layer = make_layer(moehip, dtype, ex, rw, rb, rms2)
+    got = layer.block_forward(x)
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("tag", ["layer_q8_T4", "layer_q4_T2"])
+def test_config_layers_vs_reference_digest(moehip, tag):
+    with open(os.path.join(GOLD, "ref_config.json")) as f:
+        c = next(c for c in json.load(f)["cases"] if c["tag"] == tag)
+    print("case", tag, flush=True)
+    ex = O.make_experts(c["dtype"], c["E"], c["D"], c["d_ff"], c["seed"], c["std_w"])
+    assert sha(ex.gq) == c["sha_gq"]
+    T, D = c["T"], c["D"]
+    x = O.normal(T * D, c["seed"] + 1, 0.0, 1.0).reshape(T, D)
+    rw = O.normal(c["E"] * D, c["seed"] + 2, 0.0, c["std_w"]).reshape(c["E"], D)
+    layer = make_layer(moehip, c["dtype"], ex, rw, None, np.ones(D, np.float32))
+    out = layer.block_forward(x)
+    assert sha(out) == c["sha_out"]
+
+
+CASES = [  # dtype, T, E, D, d_ff, bias, resid
+    (2, 1, 128, 2048, 768, False, True),
+    (2, 4, 128, 2048, 768, True, True),
+    (2, 16, 128, 2048, 768, False, False),
+    (3, 1, 128, 2048, 768, False, True),
+    (3, 5, 128, 2048, 768, True, True),
+    (3, 16, 128, 2048, 768, False, True),
+    (2, 37, 64, 1024, 512, True, True),
+    (3, 9, 32, 512, 384, False, True),
+    (2, 3, 16, 96, 64, False, True),     # generic (untiled) expert rows
+]
+
+
+@pytest.mark.parametrize("dtype,T,E,D,dff,bias,resid", CASES)
+def test_layer_vs_oracle(moehip, dtype, T, E, D, dff, bias, resid):
+    seed = 7000 + dtype * 100 + T
+    print("case", dtype, T, E, D, dff, bias, resid, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    rb = O.normal(E, seed + 11, 0.0, 0.05) if bias else None
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    xr = O.normal(T * D, seed + 13, 0.0, 1.0).reshape(T, D) if resid else None
+    want, widx, wp, wlog = O.moe_block(xn, xr, rw, rb, ex)
+    layer = make_layer(moehip, dtype, ex, rw, rb)
+    got, idx, p = layer.forward(xn, xr)
+    dbg = layer.debug(T)
+    np.testing.assert_array_equal(bits(dbg["logits"]), bits(wlog))
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+def test_router_ties_and_nan(moehip):
+    """Equal logits keep the lower expert first; NaN logits are never chosen."""
+    dtype, T, E, D, dff = 2, 3, 32, 256, 128
+    ex = random_experts(dtype, E, D, dff, 99)
+    rw = O.normal(E * D, 98, 0.0, 0.02).reshape(E, D)
+    rw[5] = rw[17]          # experts 5 and 17 tie exactly
+    rw[9] = rw[17]
+    rw[3, 0] = np.nan       # expert 3's logit is NaN for every token
+    xn = O.normal(T * D, 97, 0.0, 1.0).reshape(T, D)
+    xn[:, :] += rw[17] * 50  # push the tied experts to the top
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    layer = make_layer(moehip, dtype, ex, rw)
+    got, idx, p = layer.forward(xn, xn)
+    assert 3 not in idx
+    np.testing.assert_array_equal(idx, widx)
+    assert list(idx[0][:3]) == [5, 9, 17]
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+def test_rmsnorm_dev(moehip):
+    for T, D in ((3, 2048), (2, 100)):
+        x = O.normal(T * D, 5 + D, 0.0, 2.0).reshape(T, D)
+        w = O.normal(D, 6 + D, 1.0, 0.1)
+        dx, dw, dy = (moehip.DeviceBuffer.from_array(x), moehip.DeviceBuffer.from_array(w),
+                      moehip.DeviceBuffer(x.nbytes))
+        moehip.check(moehip.lib().moe_rmsnorm_dev(dx.ptr, dw.ptr, dy.ptr, T, D, 1e-6))
+        np.testing.assert_array_equal(bits(dy.download((T, D), np.float32)), bits(O.rmsnorm(x, w)))
+
+
+def test_repeated_forward_and_growing_T(moehip):
+    """Scratch reuse: T grows and shrinks between calls; results stay exact."""
+    dtype, E, D, dff = 3, 64, 1024, 512
+    ex = random_experts(dtype, E, D, dff, 55)
+    rw = O.normal(E * D, 56, 0.0, 0.02).reshape(E, D)
+    layer = make_layer(moehip, dtype, ex, rw)
+    for T in (2, 11, 1, 11):
+        xn = O.normal(T * D, 60 + T, 0.0, 1.0).reshape(T, D)
+        want, widx, _, _ = O.moe_block(xn, xn, rw, None, ex)
+        got, idx, _ = layer.forward(xn, xn)
+        np.testing.assert_array_equal(idx, widx)
+        np.testing.assert_array_equal(bits(got), bits(want))
