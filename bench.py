@@ -184,6 +184,94 @@ def run_gemv(args, dtype, shapes, workload):
     return out
 
 
+def expert_bytes(dtype: int, D: int, dff: int) -> int:
+    """One expert's gate + up + down weights and scales."""
+    rb_g = D if dtype == 2 else D // 2
+    rb_d = dff if dtype == 2 else dff // 2
+    return 2 * dff * rb_g + D * rb_d + 4 * (2 * dff + D)
+
+
+class LayerPool:
+    """`n` device-resident MoE layers (Qwen3-30B-A3B shapes) with weights
+    generated and quantized on the device."""
+
+    def __init__(self, dtype, n, E=128, D=2048, dff=768, seed=77):
+        self.dtype, self.E, self.D, self.dff = dtype, E, D, dff
+        L = M.lib()
+        rb_g = D if dtype == 2 else D // 2
+        rb_d = dff if dtype == 2 else dff // 2
+        tmp = M.DeviceBuffer(E * max(dff * D, D * dff) * 4)
+        self.layers = []
+        for i in range(n):
+            bufs = {"rw": M.DeviceBuffer(E * D * 4), "gq": M.DeviceBuffer(E * dff * rb_g),
+                    "uq": M.DeviceBuffer(E * dff * rb_g), "dq": M.DeviceBuffer(E * D * rb_d),
+                    "gs": M.DeviceBuffer(E * dff * 4), "us": M.DeviceBuffer(E * dff * 4),
+                    "ds": M.DeviceBuffer(E * D * 4)}
+            sd = seed + 1000 * i
+            M.check(L.moe_fill_normal_dev(bufs["rw"].ptr, E * D, sd, 0.0, 0.02))
+            for name, rows, K in (("g", dff, D), ("u", dff, D), ("d", D, dff)):
+                sd += 1
+                M.check(L.moe_fill_normal_dev(tmp.ptr, E * rows * K, sd, 0.0, 0.02))
+                M.check(L.moe_quantize_rows_dev(dtype, tmp.ptr, E * rows, K, bufs[name + "q"].ptr,
+                                                bufs[name + "s"].ptr))
+            h = ctypes.c_void_p()
+            M.check(L.moe_layer_create_raw(dtype, D, dff, E, 8, bufs["rw"].ptr, None, None,
+                                           bufs["gq"].ptr, bufs["gs"].ptr, bufs["uq"].ptr,
+                                           bufs["us"].ptr, bufs["dq"].ptr, bufs["ds"].ptr, 1,
+                                           ctypes.byref(h)), "layer_create")
+            for b in bufs.values():
+                b.free()
+            self.layers.append(M.MoeLayer(h.value, dtype, D, dff, E, 8))
+        tmp.free()
+        M.synchronize()
+
+
+def run_decode(dtype, Ts, n_layers, steps, warmup):
+    """One MoE layer forward per step (configs[2]: Q8 experts, T tokens,
+    x ~ N(0,1)); layers and inputs rotate so expert weights stream from HBM."""
+    M.init(0)
+    pool = LayerPool(dtype, n_layers)
+    D = pool.D
+    res = []
+    for T in Ts:
+        n_in = 8
+        xs = M.DeviceBuffer(n_in * T * D * 4)
+        M.check(M.lib().moe_fill_normal_dev(xs.ptr, n_in * T * D, 4242 + T, 0.0, 1.0))
+        out = M.DeviceBuffer(T * D * 4)
+        idx = M.DeviceBuffer(steps * T * 8 * 4)
+        for i in range(warmup):
+            lay = pool.layers[i % n_layers]
+            lay.forward_dev(xs.ptr + (i % n_in) * T * D * 4, xs.ptr + (i % n_in) * T * D * 4, T,
+                            out.ptr)
+        M.synchronize()
+        ev = [(M.Event(), M.Event()) for _ in range(steps)]
+        t0, t1 = M.Event(), M.Event()
+        t0.record()
+        for i in range(steps):
+            lay = pool.layers[i % n_layers]
+            x = xs.ptr + (i % n_in) * T * D * 4
+            ev[i][0].record()
+            lay.forward_dev(x, x, T, out.ptr, idx.ptr + i * T * 8 * 4)
+            ev[i][1].record()
+        t1.record()
+        M.synchronize()
+        per = [a.elapsed_ms(b) for a, b in ev]
+        total_ms = t0.elapsed_ms(t1)
+        ids = idx.download((steps, T * 8), np.int32)
+        U = float(np.mean([len(set(r.tolist()) - {-1}) for r in ids]))
+        algo = 1048576 + U * expert_bytes(dtype, D, pool.dff) + 2 * T * D * 4
+        med = float(np.median(per))
+        res.append({"T": T, "layers_in_pool": n_layers, "steps": steps,
+                    "us_per_layer_median": round(med * 1e3, 2),
+                    "us_per_layer_mean": round(total_ms / steps * 1e3, 2),
+                    "tokens_per_s_one_layer": round(T / (med * 1e-3), 1),
+                    "distinct_experts_avg": U, "algorithmic_bytes": int(algo),
+                    "GBs": round(algo / (med * 1e-3) / 1e9, 1),
+                    "pct_hbm_peak": round(100 * algo / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)})
+        log(f"[bench] decode T={T}: {res[-1]}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,6 +281,9 @@ def main():
     ap.add_argument("--pool-gib", type=float, default=1.0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode", default="1,4,16",
+                    help="also time one Q8 MoE decode layer at these T (configs[2]); '' to skip")
+    ap.add_argument("--decode-layers", type=int, default=6)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the expert path on a single MI355X "
@@ -205,6 +296,10 @@ def main():
     else:
         out = run_gemv(args, 2, [(768, 2048)],
                        "q8_rowwise_gemv_batch1 gate[768x2048] (BASELINE configs[0])")
+    if args.decode:
+        Ts = [int(t) for t in args.decode.split(",") if t]
+        out["moe_decode_q8"] = run_decode(2, Ts, args.decode_layers, max(args.steps, 20),
+                                          args.warmup)
     print(json.dumps(out), flush=True)
 
 

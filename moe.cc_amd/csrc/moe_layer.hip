@@ -1,26 +1,28 @@
 // moe_layer.hip - the MoE block of one Qwen3-MoE layer on gfx950
 // (test_model_trace.c:460-517), bit-identical to the reference.
 //
-// Launch sequence of one forward (T tokens):
+// Launch sequence of one forward (T tokens), three kernels:
 //   [rmsnorm]   x_norm = rmsnorm(x, rms2_w)          (block forward only; :461)
 //   router      logits[t,e] = sum_k x_norm[t,k] * Wr[e,k], k ascending,
-//               separate roundings (:465 -> :213-227), + bias (:466-468);
-//               top-k by the insertion rule (:480 -> :275-288), softmax over
-//               the selected logits (:482-487); packs x_norm[t] for the
-//               expert GEMVs.  One block of 1024 threads per token.
-//   tasks       groups the T*k (token, rank) pairs by expert, ascending
-//               (token, rank) inside an expert: one task per routed expert,
-//               so an expert's weights are read once for all its tokens.
-//   gate_up     per task and row chunk: g = Q(x Wg), u = Q(x Wu), both exact
-//               integer dots; h = (g / (1 + expf(-g))) * u  (:496-501)
-//   pack_h      packs every h row for the down GEMV
-//   down        per task and row chunk: y = Q(h Wd)  (:502-503)
-//   combine     out[t] = x_resid[t] + (((0 + p0 y0) + p1 y1) + ...), ranks in
-//               order, each product and sum rounded on its own (:513, :517)
+//               separate roundings (:465 -> :213-227), + bias (:466-468).
+//               Blocks of 8 experts stage their rows in LDS; the last block
+//               to finish does top-k by the insertion rule (:480 -> :275-288)
+//               and the softmax over the selected logits (:482-487), and
+//               packs x_norm for the expert GEMVs.
+//   gate_up     per (token, rank) pair and row chunk: g = Q(x Wg), u = Q(x Wu),
+//               exact integer dots; h = (g / (1 + expf(-g))) * u (:496-501),
+//               written straight into the pair's packed table for down.
+//   down        per token and row chunk, one wave per rank: y_j = Q(h_j Wd_j)
+//               (:502-503) into LDS, then out = x_resid + (((0 + p0 y0) +
+//               p1 y1) + ...) in rank order, each product and sum rounded on
+//               its own (:513, :517).
+// Cross-block hand-offs go through kernel boundaries (and one last-block
+// step in the 16-block router), never through per-block device fences.
 // The router's sequential sum runs as one add chain per (token, expert):
 // 8 lanes hold 32 consecutive products and lane 0 of the group adds them in
 // k order through DPP row shifts (v_add_f32_dpp), so a wave carries 8 chains.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <type_traits>
@@ -49,185 +51,294 @@ struct LayerDev {
   uint8_t* xtab = nullptr;   // [T] packed x_norm rows
   uint8_t* htab = nullptr;   // [T*topk] packed h rows
   float* h = nullptr;        // [T*topk][dff]
-  float* y = nullptr;        // [T*topk][D]
   float* xn = nullptr;       // [T][D] normed input (block forward)
-  int* tasks = nullptr;      // [0]=U, expert[E], start[E], count[E], pairs[T*topk]
+  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables
+  uint32_t* hpart = nullptr; // [T*topk][gate/up chunks][2] partial headers of the h tables
+  // completion counter of the router's last-block step, zero between launches
+  unsigned* counters = nullptr;
 };
 
 namespace {
 
-constexpr int kRouterThreads = 1024;
+constexpr int kRouterThreads = 512;            // 8 waves
 constexpr int kRouterWaves = kRouterThreads / kWave;
+constexpr int kRouterExperts = 8;              // experts per router block
+constexpr int kRouterTokens = 8;               // tokens per router block: 64 chains = 1 wave
 constexpr int kMaxTopK = 32;
+constexpr size_t kMaxLds = 160 * 1024 - 2048;  // dynamic LDS budget (static LDS fits in the rest)
 
-template <int J>
-__device__ __forceinline__ float shl8(float v) {
-  if constexpr (J == 0) return v;
-  else return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + J, 0xF, 0xF, true));
-}
-
-// acc + p_m(lane+J), m = 0..3, in that order
-template <int J>
-__device__ __forceinline__ float chain4(float acc, float p0, float p1, float p2, float p3) {
-  acc = acc + shl8<J>(p0);
-  acc = acc + shl8<J>(p1);
-  acc = acc + shl8<J>(p2);
-  acc = acc + shl8<J>(p3);
-  return acc;
-}
-
-// Sequential fp32 dot of x[0..D) with row w (test_model_trace.c:221-222):
-// lanes 8g..8g+7 of a wave cooperate on one row; the result is valid in lane
-// 8g.  Requires D % 32 == 0 and 16-byte aligned x and w.
-__device__ __forceinline__ float seq_dot_group8(const float* __restrict__ x,
-                                                const float* __restrict__ w, int D, bool live) {
-  const int j = threadIdx.x % 8;
+// Sequential fp32 dot of x[0..D) with w, k ascending, each product and each
+// sum rounded on its own (test_model_trace.c:221-222), one chain per lane
+// with the products in the lane's own registers (a dependent v_add_f32 every
+// 8 clocks).  x and w point into LDS, 16-byte aligned, D % 16 == 0, and both
+// rows are readable (padding) up to index D + 15, so the next 16 values are
+// always prefetched without a branch.
+constexpr int kRowPad = 16;
+__device__ __forceinline__ float seq_dot_lane(const float* x, const float* w, int D) {
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
   float acc = 0.0f;
-  float4 wa = live ? *reinterpret_cast<const float4*>(w + 4 * j) : make_float4(0, 0, 0, 0);
-  float4 xa = *reinterpret_cast<const float4*>(x + 4 * j);
-  for (int k0 = 0; k0 < D; k0 += 32) {
-    float4 wn = make_float4(0, 0, 0, 0), xn = make_float4(0, 0, 0, 0);
-    if (k0 + 32 < D) {
-      if (live) wn = *reinterpret_cast<const float4*>(w + k0 + 32 + 4 * j);
-      xn = *reinterpret_cast<const float4*>(x + k0 + 32 + 4 * j);
+  int k4 = 0;
+  // 64 columns per step: all 32 LDS reads are issued first, so their latency
+  // is paid once per 64 dependent adds
+  for (; k4 + 16 <= D / 4; k4 += 16) {
+    float4 xv[16], wv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { xv[i] = x4[k4 + i]; wv[i] = w4[k4 + i]; }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p0 = xv[i].x * wv[i].x, p1 = xv[i].y * wv[i].y;
+      const float p2 = xv[i].z * wv[i].z, p3 = xv[i].w * wv[i].w;
+      acc = acc + p0;
+      acc = acc + p1;
+      acc = acc + p2;
+      acc = acc + p3;
     }
-    const float p0 = xa.x * wa.x, p1 = xa.y * wa.y, p2 = xa.z * wa.z, p3 = xa.w * wa.w;
-    acc = chain4<0>(acc, p0, p1, p2, p3);
-    acc = chain4<1>(acc, p0, p1, p2, p3);
-    acc = chain4<2>(acc, p0, p1, p2, p3);
-    acc = chain4<3>(acc, p0, p1, p2, p3);
-    acc = chain4<4>(acc, p0, p1, p2, p3);
-    acc = chain4<5>(acc, p0, p1, p2, p3);
-    acc = chain4<6>(acc, p0, p1, p2, p3);
-    acc = chain4<7>(acc, p0, p1, p2, p3);
-    wa = wn;
-    xa = xn;
+  }
+  for (; k4 < D / 4; ++k4) {
+    const float4 xv = x4[k4], wv = w4[k4];
+    const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
+    acc = acc + p0;
+    acc = acc + p1;
+    acc = acc + p2;
+    acc = acc + p3;
   }
   return acc;
 }
 
-template <bool Q4>
-__global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
-    const float* __restrict__ xn, int D, int E, int topk, const float* __restrict__ Wr,
-    const float* __restrict__ rb, float* __restrict__ logits_out, int* __restrict__ idx_out,
-    float* __restrict__ p_out, uint8_t* __restrict__ xtab, size_t tab_bytes, int fast) {
-  extern __shared__ float lds[];
-  float* lg = lds;                                   // [E]
-  int* rank = reinterpret_cast<int*>(lds + E);       // [E]
-  __shared__ int slot_idx[kMaxTopK];
-  __shared__ float slot_val[kMaxTopK];
-  __shared__ float slot_exp[kMaxTopK];
-  __shared__ float inv_sum;
-  __shared__ int scratch[2];
-  const int t = blockIdx.x;
-  const float* x = xn + (size_t)t * D;
-  const int tid = threadIdx.x;
-
-  // 1. logits
-  if (fast) {
-    const int wave = tid / kWave, g = (tid % kWave) / 8;
-    for (int e0 = 0; e0 < E; e0 += kRouterWaves * 8) {
-      const int e = e0 + wave * 8 + g;
-      const bool live = e < E;
-      const float acc = seq_dot_group8(x, Wr + (size_t)(live ? e : 0) * D, D, live);
-      if (live && (tid % 8) == 0) lg[e] = rb ? acc + rb[e] : acc;
-    }
-  } else {
-    for (int e = tid; e < E; e += blockDim.x) {
-      const float* w = Wr + (size_t)e * D;
-      float acc = 0.0f;
-      for (int k = 0; k < D; ++k) {
-        const float pk = x[k] * w[k];
-        acc = acc + pk;
-      }
-      lg[e] = rb ? acc + rb[e] : acc;
-    }
-  }
-  for (int e = tid; e < E; e += blockDim.x) rank[e] = 0;
-  if (tid < topk) { slot_idx[tid] = -1; slot_val[tid] = -__builtin_inff(); }
-  __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) logits_out[(size_t)t * E + e] = lg[e];
-
-  // 2. top-k: rank of e = #{c : v_c > v_e} + #{c < e : v_c == v_e}; NaN and
-  //    -inf are never selected (insertion rule of test_model_trace.c:275-288)
-  const int tpe = E <= (int)blockDim.x ? (int)blockDim.x / E : 1;
-  for (int i = tid; i < tpe * E; i += blockDim.x) {
-    const int e = i / tpe, part = i % tpe;
-    const float v = lg[e];
-    int cnt = 0;
-    for (int c = part; c < E; c += tpe) {
-      const float vc = lg[c];
-      cnt += (vc > v) || (vc == v && c < e);
-    }
-    atomicAdd(&rank[e], cnt);
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) {
-    const float v = lg[e];
-    const int r = rank[e];
-    if (v > -__builtin_inff() && r < topk) { slot_idx[r] = e; slot_val[r] = v; }
-  }
-  __syncthreads();
-
-  // 3. softmax over the selected logits (:482-487)
-  if (tid < topk) {
-    float mx = slot_val[0];
-    for (int i = 1; i < topk; ++i) if (slot_val[i] > mx) mx = slot_val[i];
-    slot_exp[tid] = expf_glibc(slot_val[tid] - mx);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float sum = 0.0f;
-    for (int i = 0; i < topk; ++i) sum = sum + slot_exp[i];
-    inv_sum = 1.0f / (sum + 1e-9f);
-  }
-  __syncthreads();
-  if (tid < topk) {
-    idx_out[(size_t)t * topk + tid] = slot_idx[tid];
-    p_out[(size_t)t * topk + tid] = slot_exp[tid] * inv_sum;
-  }
-
-  // 4. packed activations of x_norm[t] for the gate/up GEMVs
-  pack_act_row<Q4>(x, D, xtab + (size_t)t * tab_bytes, scratch);
-}
-
-// Groups the (token, rank) pairs by expert: task u = u-th routed expert in
-// ascending id; its pairs in ascending pair id = t*topk + j.
-__global__ __launch_bounds__(256) void build_tasks_kernel(const int* __restrict__ idx, int npairs,
-                                                          int E, int* __restrict__ tasks) {
-  extern __shared__ int cnt[];   // [E] counts then [E] starts
-  int* start = cnt + E;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int c = 0;
-    for (int q = 0; q < npairs; ++q) c += idx[q] == e;
-    cnt[e] = c;
-  }
+// Block-level "am I the last block to finish this step" test: every thread
+// publishes its writes (agent-scope fence), one thread counts the block in,
+// and the block that brings the count to `total` gets true (after an acquire
+// fence, so it sees every other block's writes) and resets the counter.
+// Used only by the 16-block router: a device fence per block is expensive.
+__device__ __forceinline__ bool last_block_in(unsigned* counter, unsigned total) {
+  __shared__ int last;
+  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
-    int u = 0, s = 0;
-    for (int e = 0; e < E; ++e) {
-      start[e] = s;
-      if (cnt[e] > 0) {
-        tasks[1 + u] = e;
-        tasks[1 + E + u] = s;
-        tasks[1 + 2 * E + u] = cnt[e];
-        ++u;
-      }
-      s += cnt[e];
-    }
-    tasks[0] = u;
+    const unsigned prev = atomicAdd(counter, 1u);
+    last = prev == total - 1;
+    if (last) *counter = 0u;
   }
   __syncthreads();
-  int* pairs = tasks + 1 + 3 * E;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    if (cnt[e] == 0) continue;
-    int o = start[e];
-    for (int q = 0; q < npairs; ++q)
-      if (idx[q] == e) pairs[o++] = q;
+  if (!last) return false;
+  __threadfence();
+  return true;
+}
+
+struct RouterArgs {
+  const float* xn;
+  int T, D, E, topk;
+  const float* W;
+  const float* b;
+  float* logits;
+  int* idx;
+  float* p;
+  int* idx_user;
+  float* p_user;
+  uint8_t* xtab;         // packed x_norm rows
+  size_t tab_bytes;
+  uint32_t* xpart;       // [T][gridDim.x][2] partial (limbs, sum) of each column slice
+  unsigned* counter;
+  int tb;                // tokens per block
+  int staged;            // rows staged in LDS, one chain per lane
+  int cols;              // x columns packed per block (multiple of 8)
+};
+
+// (v, i) beats (w, j): valid and larger, or equal with the lower index.
+__device__ __forceinline__ bool beats(float v, int i, float w, int j) {
+  if (i < 0) return false;
+  if (j < 0) return true;
+  return v > w || (v == w && i < j);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step_dpp(float& bv, int& bi) {
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bv), CTRL, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_update_dpp(-1, bi, CTRL, 0xF, 0xF, false);
+  if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+}
+
+// Wave-wide arg-max of (value, index) pairs under `beats`; every lane ends
+// with the winner.  DPP within rows of 16, then two cross-row exchanges.
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+  argmax_step_dpp<0xB1>(bv, bi);    // quad_perm [1,0,3,2]
+  argmax_step_dpp<0x4E>(bv, bi);    // quad_perm [2,3,0,1]
+  argmax_step_dpp<0x141>(bv, bi);   // row_half_mirror
+  argmax_step_dpp<0x140>(bv, bi);   // row_mirror
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
 }
 
-constexpr int kMTok = 4;   // token slots per block pass in the expert kernels
+// Runs in the last router block.  Headers of the packed x rows; then, one
+// wave per token, top-k by repeated arg-max (the largest remaining value,
+// lowest index among equals: the result of the insertion rule of
+// test_model_trace.c:275-288; NaN and -inf never selected) and the softmax
+// over the selected logits (:482-487).  C = candidates per lane (E <= 64*C).
+template <bool Q4, int C>
+__device__ void router_finish(const RouterArgs& a) {
+  __shared__ int sidx[kRouterWaves][kMaxTopK];
+  __shared__ float sval[kRouterWaves][kMaxTopK];
+  __shared__ float sexp[kRouterWaves][kMaxTopK];
+  const int tid = threadIdx.x, E = a.E, K = a.topk;
+  const int nbx = gridDim.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  // headers of the packed x rows: one wave per token, lanes over the partials
+  for (int t = wave; t < a.T; t += kRouterWaves) {
+    int nl = 1;
+    uint32_t sum = 0;
+    for (int bx = lane; bx < nbx; bx += kWave) {
+      const uint32_t* pp = a.xpart + ((size_t)t * nbx + bx) * 2;
+      nl = (int)pp[0] > nl ? (int)pp[0] : nl;
+      sum += pp[1];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int on = __shfl_xor(nl, off, kWave);
+      nl = on > nl ? on : nl;
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    }
+    if (lane == 0) {
+      uint32_t* hh = reinterpret_cast<uint32_t*>(a.xtab + (size_t)t * a.tab_bytes);
+      hh[0] = (uint32_t)nl;
+      hh[1] = sum;
+    }
+  }
+  for (int t = wave; t < a.T; t += kRouterWaves) {
+    float v[C];
+    bool live[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int e = lane + kWave * c;
+      v[c] = e < E ? a.logits[(size_t)t * E + e] : -__builtin_inff();
+      live[c] = e < E && v[c] > -__builtin_inff();   // false for NaN and -inf
+    }
+    for (int r = 0; r < K; ++r) {
+      float bv = -__builtin_inff();
+      int bi = -1;
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (live[c] && beats(v[c], lane + kWave * c, bv, bi)) { bv = v[c]; bi = lane + kWave * c; }
+      wave_argmax(bv, bi);
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (bi == lane + kWave * c) live[c] = false;
+      if (lane == 0) { sidx[wave][r] = bi; sval[wave][r] = bi >= 0 ? bv : -__builtin_inff(); }
+    }
+    __threadfence_block();
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) {
+      float mx = sval[wave][0];
+      for (int i = 1; i < K; ++i) if (sval[wave][i] > mx) mx = sval[wave][i];
+      sexp[wave][lane] = expf_glibc(sval[wave][lane] - mx);
+    }
+    __threadfence_block();
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int i = 0; i < K; ++i) sum = sum + sexp[wave][i];
+    const float inv = 1.0f / (sum + 1e-9f);
+    if (lane < K) {
+      const size_t q = (size_t)t * K + lane;
+      const float pv = sexp[wave][lane] * inv;
+      a.idx[q] = sidx[wave][lane];
+      a.p[q] = pv;
+      if (a.idx_user) a.idx_user[q] = sidx[wave][lane];
+      if (a.p_user) a.p_user[q] = pv;
+    }
+    __threadfence_block();
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Router logits (test_model_trace.c:465-468).  Block (bx, by) = 8 experts x
+// up to 8 tokens: the experts' rows and the tokens' x are staged in LDS
+// (rows padded by 16 bytes against bank conflicts); wave 0 runs the 64
+// sequential chains, one per lane, while the other waves pack column slice
+// bx of the tokens' x for the expert GEMVs.  The last block to finish
+// selects the experts (router_finish).
+template <bool Q4>
+__global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
+  extern __shared__ float lds[];
+  __shared__ int red_nl[kRouterTokens];
+  __shared__ unsigned red_sum[kRouterTokens];
+  const int tid = threadIdx.x, wave = tid / kWave;
+  const int e0 = blockIdx.x * kRouterExperts;
+  const int t0 = blockIdx.y * a.tb;
+  const int ntb = a.T - t0 < a.tb ? a.T - t0 : a.tb;
+  const int D = a.D, E = a.E, Dp = D + kRowPad;
+  float* Wl = lds;                           // [8][Dp]
+  float* Xl = lds + kRouterExperts * Dp;     // [tb][Dp]
+  if (a.staged) {
+    // per column block of blockDim float4: the 8 weight rows and the tokens'
+    // x rows are loaded into registers first, then stored (one memory latency)
+    const int d4 = D / 4, p4 = Dp / 4;
+    for (int c = tid; c < d4; c += blockDim.x) {
+      float4 vw[kRouterExperts], vx[kRouterTokens];
+#pragma unroll
+      for (int r = 0; r < kRouterExperts; ++r)
+        vw[r] = e0 + r < E ? reinterpret_cast<const float4*>(a.W + (size_t)(e0 + r) * D)[c]
+                           : make_float4(0, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < kRouterTokens; ++r)
+        vx[r] = reinterpret_cast<const float4*>(a.xn + (size_t)(t0 + (r < ntb ? r : 0)) * D)[c];
+#pragma unroll
+      for (int r = 0; r < kRouterExperts; ++r) reinterpret_cast<float4*>(Wl)[r * p4 + c] = vw[r];
+#pragma unroll
+      for (int r = 0; r < kRouterTokens; ++r)
+        if (r < ntb) reinterpret_cast<float4*>(Xl)[r * p4 + c] = vx[r];
+    }
+  }
+  if (tid < kRouterTokens) { red_nl[tid] = 1; red_sum[tid] = 0; }
+  __syncthreads();
+  if (wave == 0) {
+    const int tl = tid / kRouterExperts, g = tid % kRouterExperts;
+    const int t = t0 + tl, e = e0 + g;
+    if (tl < ntb && e < E) {
+      float acc;
+      if (a.staged) {
+        acc = seq_dot_lane(Xl + (size_t)tl * Dp, Wl + (size_t)g * Dp, D);
+      } else {
+        const float* x = a.xn + (size_t)t * D;
+        const float* w = a.W + (size_t)e * D;
+        acc = 0.0f;
+        for (int k = 0; k < D; ++k) {
+          const float pk = x[k] * w[k];
+          acc = acc + pk;
+        }
+      }
+      a.logits[(size_t)t * E + e] = a.b ? acc + a.b[e] : acc;
+    }
+  } else {
+    const int c0 = blockIdx.x * a.cols;
+    const int c1 = c0 + a.cols < D ? c0 + a.cols : D;
+    for (int tl = 0; tl < ntb; ++tl) {
+      const float* x = a.staged ? Xl + (size_t)tl * Dp : a.xn + (size_t)(t0 + tl) * D;
+      int nl;
+      uint32_t sum;
+      pack_act_cols<Q4>(x, D, c0, c1 > c0 ? c1 : c0, a.xtab + (size_t)(t0 + tl) * a.tab_bytes,
+                        tid - kWave, blockDim.x - kWave, nl, sum);
+      atomicMax(&red_nl[tl], nl);
+      atomicAdd(&red_sum[tl], sum);
+    }
+  }
+  __syncthreads();
+  if (tid < ntb) {
+    uint32_t* pp = a.xpart + ((size_t)(t0 + tid) * gridDim.x + blockIdx.x) * 2;
+    pp[0] = (uint32_t)red_nl[tid];
+    pp[1] = red_sum[tid];
+  }
+  if (!last_block_in(a.counter, gridDim.x * gridDim.y)) return;
+  if (E <= 64) router_finish<Q4, 1>(a);
+  else if (E <= 128) router_finish<Q4, 2>(a);
+  else if (E <= 256) router_finish<Q4, 4>(a);
+  else router_finish<Q4, 16>(a);
+}
+
+constexpr int kMTok = 4;   // token slots per block pass in the GEMV kernels
 
 // Marks the untiled expert path: one wave per row, int32 arithmetic on the
 // fp32 activations (any row size; used for small or irregular layers).
@@ -235,184 +346,173 @@ struct GenericGeom {
   static constexpr int WR = 1;
 };
 
-// Epilogue of gate/up: h[pair, row] = silu(g) * u
-struct GateUpEpiMaker {
+// Epilogue of gate/up: hb[row - r0] = silu(g) * u  (LDS)
+struct GateUpEpi {
   const float* gs;
   const float* us;
-  float* h;
-  const int* pairs;   // this task's pairs
-  int n, dff;
+  float* hb;
+  int r0;
   float div;
-  template <int MTI>
-  struct Epi {
-    const float* gs;
-    const float* us;
-    float* h;
-    const int* pairs;
-    int n, dff;
-    float div;
-    int t0;
-    template <class Tot>
-    __device__ void operator()(int row, const Tot& tot) const {
-      const float sg = gs[row], su = us[row];
-#pragma unroll
-      for (int t = 0; t < MTI; ++t) {
-        if (t0 + t >= n) break;
-        const float g = qdot_epilogue(tot[0][t], div, sg);
-        const float u = qdot_epilogue(tot[1][t], div, su);
-        h[(size_t)pairs[t0 + t] * dff + row] = silu_mul(g, u);
-      }
-    }
-  };
-  template <int MTI>
-  __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{gs, us, h, pairs, n, dff, div, t0}; }
+  template <class Tot>
+  __device__ void operator()(int row, const Tot& tot) const {
+    const float g = qdot_epilogue(tot[0][0], div, gs[row]);
+    const float u = qdot_epilogue(tot[1][0], div, us[row]);
+    hb[row - r0] = silu_mul(g, u);
+  }
 };
-
-// Epilogue of down: y[pair, row] = Q(h Wd)
-struct DownEpiMaker {
-  const float* ds;
-  float* y;
-  const int* pairs;
-  int n, D;
-  float div;
+struct GateUpEpiMaker {
+  GateUpEpi e;
   template <int MTI>
-  struct Epi {
-    const float* ds;
-    float* y;
-    const int* pairs;
-    int n, D;
-    float div;
-    int t0;
-    template <class Tot>
-    __device__ void operator()(int row, const Tot& tot) const {
-      const float sc = ds[row];
-#pragma unroll
-      for (int t = 0; t < MTI; ++t) {
-        if (t0 + t >= n) break;
-        y[(size_t)pairs[t0 + t] * D + row] = qdot_epilogue(tot[0][t], div, sc);
-      }
-    }
-  };
-  template <int MTI>
-  __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{ds, y, pairs, n, D, div, t0}; }
+  __device__ GateUpEpi at(int) const { return e; }
 };
 
 struct GateUpArgs {
   const uint8_t* gq; const float* gs; const uint8_t* uq; const float* us;
-  long long rb; int D, dff, E, topk;
-  const int* tasks; const uint8_t* xtab; size_t tab_bytes; const float* xn;
-  float* h; int rows_per_block;
+  long long rb; int D, dff, topk;
+  const int* idx; const uint8_t* xtab; size_t tab_bytes; const float* xn;
+  float* h; uint8_t* htab; size_t htab_bytes;
+  uint32_t* hpart;      // [pair][chunk][2] partial (limbs, sum) of each row chunk of h
+  int nchunks, rows_per_block;
 };
 
+// gate/up + SwiGLU for one (token, rank) pair and one row chunk:
+// h = (g / (1 + expf(-g))) * u with g, u exact (:496-501).  h is written as
+// fp32 and, packed, into its rows of the pair's table for the down GEMV; the
+// chunk's limb count and activation sum go to hpart (no atomics).  Row chunks
+// start at multiples of 8, so a chunk owns whole packed dwords.
 template <bool Q4, class G>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
-  const int u = blockIdx.y;
-  if (u >= a.tasks[0]) return;
-  const int e = a.tasks[1 + u], st = a.tasks[1 + a.E + u], n = a.tasks[1 + 2 * a.E + u];
-  const int* pairs = a.tasks + 1 + 3 * a.E + st;
+  extern __shared__ float hb[];   // [rows_per_block]
+  __shared__ int red_nl;
+  __shared__ unsigned red_sum;
+  const int q = blockIdx.y;
+  const int e = a.idx[q];
+  if (e < 0) return;
+  const int t = q / a.topk;
   const int r0 = blockIdx.x * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.dff ? r0 + a.rows_per_block : a.dff;
   const uint8_t* W[2] = {a.gq + (size_t)e * a.dff * a.rb, a.uq + (size_t)e * a.dff * a.rb};
-  for (int c0 = 0; c0 < n; c0 += kMTok) {
-    const int nt = n - c0 < kMTok ? n - c0 : kMTok;
-    const uint8_t* tabs[kMTok];
-    const float* xs[kMTok];
-#pragma unroll
-    for (int t = 0; t < kMTok; ++t) {
-      const int tok = pairs[c0 + (t < nt ? t : nt - 1)] / a.topk;
-      tabs[t] = a.xtab + (size_t)tok * a.tab_bytes;
-      xs[t] = a.xn + (size_t)tok * a.D;
-    }
-    GateUpEpiMaker mk{a.gs + (size_t)e * a.dff, a.us + (size_t)e * a.dff, a.h, pairs + c0, nt,
-                      a.dff, Q4 ? 7.0f : 127.0f};
-    if constexpr (std::is_same<G, GenericGeom>::value) {
-      for (int t = 0; t < nt; ++t) {
-        auto epi = mk.template at<1>(t);
-        generic_rows_fp32<Q4, 2>(W, a.rb, a.D, xs[t], r0, r1, epi);
-      }
-    } else {
-      stream_tokens<Q4, G, 2, kMTok>(W, a.rb, a.D, tabs, xs, nt, r0, r1, mk);
-    }
+  const uint8_t* tabs[1] = {a.xtab + (size_t)t * a.tab_bytes};
+  const float* xs[1] = {a.xn + (size_t)t * a.D};
+  GateUpEpiMaker mk{GateUpEpi{a.gs + (size_t)e * a.dff, a.us + (size_t)e * a.dff, hb, r0,
+                              Q4 ? 7.0f : 127.0f}};
+  if (threadIdx.x == 0) { red_nl = 1; red_sum = 0; }
+  if constexpr (std::is_same<G, GenericGeom>::value) {
+    auto epi = mk.e;
+    generic_rows_fp32<Q4, 2>(W, a.rb, a.D, xs[0], r0, r1, epi);
+  } else {
+    stream_tokens<Q4, G, 2, 1>(W, a.rb, a.D, tabs, xs, 1, r0, r1, mk);
   }
-}
-
-template <bool Q4>
-__global__ __launch_bounds__(256) void pack_h_kernel(const float* __restrict__ h, int dff,
-                                                     const int* __restrict__ idx,
-                                                     uint8_t* __restrict__ htab, size_t tab_bytes) {
-  __shared__ int scratch[2];
-  const int q = blockIdx.x;
-  if (idx[q] < 0) return;
-  pack_act_row<Q4>(h + (size_t)q * dff, dff, htab + (size_t)q * tab_bytes, scratch);
+  __syncthreads();
+  for (int i = threadIdx.x; i < r1 - r0; i += blockDim.x) a.h[(size_t)q * a.dff + r0 + i] = hb[i];
+  int nl;
+  uint32_t sum;
+  pack_act_cols<Q4>(hb - r0, a.dff, r0, r1, a.htab + (size_t)q * a.htab_bytes, threadIdx.x,
+                    blockDim.x, nl, sum);
+  atomicMax(&red_nl, nl);
+  atomicAdd(&red_sum, sum);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + blockIdx.x) * 2;
+    pp[0] = (uint32_t)red_nl;
+    pp[1] = red_sum;
+  }
 }
 
 struct DownArgs {
-  const uint8_t* dq; const float* ds; long long rb; int D, dff, E;
-  const int* tasks; const uint8_t* htab; size_t tab_bytes; const float* h;
-  float* y; int rows_per_block;
+  const uint8_t* dq; const float* ds; long long rb; int T, D, dff, topk;
+  const int* idx; const float* p; const uint8_t* htab; size_t tab_bytes; const float* h;
+  const uint32_t* hpart; int nchunks;
+  const float* resid; float* out; int rows_per_block;
 };
 
+// Epilogue of down: yb[j][row - r0] = Q(h_j Wd_j)  (LDS)
+struct DownEpi {
+  const float* ds;
+  float* yb;
+  int r0;
+  float div;
+  template <class Tot>
+  __device__ void operator()(int row, const Tot& tot) const {
+    yb[row - r0] = qdot_epilogue(tot[0][0], div, ds[row]);
+  }
+};
+struct DownEpiMaker {
+  DownEpi e;
+  template <int MTI>
+  __device__ DownEpi at(int) const { return e; }
+};
+
+// down + weighted sum for one token and one row chunk: wave w computes
+// y_j for ranks j = w, w+8, ... into LDS; then out[t, o] = x_resid +
+// (((0 + p0 y0) + p1 y1) + ...) in rank order (test_model_trace.c:502-517).
 template <bool Q4, class G>
-__global__ __launch_bounds__(kTileBlock) void down_kernel(DownArgs a) {
-  const int u = blockIdx.y;
-  if (u >= a.tasks[0]) return;
-  const int e = a.tasks[1 + u], st = a.tasks[1 + a.E + u], n = a.tasks[1 + 2 * a.E + u];
-  const int* pairs = a.tasks + 1 + 3 * a.E + st;
+__global__ __launch_bounds__(kRouterThreads) void down_combine_kernel(DownArgs a) {
+  extern __shared__ float yb[];   // [topk][rows_per_block]
+  const int t = blockIdx.y;
   const int r0 = blockIdx.x * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.D ? r0 + a.rows_per_block : a.D;
-  const uint8_t* W[1] = {a.dq + (size_t)e * a.D * a.rb};
-  for (int c0 = 0; c0 < n; c0 += kMTok) {
-    const int nt = n - c0 < kMTok ? n - c0 : kMTok;
-    const uint8_t* tabs[kMTok];
-    const float* xs[kMTok];
-#pragma unroll
-    for (int t = 0; t < kMTok; ++t) {
-      const int q = pairs[c0 + (t < nt ? t : nt - 1)];
-      tabs[t] = a.htab + (size_t)q * a.tab_bytes;
-      xs[t] = a.h + (size_t)q * a.dff;
-    }
-    DownEpiMaker mk{a.ds + (size_t)e * a.D, a.y, pairs + c0, nt, a.D, Q4 ? 7.0f : 127.0f};
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int j = wave; j < a.topk; j += kRouterWaves) {
+    const int q = t * a.topk + j;
+    const int e = a.idx[q];
+    if (e < 0) continue;
+    const uint8_t* W[1] = {a.dq + (size_t)e * a.D * a.rb};
+    const uint8_t* tab = a.htab + (size_t)q * a.tab_bytes;
+    const float* x = a.h + (size_t)q * a.dff;
+    DownEpiMaker mk{DownEpi{a.ds + (size_t)e * a.D, yb + (size_t)j * a.rows_per_block, r0,
+                            Q4 ? 7.0f : 127.0f}};
     if constexpr (std::is_same<G, GenericGeom>::value) {
-      for (int t = 0; t < nt; ++t) {
-        auto epi = mk.template at<1>(t);
-        generic_rows_fp32<Q4, 1>(W, a.rb, a.dff, xs[t], r0, r1, epi);
-      }
+      auto epi = mk.e;
+      generic_rows_fp32_wave<Q4, 1>(W, a.rb, a.dff, x, r0, r1, epi);
     } else {
-      stream_tokens<Q4, G, 1, kMTok>(W, a.rb, a.dff, tabs, xs, nt, r0, r1, mk);
+      // limb count and activation sum of h: reduce the gate/up chunk partials
+      int nl = 1;
+      uint32_t sum = 0;
+      for (int c = lane; c < a.nchunks; c += kWave) {
+        const uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + c) * 2;
+        nl = (int)pp[0] > nl ? (int)pp[0] : nl;
+        sum += pp[1];
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const int on = __shfl_xor(nl, off, kWave);
+        nl = on > nl ? on : nl;
+        sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+      }
+      stream_row_wave<Q4, G, 1>(W, a.rb, a.dff, tab, x, r0, r1, mk, nl, sum);
     }
   }
-}
-
-__global__ void combine_kernel(const float* __restrict__ y, const float* __restrict__ p,
-                               const int* __restrict__ idx, const float* __restrict__ resid,
-                               float* __restrict__ out, int T, int D, int topk) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)T * D) return;
-  const int t = (int)(i / D), o = (int)(i % D);
-  float acc = 0.0f;
-  for (int j = 0; j < topk; ++j) {
-    const int q = t * topk + j;
-    if (idx[q] < 0) continue;
-    const float py = p[q] * y[(size_t)q * D + o];
-    acc = acc + py;
+  __syncthreads();
+  for (int o = r0 + threadIdx.x; o < r1; o += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < a.topk; ++j) {
+      const int q = t * a.topk + j;
+      if (a.idx[q] < 0) continue;
+      const float py = a.p[q] * yb[(size_t)j * a.rows_per_block + (o - r0)];
+      acc = acc + py;
+    }
+    const size_t oi = (size_t)t * a.D + o;
+    a.out[oi] = a.resid ? a.resid[oi] + acc : acc;
   }
-  out[i] = resid ? resid[i] + acc : acc;
 }
 
-// rmsnorm (test_model_trace.c:241-255): one wave per token; the sum of
-// squares is one sequential chain in lane 0 (8 lanes feed it through DPP).
-__global__ __launch_bounds__(64) void rmsnorm_kernel(const float* __restrict__ x,
-                                                     const float* __restrict__ w,
-                                                     float* __restrict__ y, int D, float eps,
-                                                     int fast) {
+// rmsnorm (test_model_trace.c:241-255): one block per token; the row is
+// staged in LDS and the sum of squares is one sequential chain in lane 0.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w,
+                                                      float* __restrict__ y, int D, float eps,
+                                                      int fast) {
+  extern __shared__ float xs[];
   __shared__ float inv_s;
   const int t = blockIdx.x;
   const float* xt = x + (size_t)t * D;
   if (fast) {
-    // 8 chains would be computed by the 8 groups of the wave; only group 0's
-    // lane 0 carries the real one (D-long), the others are idle copies.
-    const float acc = seq_dot_group8(xt, xt, D, true);
+    for (int i = threadIdx.x; i < D / 4; i += blockDim.x)
+      reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(xt)[i];
+    __syncthreads();
     if (threadIdx.x == 0) {
+      const float acc = seq_dot_lane(xs, xs, D);
       const float msq = acc / (float)D;
       inv_s = 1.0f / sqrtf(msq + eps);
     }
@@ -446,7 +546,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
   if (st) return st;
   hipFree(L->logits); hipFree(L->idx); hipFree(L->p); hipFree(L->xtab); hipFree(L->htab);
-  hipFree(L->h); hipFree(L->y); hipFree(L->xn); hipFree(L->tasks);
+  hipFree(L->h); hipFree(L->xn); hipFree(L->xpart); hipFree(L->hpart);
   L->capT = 0;
   const size_t np = (size_t)T * L->topk;
   if ((st = dev_alloc(&L->logits, (size_t)T * L->E))) return st;
@@ -455,56 +555,81 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   if ((st = dev_alloc(&L->xtab, (size_t)T * act_table_bytes(L->D)))) return st;
   if ((st = dev_alloc(&L->htab, np * act_table_bytes(L->dff)))) return st;
   if ((st = dev_alloc(&L->h, np * L->dff))) return st;
-  if ((st = dev_alloc(&L->y, np * L->D))) return st;
   if ((st = dev_alloc(&L->xn, (size_t)T * L->D))) return st;
-  if ((st = dev_alloc(&L->tasks, 1 + 3 * (size_t)L->E + np))) return st;
+  const size_t nbx = (size_t)(L->E + kRouterExperts - 1) / kRouterExperts;
+  if ((st = dev_alloc(&L->xpart, (size_t)T * nbx * 2))) return st;
+  if ((st = dev_alloc(&L->hpart, np * (size_t)((L->dff + 7) / 8) * 2))) return st;
+  if (!L->counters) {
+    if ((st = dev_alloc(&L->counters, 1))) return st;
+    if ((st = check_hip(hipMemsetAsync(L->counters, 0, 4, stream()), "counter init"))) return st;
+  }
   L->capT = T;
   return MOE_OK;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
+// Rows-per-block targets (tuning knobs, read once): MOEHIP_GATEUP_BLOCKS and
+// MOEHIP_DOWN_BLOCKS set the number of blocks a launch aims for.
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+int gateup_target_blocks() { static const int v = env_int("MOEHIP_GATEUP_BLOCKS", 1024); return v; }
+int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 512); return v; }
+
 template <bool Q4, class G>
-void launch_gate_up(const LayerDev* L, const float* xn, int T, int U_max, hipStream_t s) {
-  constexpr int unit = kTileWaves * G::WR;
-  const long long total = (long long)L->dff * std::min(U_max, T * L->topk);
-  long long rpb = (total + 1023) / 1024;
+void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s) {
+  // rows per block: a multiple of both the wave-group unit and 8 (whole
+  // packed dwords of h), sized for ~1024 blocks
+  constexpr int unit0 = kTileWaves * G::WR;
+  constexpr int unit = unit0 % 8 == 0 ? unit0 : (unit0 % 4 == 0 ? unit0 * 2 : unit0 * 8);
+  const int npairs = T * L->topk;
+  const long long total = (long long)L->dff * npairs;
+  const int tgt = gateup_target_blocks();
+  long long rpb = (total + tgt - 1) / tgt;
   rpb = std::max<long long>(unit, (rpb + unit - 1) / unit * unit);
   rpb = std::min<long long>(rpb, 8 * unit);
-  GateUpArgs a{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->E, L->topk, L->tasks,
-               L->xtab, act_table_bytes(L->D), xn, L->h, (int)rpb};
-  dim3 grid((unsigned)((L->dff + rpb - 1) / rpb), (unsigned)U_max);
-  hipLaunchKernelGGL((gate_up_kernel<Q4, G>), grid, dim3(kTileBlock), 0, s, a);
+  const int nc = (int)((L->dff + rpb - 1) / rpb);
+  *nchunks = nc;
+  GateUpArgs a{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk, L->idx,
+               L->xtab, act_table_bytes(L->D), xn, L->h, L->htab, act_table_bytes(L->dff),
+               L->hpart, nc, (int)rpb};
+  dim3 grid((unsigned)nc, (unsigned)npairs);
+  hipLaunchKernelGGL((gate_up_kernel<Q4, G>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
 }
 
 template <bool Q4, class G>
-void launch_down(const LayerDev* L, int T, int U_max, hipStream_t s) {
-  constexpr int unit = kTileWaves * G::WR;
-  const long long total = (long long)L->D * std::min(U_max, T * L->topk);
-  long long rpb = (total + 1023) / 1024;
+void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, float* out,
+                 hipStream_t s) {
+  constexpr int unit = G::WR;                   // one wave per rank
+  const long long total = (long long)L->D * T;
+  const int tgt = down_target_blocks();
+  long long rpb = (total + tgt - 1) / tgt;
   rpb = std::max<long long>(unit, (rpb + unit - 1) / unit * unit);
-  rpb = std::min<long long>(rpb, 8 * unit);
-  DownArgs a{L->dq, L->ds, L->rbd, L->D, L->dff, L->E, L->tasks, L->htab,
-             act_table_bytes(L->dff), L->h, L->y, (int)rpb};
-  dim3 grid((unsigned)((L->D + rpb - 1) / rpb), (unsigned)U_max);
-  hipLaunchKernelGGL((down_kernel<Q4, G>), grid, dim3(kTileBlock), 0, s, a);
+  rpb = std::min<long long>(rpb, 16 * unit);
+  DownArgs a{L->dq, L->ds, L->rbd, T, L->D, L->dff, L->topk, L->idx, L->p, L->htab,
+             act_table_bytes(L->dff), L->h, L->hpart, nchunks, resid, out, (int)rpb};
+  dim3 grid((unsigned)((L->D + rpb - 1) / rpb), (unsigned)T);
+  hipLaunchKernelGGL((down_combine_kernel<Q4, G>), grid, dim3(kRouterThreads),
+                     (size_t)L->topk * rpb * 4, s, a);
 }
 
 // Row-byte dispatch for the expert GEMVs (same geometries as gemv.hip).
 template <bool Q4, class F>
-bool with_geom(long long rb, F&& f) {
+void with_geom(long long rb, F&& f) {
   switch (rb) {
-    case 192:  f(TileGeom<3, 4>()); return true;
-    case 256:  f(TileGeom<4, 4>()); return true;
-    case 384:  f(TileGeom<3, 8>()); return true;
-    case 512:  f(TileGeom<4, 8>()); return true;
-    case 768:  f(TileGeom<3, 16>()); return true;
-    case 1024: f(TileGeom<4, 16>()); return true;
-    case 1536: f(TileGeom<3, 32>()); return true;
-    case 2048: f(TileGeom<4, 32>()); return true;
-    case 3072: f(TileGeom<3, 64>()); return true;
-    case 4096: f(TileGeom<4, 64>()); return true;
-    default: f(GenericGeom()); return true;
+    case 192:  f(TileGeom<3, 4>()); return;
+    case 256:  f(TileGeom<4, 4>()); return;
+    case 384:  f(TileGeom<3, 8>()); return;
+    case 512:  f(TileGeom<4, 8>()); return;
+    case 768:  f(TileGeom<3, 16>()); return;
+    case 1024: f(TileGeom<4, 16>()); return;
+    case 1536: f(TileGeom<3, 32>()); return;
+    case 2048: f(TileGeom<4, 32>()); return;
+    case 3072: f(TileGeom<3, 64>()); return;
+    case 4096: f(TileGeom<4, 64>()); return;
+    default: f(GenericGeom()); return;
   }
 }
 
@@ -517,52 +642,49 @@ moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T
   if (st) return st;
   hipStream_t s = stream();
   const bool q4 = L->dtype == 3;
-  const int fast = (L->D % 32 == 0) && aligned16(xn) && aligned16(L->router_w);
-  const size_t lds = 2 * (size_t)L->E * sizeof(float);
+  RouterArgs ra;
+  ra.xn = xn; ra.T = T; ra.D = L->D; ra.E = L->E; ra.topk = L->topk;
+  ra.W = L->router_w; ra.b = L->router_b; ra.logits = L->logits; ra.idx = L->idx; ra.p = L->p;
+  ra.idx_user = idx_out; ra.p_user = p_out; ra.xtab = L->xtab; ra.tab_bytes = act_table_bytes(L->D);
+  ra.xpart = L->xpart; ra.counter = L->counters;
+  const int nbx = (L->E + kRouterExperts - 1) / kRouterExperts;
+  ra.cols = ((L->D + nbx - 1) / nbx + 7) / 8 * 8;
+  const size_t row_bytes = (size_t)(L->D + kRowPad) * 4;
+  ra.tb = std::min(kRouterTokens, T);
+  ra.staged = (L->D % 16 == 0) && aligned16(xn) && aligned16(L->router_w) &&
+              (kRouterExperts + ra.tb) * row_bytes <= kMaxLds;
+  const size_t lds = ra.staged ? (kRouterExperts + (size_t)ra.tb) * row_bytes : 0;
+  dim3 rgrid((unsigned)nbx, (unsigned)((T + ra.tb - 1) / ra.tb));
+  const void* rfn = q4 ? (const void*)router_kernel<true> : (const void*)router_kernel<false>;
+  if (lds > 65536 &&
+      (st = check_hip(hipFuncSetAttribute(rfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                      "router LDS attribute")))
+    return st;
   if (q4)
-    hipLaunchKernelGGL(router_topk_kernel<true>, dim3(T), dim3(kRouterThreads), lds, s, xn, L->D,
-                       L->E, L->topk, L->router_w, L->router_b, L->logits, L->idx, L->p, L->xtab,
-                       act_table_bytes(L->D), fast);
+    hipLaunchKernelGGL(router_kernel<true>, rgrid, dim3(kRouterThreads), lds, s, ra);
   else
-    hipLaunchKernelGGL(router_topk_kernel<false>, dim3(T), dim3(kRouterThreads), lds, s, xn, L->D,
-                       L->E, L->topk, L->router_w, L->router_b, L->logits, L->idx, L->p, L->xtab,
-                       act_table_bytes(L->D), fast);
+    hipLaunchKernelGGL(router_kernel<false>, rgrid, dim3(kRouterThreads), lds, s, ra);
   if ((st = check_hip(hipGetLastError(), "router launch"))) return st;
-  const int npairs = T * L->topk;
-  hipLaunchKernelGGL(build_tasks_kernel, dim3(1), dim3(256), 2 * (size_t)L->E * sizeof(int), s,
-                     L->idx, npairs, L->E, L->tasks);
-  if ((st = check_hip(hipGetLastError(), "tasks launch"))) return st;
-  const int U_max = std::min(L->E, npairs);
-  bool ok = q4 ? with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, U_max, s); })
-               : with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, U_max, s); });
-  if (!ok) return set_error(MOE_ERR_UNSUPPORTED, "gate/up row bytes %lld have no tiled geometry", L->rbg);
+  int nchunks = 0;
+  if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s); });
+  else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s); });
   if ((st = check_hip(hipGetLastError(), "gate_up launch"))) return st;
-  if (q4)
-    hipLaunchKernelGGL(pack_h_kernel<true>, dim3(npairs), dim3(256), 0, s, L->h, L->dff, L->idx,
-                       L->htab, act_table_bytes(L->dff));
-  else
-    hipLaunchKernelGGL(pack_h_kernel<false>, dim3(npairs), dim3(256), 0, s, L->h, L->dff, L->idx,
-                       L->htab, act_table_bytes(L->dff));
-  if ((st = check_hip(hipGetLastError(), "pack_h launch"))) return st;
-  ok = q4 ? with_geom<true>(L->rbd, [&](auto g) { launch_down<true, decltype(g)>(L, T, U_max, s); })
-          : with_geom<false>(L->rbd, [&](auto g) { launch_down<false, decltype(g)>(L, T, U_max, s); });
-  if (!ok) return set_error(MOE_ERR_UNSUPPORTED, "down row bytes %lld have no tiled geometry", L->rbd);
-  if ((st = check_hip(hipGetLastError(), "down launch"))) return st;
-  const size_t n = (size_t)T * L->D;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, L->y,
-                     L->p, L->idx, resid, out, T, L->D, L->topk);
-  if ((st = check_hip(hipGetLastError(), "combine launch"))) return st;
-  if (idx_out)
-    if ((st = check_hip(hipMemcpyAsync(idx_out, L->idx, (size_t)npairs * 4, hipMemcpyDeviceToDevice, s), "idx copy"))) return st;
-  if (p_out)
-    if ((st = check_hip(hipMemcpyAsync(p_out, L->p, (size_t)npairs * 4, hipMemcpyDeviceToDevice, s), "p copy"))) return st;
-  return MOE_OK;
+  if (q4) with_geom<true>(L->rbd, [&](auto g) { launch_down<true, decltype(g)>(L, T, nchunks, resid, out, s); });
+  else with_geom<false>(L->rbd, [&](auto g) { launch_down<false, decltype(g)>(L, T, nchunks, resid, out, s); });
+  return check_hip(hipGetLastError(), "down launch");
 }
 
 moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps) {
   if (T <= 0) return MOE_OK;
-  const int fast = (D % 32 == 0) && aligned16(x);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(64), 0, stream(), x, w, y, D, eps, fast);
+  const int fast = (D % 16 == 0) && aligned16(x) && (size_t)(D + kRowPad) * 4 <= kMaxLds;
+  const size_t lds = fast ? (size_t)(D + kRowPad) * 4 : 0;
+  if (lds > 65536) {
+    moe_status st = check_hip(hipFuncSetAttribute((const void*)rmsnorm_kernel,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  (int)lds), "rmsnorm LDS attribute");
+    if (st) return st;
+  }
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), lds, stream(), x, w, y, D, eps, fast);
   return check_hip(hipGetLastError(), "rmsnorm launch");
 }
 
@@ -585,7 +707,7 @@ void free_layer(LayerDev& L) {
   hipFree(L.router_w); hipFree(L.router_b); hipFree(L.rms2_w);
   hipFree(L.gq); hipFree(L.gs); hipFree(L.uq); hipFree(L.us); hipFree(L.dq); hipFree(L.ds);
   hipFree(L.logits); hipFree(L.idx); hipFree(L.p); hipFree(L.xtab); hipFree(L.htab);
-  hipFree(L.h); hipFree(L.y); hipFree(L.xn); hipFree(L.tasks);
+  hipFree(L.h); hipFree(L.xn); hipFree(L.xpart); hipFree(L.hpart); hipFree(L.counters);
 }
 
 }  // namespace
@@ -711,7 +833,7 @@ moe_status moe_layer_debug_buffers(moe_layer* layer, const float** logits, const
   if (!layer) return set_error(MOE_ERR_ARG, "debug_buffers: null layer");
   if (logits) *logits = layer->L.logits;
   if (h) *h = layer->L.h;
-  if (y) *y = layer->L.y;
+  if (y) *y = nullptr;   // expert outputs stay in LDS (fused with the weighted sum)
   return MOE_OK;
 }
 

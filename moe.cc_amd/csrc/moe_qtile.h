@@ -85,6 +85,48 @@ __device__ void pack_act_row(const float* __restrict__ x, int K, uint8_t* __rest
   }
 }
 
+// Packs columns [c0, c1) of one activation row (x points at column 0) into
+// the table's planes; c0 is a multiple of 8.  Returns this thread's limb
+// count and activation sum over the columns it packed; threads of a team
+// (tid in [0, nthr)) split the work.
+template <bool Q4>
+__device__ void pack_act_cols(const float* x, int K, int c0, int c1, uint8_t* tab, int tid,
+                              int nthr, int& nl_out, uint32_t& sum_out) {
+  const float mult = Q4 ? 7.0f : 127.0f;
+  constexpr int V = Q4 ? 8 : 4;
+  const size_t plane = (((size_t)K + 15) / 16) * 16;
+  uint32_t* p0 = reinterpret_cast<uint32_t*>(tab + 16);
+  const int KW = (K + 7) / 8;
+  int nl = 1;
+  uint32_t part = 0;
+  const int nv = (c1 - c0 + V - 1) / V;
+  for (int i = tid; i < nv; i += nthr) {
+    const int d = c0 / V + i;
+    uint32_t b[V][4];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int k = V * d + v;
+      const int32_t a = k < c1 ? f2i_trunc_x86(x[k] * mult) : 0;
+      const int n = limbs_needed(a);
+      nl = n > nl ? n : nl;
+      part += (uint32_t)a;
+      split_limbs(a, b[v]);
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      uint32_t* pl = p0 + (size_t)l * (plane / 4);
+      if constexpr (!Q4) {
+        pl[d] = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+      } else {
+        pl[d] = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
+        pl[KW + d] = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
+      }
+    }
+  }
+  nl_out = nl;
+  sum_out = part;
+}
+
 // ---- cross-lane integer sums with DPP ----
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
@@ -184,13 +226,16 @@ __device__ __forceinline__ uint32_t lane_dot(const uint32_t (&w)[G::DW],
 // with the loads of the next group issued before the current one is reduced.
 // For each valid row, lane 0 of its lane group calls
 //     epi(row, tot)   with tot[mat][t] = exact int32 dot (Q4 offset removed).
+// The rows are shared by a team of nwv waves; this wave is number wv.
+// asum_in (optional, per token slot) replaces the tables' header sums.
 template <bool Q4, class G, int NL, int MTI, int NM, class Epi>
 __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long rs, int K,
                                             const uint8_t* const* tab, int r0, int r1,
-                                            Epi& epi) {
+                                            Epi& epi, int wv, int nwv,
+                                            const uint32_t* asum_in = nullptr) {
   ActRegs<Q4, G, NL> ar[MTI];
   uint32_t asum[MTI];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave, wave = wv;
   const int g = lane / G::LPR, r = lane % G::LPR;
   const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
   auto load = [&](int gi, uint32_t (&w)[NM][G::DW]) {
@@ -224,15 +269,15 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
 #pragma unroll
   for (int t = 0; t < MTI; ++t) {
     load_act_regs<Q4, G, NL>(tab[t], K, ar[t]);
-    asum[t] = Q4 ? act_asum(tab[t]) : 0u;
+    asum[t] = Q4 ? (asum_in ? asum_in[t] : act_asum(tab[t])) : 0u;
   }
   while (gi < ngroups) {
-    int gn = gi + kTileWaves;
+    int gn = gi + nwv;
     if (gn < ngroups) load(gn, wb);
     finish(gi, wa);
     gi = gn;
     if (gi >= ngroups) break;
-    gn = gi + kTileWaves;
+    gn = gi + nwv;
     if (gn < ngroups) load(gn, wa);
     finish(gi, wb);
     gi = gn;
@@ -254,9 +299,9 @@ constexpr int mti_for() {
 // token slot.
 template <bool Q4, int NM, class Epi>
 __device__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K, const float* x,
-                                  int r0, int r1, Epi& epi) {
+                                  int r0, int r1, Epi& epi, int wv, int nwv) {
   const int lane = threadIdx.x % kWave;
-  for (int row = r0 + (int)(threadIdx.x / kWave); row < r1; row += blockDim.x / kWave) {
+  for (int row = r0 + wv; row < r1; row += nwv) {
     uint32_t tot[NM][1];
 #pragma unroll
     for (int mat = 0; mat < NM; ++mat) {
@@ -289,7 +334,7 @@ __device__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K, 
 template <bool Q4, class G, int NM, int MT, class MakeEpi>
 __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
                               const uint8_t* const* tabs, const float* const* xs, int ntok, int r0,
-                              int r1, MakeEpi& make_epi) {
+                              int r1, MakeEpi& make_epi, int wv, int nwv) {
   int nl = 1;
   for (int t = 0; t < ntok; ++t) {
     const int v = act_nl(tabs[t]);
@@ -301,7 +346,7 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
     if constexpr (M0 == 0) {
       for (int t = 0; t < ntok; ++t) {
         auto epi = make_epi.template at<1>(t);
-        generic_rows_fp32<Q4, NM>(W, rs, K, xs[t], r0, r1, epi);
+        generic_rows_fp32<Q4, NM>(W, rs, K, xs[t], r0, r1, epi, wv, nwv);
       }
     } else {
       constexpr int MTI = M0 < MT ? M0 : MT;
@@ -310,7 +355,7 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
 #pragma unroll
         for (int t = 0; t < MTI; ++t) tb[t] = tabs[t0 + t < ntok ? t0 + t : ntok - 1];
         auto epi = make_epi.template at<MTI>(t0);
-        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi);
+        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi, wv, nwv);
       }
     }
   };
@@ -320,6 +365,56 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
     run(std::integral_constant<int, 2>());
   else
     run(std::integral_constant<int, 4>());
+}
+
+// Whole-block team: every wave of the block shares the rows.
+template <bool Q4, class G, int NM, int MT, class MakeEpi>
+__device__ __forceinline__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
+                                              const uint8_t* const* tabs, const float* const* xs,
+                                              int ntok, int r0, int r1, MakeEpi& make_epi) {
+  stream_tokens<Q4, G, NM, MT>(W, rs, K, tabs, xs, ntok, r0, r1, make_epi,
+                               (int)(threadIdx.x / kWave), (int)(blockDim.x / kWave));
+}
+
+// One wave alone streams rows [r0, r1) for one activation row whose limb
+// count nl and activation sum asum are given (the table's header is not read).
+template <bool Q4, class G, int NM, class MakeEpi>
+__device__ __forceinline__ void stream_row_wave(const uint8_t* const* W, long long rs, int K,
+                                                const uint8_t* tab, const float* x, int r0,
+                                                int r1, MakeEpi& make_epi, int nl,
+                                                uint32_t asum) {
+  const uint8_t* tabs[1] = {tab};
+  const uint32_t as[1] = {asum};
+  auto run = [&](auto nl_tag) {
+    constexpr int NL = decltype(nl_tag)::value;
+    if constexpr (mti_for<Q4, G, NL, NM>() == 0) {
+      auto epi = make_epi.template at<1>(0);
+      generic_rows_fp32<Q4, NM>(W, rs, K, x, r0, r1, epi, 0, 1);
+    } else {
+      auto epi = make_epi.template at<1>(0);
+      stream_rows<Q4, G, NL, 1, NM>(W, rs, K, tabs, r0, r1, epi, 0, 1, as);
+    }
+  };
+  if (nl <= 1)
+    run(std::integral_constant<int, 1>());
+  else if (nl == 2)
+    run(std::integral_constant<int, 2>());
+  else
+    run(std::integral_constant<int, 4>());
+}
+
+template <bool Q4, int NM, class Epi>
+__device__ __forceinline__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K,
+                                                  const float* x, int r0, int r1, Epi& epi) {
+  generic_rows_fp32<Q4, NM>(W, rs, K, x, r0, r1, epi, (int)(threadIdx.x / kWave),
+                            (int)(blockDim.x / kWave));
+}
+
+template <bool Q4, int NM, class Epi>
+__device__ __forceinline__ void generic_rows_fp32_wave(const uint8_t* const* W, long long rs,
+                                                       int K, const float* x, int r0, int r1,
+                                                       Epi& epi) {
+  generic_rows_fp32<Q4, NM>(W, rs, K, x, r0, r1, epi, 0, 1);
 }
 
 }  // namespace moe

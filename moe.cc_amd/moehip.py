@@ -279,6 +279,8 @@ class MoeLayer:
         for name, ptr, shape in (("logits", lg.value, (T, self.E)),
                                  ("h", hh.value, (T * self.top_k, self.d_ff)),
                                  ("y", yy.value, (T * self.top_k, self.D))):
+            if not ptr:
+                continue
             a = np.empty(shape, np.float32)
             check(lib().moe_memcpy_d2h(a.ctypes.data, ptr, a.nbytes))
             out[name] = a
