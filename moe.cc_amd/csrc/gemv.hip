@@ -16,6 +16,8 @@
 // Shapes without a tiled geometry (row bytes not LPR*P*16, unaligned rows,
 // odd-K Q4) and Q4 activations that need 4 limbs use a one-wave-per-row
 // kernel with plain int32 arithmetic on the fp32 activations.
+#include <cstdlib>
+
 #include "moe_device.h"
 #include "moe_internal.h"
 #include "moe_qtile.h"
@@ -47,6 +49,7 @@ __global__ __launch_bounds__(kBlock) void act_pack_kernel(QShape sh, const QJob*
   __shared__ int scratch[2];
   const int j = blockIdx.x, m = blockIdx.y;
   const QJob job = jobs ? jobs[j] : one;
+  if (j > 0 && job.A == jobs[0].A) return;   // shares job 0's activations and tables
   pack_act_row<Q4>(job.A + (size_t)m * sh.lda, sh.K, tabs + ((size_t)j * sh.M + m) * tab_bytes,
                    scratch);
 }
@@ -83,12 +86,14 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
   const QJob job = get_job(a, job_id);
   const int mbase = blockIdx.y * MT;
   const int ntok = a.sh.M - mbase < MT ? a.sh.M - mbase : MT;
+  // jobs whose activations are job 0's use job 0's packed tables
+  const int tab_job = (a.jobs && job_id > 0 && job.A == a.jobs[0].A) ? 0 : job_id;
   const uint8_t* tabs[MT];
   const float* xs[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     const int m = mbase + (t < ntok ? t : ntok - 1);
-    tabs[t] = a.tabs + ((size_t)job_id * a.sh.M + m) * a.tab_bytes;
+    tabs[t] = a.tabs + ((size_t)tab_job * a.sh.M + m) * a.tab_bytes;
     xs[t] = job.A + (size_t)m * a.sh.lda;
   }
   const uint8_t* W[1] = {job.W};
@@ -232,13 +237,16 @@ hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one,
       hipLaunchKernelGGL(act_pack_kernel<false>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
                          jobs_dev, one, g_ws, tb);
     // rows per block: a multiple of (waves x rows per wave group), large
-    // enough to amortise the activation loads, small enough for >= ~2048 blocks
+    // enough to amortise the activation loads, small enough for >= target
+    // blocks (tuning knobs MOEHIP_GEMV_BLOCKS, MOEHIP_GEMV_MAX_GROUPS)
+    static const int target = getenv("MOEHIP_GEMV_BLOCKS") ? atoi(getenv("MOEHIP_GEMV_BLOCKS")) : 2048;
+    static const int max_groups = getenv("MOEHIP_GEMV_MAX_GROUPS") ? atoi(getenv("MOEHIP_GEMV_MAX_GROUPS")) : 8;
     const int unit = kWaves * v.wr;
     const long long total_rows = (long long)sh.N * njobs;
-    long long rpb = (total_rows + 2047) / 2048;
+    long long rpb = (total_rows + target - 1) / target;
     rpb = (rpb + unit - 1) / unit * unit;
     if (rpb < unit) rpb = unit;
-    if (rpb > 8 * unit) rpb = 8 * unit;
+    if (rpb > (long long)max_groups * unit) rpb = (long long)max_groups * unit;
     if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
     TiledArgs a;
     a.sh = sh;

@@ -16,7 +16,8 @@ from typing import Optional
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmoehip.so")
+# MOEHIP_LIB selects another build of the library (for comparing variants)
+LIB_PATH = os.environ.get("MOEHIP_LIB") or os.path.join(_HERE, "libmoehip.so")
 
 _lib: Optional[ctypes.CDLL] = None
 
