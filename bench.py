@@ -73,12 +73,18 @@ class Pool:
         self.jobs = M.DeviceBuffer(ctypes.sizeof(jobs))
         M.check(L.moe_memcpy_h2d(self.jobs.ptr, ctypes.addressof(jobs), ctypes.sizeof(jobs)))
         M.synchronize()
+        self.tabs = M.DeviceBuffer(L.moe_act_table_bytes(K))
         self.bytes_per_launch = count * gemv_bytes(dtype, N, K)
         self.weight_bytes = count * N * rb
 
+    def pack(self):
+        """Quantizes x into its packed tables (kernels.c:56-60 / :107-110)."""
+        M.check(M.lib().moe_act_pack_dev(self.dtype, self.x.ptr, 1, self.K, self.tabs.ptr), "pack")
+
     def launch(self):
-        M.check(M.lib().moe_matmul_q_batched_dev(self.dtype, self.jobs.ptr, self.count, 1,
-                                                 self.N, self.K), "batched gemv")
+        """The `count` GEMVs from the packed tables, one launch."""
+        M.check(M.lib().moe_matmul_q_prepacked_dev(self.dtype, self.jobs.ptr, self.count, 1,
+                                                   self.N, self.K, self.tabs.ptr), "gemv")
 
 
 def kernel_name(dtype, N, K):
@@ -122,17 +128,50 @@ def cpu_baseline(shapes, budget_s: float):
                       f"{os.cpu_count()} host cores"}
 
 
+COPY_CALIB_BYTES = 256 << 20
+
+
+def copy_calibration():
+    """One device-to-device copy of known size before the timed region: the
+    HBM-traffic counters (FETCH_SIZE / WRITE_SIZE) of the rocprofv3 --pmc runs
+    are scaled by what they read for this copy."""
+    a = M.DeviceBuffer(COPY_CALIB_BYTES)
+    b = M.DeviceBuffer(COPY_CALIB_BYTES)
+    M.check(M.lib().moe_memset(a.ptr, 1, COPY_CALIB_BYTES))
+    M.check(M.lib().moe_memcpy_d2d(b.ptr, a.ptr, COPY_CALIB_BYTES))
+    a.free()
+    b.free()
+
+
+def measured_traffic(kernel_name):
+    """HBM bytes per launch of `kernel_name` from the committed PMC summary
+    (profiles/traffic.json, written from two rocprofv3 --pmc runs of this
+    script), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t["kernels"].get(kernel_name, {}).get("traffic_bytes_per_launch")
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def run_gemv(args, dtype, shapes, workload):
     M.init(0)
+    copy_calibration()
     pools = []
     for i, (N, K) in enumerate(shapes):
         rb = K if dtype == 2 else K // 2
         count = int(np.ceil(args.pool_gib * (1 << 30) / (N * rb)))
         log(f"[bench] building pool {N}x{K} dtype {dtype}: {count} matrices")
         pools.append(Pool(dtype, N, K, count, seed=1000 * (i + 1)))
-    evs = {i: [(M.Event(), M.Event()) for _ in range(args.steps)] for i in range(len(pools))}
+    # per step and shape: pack (event a -> b), then the GEMV launch (b -> c);
+    # the roofline is taken on the GEMV launch alone, the step value on both
+    evs = {i: [(M.Event(), M.Event(), M.Event()) for _ in range(args.steps)]
+           for i in range(len(pools))}
     for _ in range(args.warmup):
         for p in pools:
+            p.pack()
             p.launch()
     M.synchronize()
     t_start, t_end = M.Event(), M.Event()
@@ -140,21 +179,25 @@ def run_gemv(args, dtype, shapes, workload):
     t_start.record()
     for s in range(args.steps):
         for i, p in enumerate(pools):
-            a, b = evs[i][s]
+            a, b, c = evs[i][s]
             a.record()
-            p.launch()
+            p.pack()
             b.record()
+            p.launch()
+            c.record()
     t_end.record()
     M.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_ms(t_end)
     per_kernel = []
     for i, p in enumerate(pools):
-        ms = [a.elapsed_ms(b) for a, b in evs[i]]
+        ms = [b.elapsed_ms(c) for a, b, c in evs[i]]
+        pack_ms = [a.elapsed_ms(b) for a, b, c in evs[i]]
         avg = float(np.mean(ms))
         per_kernel.append({"kernel": f"qgemv_{kernel_name(dtype, p.N, p.K)}",
                            "shape": f"{p.N}x{p.K}", "matrices_per_launch": p.count,
                            "avg_launch_us": round(avg * 1e3, 2),
+                           "avg_pack_us": round(float(np.mean(pack_ms)) * 1e3, 2),
                            "algorithmic_bytes_per_launch": p.bytes_per_launch,
                            "achieved_GBs": round(p.bytes_per_launch / (avg * 1e-3) / 1e9, 1)})
     bytes_step = sum(p.bytes_per_launch for p in pools)
@@ -174,7 +217,8 @@ def run_gemv(args, dtype, shapes, workload):
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": dom["kernel"]},
+                     "traffic": measured_traffic(dom["kernel"]), "kernel": dom["kernel"],
+                     "algorithmic_bytes": dom["algorithmic_bytes_per_launch"]},
         "kernels": per_kernel,
         "wall_s_timed": round(wall, 3),
     }

@@ -160,6 +160,21 @@ typedef struct {
 moe_status moe_matmul_q_batched_dev(int dtype, const moe_qjob* jobs_dev, int njobs,
                                     int M, int N, int K);
 
+/* The two halves of moe_matmul_q_batched_dev, for callers that reuse one set
+ * of activations across many products (gate and up of every expert read the
+ * same x).  moe_act_pack_dev is the activation quantization of
+ * kernels.c:56-60 (Q8) / kernels.c:107-110 (Q4) for M rows of A [M x K],
+ * written as M packed tables of moe_act_table_bytes(K) bytes each into tabs
+ * (16-byte aligned).  moe_matmul_q_prepacked_dev then runs the products of
+ * kernels.c:62-72 / :112-126 from those tables; every job's A must be the
+ * array the tables were packed from (rows whose quantized activations need
+ * four bytes fall back to reading it).  Shapes whose row bytes (K or K/2)
+ * are not one of the tiled widths 192..4096 return MOE_ERR_ARG. */
+size_t moe_act_table_bytes(int K);
+moe_status moe_act_pack_dev(int dtype, const float* A, int M, int K, void* tabs);
+moe_status moe_matmul_q_prepacked_dev(int dtype, const moe_qjob* jobs_dev, int njobs,
+                                      int M, int N, int K, const void* tabs);
+
 /* test_model_trace.c:229-236 and :500 on device arrays of n floats:
  * h = (g / (1 + expf(-g))) * u  (u may be NULL: h = silu(g)).  expf is
  * bit-identical to the host glibc expf, so h matches the reference exactly. */

@@ -332,6 +332,52 @@ moe_status moe_matmul_q_batched_dev(int dtype, const moe_qjob* jobs_dev, int njo
                    "batched qgemv launch");
 }
 
+size_t moe_act_table_bytes(int K) { return K < 0 ? 0 : act_table_size(K); }
+
+static moe_status prepacked_shape(int dtype, int M, int N, int K, const char* who, QShape* sh) {
+  if (dtype != 2 && dtype != 3) return set_error(MOE_ERR_ARG, "%s: dtype %d", who, dtype);
+  if (M < 0 || N < 0 || K <= 0) return set_error(MOE_ERR_ARG, "%s: bad shape", who);
+  if (dtype == 3 && (K & 1)) return set_error(MOE_ERR_ARG, "%s: Q4 needs even K", who);
+  sh->dtype = dtype;
+  sh->M = M;
+  sh->N = N;
+  sh->K = K;
+  sh->lda = K;
+  sh->ldc = N;
+  sh->rs = dtype == 3 ? K / 2 : K;
+  if (!qgemv_tiled_ok(*sh, nullptr))
+    return set_error(MOE_ERR_ARG, "%s: no tiled geometry for %lld-byte rows", who, sh->rs);
+  return MOE_OK;
+}
+
+moe_status moe_act_pack_dev(int dtype, const float* A, int M, int K, void* tabs) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  QShape sh;
+  st = prepacked_shape(dtype, M, 1, K, "act_pack", &sh);
+  if (st) return st;
+  if (((uintptr_t)tabs % 16) != 0) return set_error(MOE_ERR_ARG, "act_pack: tabs not 16-byte aligned");
+  if (M == 0) return MOE_OK;
+  QJob one{nullptr, nullptr, A, nullptr};
+  return check_hip(launch_act_pack(sh, nullptr, one, 1, (uint8_t*)tabs, g_stream), "act_pack launch");
+}
+
+moe_status moe_matmul_q_prepacked_dev(int dtype, const moe_qjob* jobs_dev, int njobs, int M, int N,
+                                      int K, const void* tabs) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  QShape sh;
+  st = prepacked_shape(dtype, M, N, K, "prepacked", &sh);
+  if (st) return st;
+  if (njobs < 0) return set_error(MOE_ERR_ARG, "prepacked: njobs %d", njobs);
+  if (((uintptr_t)tabs % 16) != 0) return set_error(MOE_ERR_ARG, "prepacked: tabs not 16-byte aligned");
+  if (njobs == 0 || M == 0 || N == 0) return MOE_OK;
+  QJob none{nullptr, nullptr, nullptr, nullptr};
+  return check_hip(launch_qgemv_tables(sh, (const QJob*)jobs_dev, none, njobs, (const uint8_t*)tabs,
+                                       1, g_stream),
+                   "prepacked qgemv launch");
+}
+
 const char* moe_gemv_variant(int dtype, int M, int N, int K) {
   QShape sh;
   sh.dtype = dtype;

@@ -34,6 +34,7 @@ struct TiledArgs {
   QJob one;
   const uint8_t* tabs;  // packed activations, [job][m] tables of tab_bytes
   size_t tab_bytes;
+  int shared_tabs;      // 1: every job uses job 0's tables
   int blocks_per_job;
   int rows_per_block;
 };
@@ -87,7 +88,8 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
   const int mbase = blockIdx.y * MT;
   const int ntok = a.sh.M - mbase < MT ? a.sh.M - mbase : MT;
   // jobs whose activations are job 0's use job 0's packed tables
-  const int tab_job = (a.jobs && job_id > 0 && job.A == a.jobs[0].A) ? 0 : job_id;
+  const int tab_job =
+      (a.shared_tabs || (a.jobs && job_id > 0 && job.A == a.jobs[0].A)) ? 0 : job_id;
   const uint8_t* tabs[MT];
   const float* xs[MT];
 #pragma unroll
@@ -219,53 +221,75 @@ const char* qgemv_variant_name(const QShape& sh, const void* w_base) {
   return "generic";
 }
 
+hipError_t launch_act_pack(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                           uint8_t* tabs, hipStream_t stream) {
+  const size_t tb = act_table_bytes(sh.K);
+  if (sh.dtype == 3)
+    hipLaunchKernelGGL(act_pack_kernel<true>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
+                       jobs_dev, one, tabs, tb);
+  else
+    hipLaunchKernelGGL(act_pack_kernel<false>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
+                       jobs_dev, one, tabs, tb);
+  return hipGetLastError();
+}
+
+hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                               const uint8_t* tabs, int shared_tabs, hipStream_t stream) {
+  Variant v;
+  if (!select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) return hipErrorInvalidValue;
+  // rows per block: a multiple of (waves x rows per wave group), large
+  // enough to amortise the activation loads, small enough for >= target
+  // blocks (tuning knobs MOEHIP_GEMV_BLOCKS, MOEHIP_GEMV_MAX_GROUPS)
+  static const int target = getenv("MOEHIP_GEMV_BLOCKS") ? atoi(getenv("MOEHIP_GEMV_BLOCKS")) : 2048;
+  static const int max_groups = getenv("MOEHIP_GEMV_MAX_GROUPS") ? atoi(getenv("MOEHIP_GEMV_MAX_GROUPS")) : 8;
+  const int unit = kWaves * v.wr;
+  const long long total_rows = (long long)sh.N * njobs;
+  long long rpb = (total_rows + target - 1) / target;
+  rpb = (rpb + unit - 1) / unit * unit;
+  if (rpb < unit) rpb = unit;
+  if (rpb > (long long)max_groups * unit) rpb = (long long)max_groups * unit;
+  if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
+  TiledArgs a;
+  a.sh = sh;
+  a.jobs = jobs_dev;
+  a.one = one;
+  a.tabs = tabs;
+  a.tab_bytes = act_table_bytes(sh.K);
+  a.shared_tabs = shared_tabs;
+  a.rows_per_block = (int)rpb;
+  a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
+  dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
+  hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
+  return hipGetLastError();
+}
+
+size_t act_table_size(int K) { return act_table_bytes(K); }
+
+bool qgemv_tiled_ok(const QShape& sh, const void* w_base) {
+  Variant v;
+  return select_tiled(sh, w_base, &v);
+}
+
 hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
                         hipStream_t stream) {
   if (sh.M <= 0 || sh.N <= 0 || njobs <= 0) return hipSuccess;
   if (sh.dtype != 2 && sh.dtype != 3) return hipErrorInvalidValue;
-  Variant v;
   // With a device job array the host cannot see the pointers; callers of the
   // batched entry point guarantee 16-byte aligned packed rows (capi.cpp).
-  if (select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) {
+  if (qgemv_tiled_ok(sh, jobs_dev ? nullptr : one.W)) {
     const size_t tb = act_table_bytes(sh.K);
     hipError_t e = ensure_ws(tb * (size_t)njobs * (size_t)sh.M);
     if (e != hipSuccess) return e;
-    if (sh.dtype == 3)
-      hipLaunchKernelGGL(act_pack_kernel<true>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
-                         jobs_dev, one, g_ws, tb);
-    else
-      hipLaunchKernelGGL(act_pack_kernel<false>, dim3(njobs, sh.M), dim3(kBlock), 0, stream, sh,
-                         jobs_dev, one, g_ws, tb);
-    // rows per block: a multiple of (waves x rows per wave group), large
-    // enough to amortise the activation loads, small enough for >= target
-    // blocks (tuning knobs MOEHIP_GEMV_BLOCKS, MOEHIP_GEMV_MAX_GROUPS)
-    static const int target = getenv("MOEHIP_GEMV_BLOCKS") ? atoi(getenv("MOEHIP_GEMV_BLOCKS")) : 2048;
-    static const int max_groups = getenv("MOEHIP_GEMV_MAX_GROUPS") ? atoi(getenv("MOEHIP_GEMV_MAX_GROUPS")) : 8;
-    const int unit = kWaves * v.wr;
-    const long long total_rows = (long long)sh.N * njobs;
-    long long rpb = (total_rows + target - 1) / target;
-    rpb = (rpb + unit - 1) / unit * unit;
-    if (rpb < unit) rpb = unit;
-    if (rpb > (long long)max_groups * unit) rpb = (long long)max_groups * unit;
-    if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
-    TiledArgs a;
-    a.sh = sh;
-    a.jobs = jobs_dev;
-    a.one = one;
-    a.tabs = g_ws;
-    a.tab_bytes = tb;
-    a.rows_per_block = (int)rpb;
-    a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
-    dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
-    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
-  } else {
-    const int bpj = (sh.N + kWaves - 1) / kWaves;
-    dim3 grid((unsigned)((long long)bpj * njobs), (unsigned)((sh.M + 15) / 16));
-    if (sh.dtype == 3)
-      hipLaunchKernelGGL(qgemv_generic<true>, grid, dim3(kBlock), 0, stream, sh, jobs_dev, one, bpj);
-    else
-      hipLaunchKernelGGL(qgemv_generic<false>, grid, dim3(kBlock), 0, stream, sh, jobs_dev, one, bpj);
+    e = launch_act_pack(sh, jobs_dev, one, njobs, g_ws, stream);
+    if (e != hipSuccess) return e;
+    return launch_qgemv_tables(sh, jobs_dev, one, njobs, g_ws, 0, stream);
   }
+  const int bpj = (sh.N + kWaves - 1) / kWaves;
+  dim3 grid((unsigned)((long long)bpj * njobs), (unsigned)((sh.M + 15) / 16));
+  if (sh.dtype == 3)
+    hipLaunchKernelGGL(qgemv_generic<true>, grid, dim3(kBlock), 0, stream, sh, jobs_dev, one, bpj);
+  else
+    hipLaunchKernelGGL(qgemv_generic<false>, grid, dim3(kBlock), 0, stream, sh, jobs_dev, one, bpj);
   return hipGetLastError();
 }
 

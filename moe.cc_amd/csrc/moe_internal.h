@@ -29,6 +29,17 @@ struct QShape {
 hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
                         hipStream_t stream);
 
+// The two halves of a tiled launch, for callers that pack activations once
+// and reuse them: act tables for job j, row m at tabs + (j*M + m)*table bytes
+// (shared_tabs: every job uses job 0's).  launch_qgemv_tables requires a
+// shape with a tiled geometry (qgemv_tiled_ok).
+hipError_t launch_act_pack(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                           uint8_t* tabs, hipStream_t stream);
+hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                               const uint8_t* tabs, int shared_tabs, hipStream_t stream);
+bool qgemv_tiled_ok(const QShape& sh, const void* w_base);
+size_t act_table_size(int K);
+
 // fp32 path of matmul_adaptive (kernels.c:153-165): sequential k, one
 // rounding per multiply and per add.  W row-major [N][ldw].
 hipError_t launch_f32gemv(const float* A, const float* W, float* C, int M, int N, int K,

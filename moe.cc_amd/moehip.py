@@ -76,6 +76,9 @@ _SIGS = {
     "moe_matmul_adaptive_dev": (_I, [_P, _P, ctypes.POINTER(QuantizedWeight), _P, _I, _I, _I]),
     "moe_matmul_q_batched_dev": (_I, [_I, _P, _I, _I, _I, _I]),
     "moe_gemv_variant": (ctypes.c_char_p, [_I, _I, _I, _I]),
+    "moe_act_table_bytes": (_SZ, [_I]),
+    "moe_act_pack_dev": (_I, [_I, _P, _I, _I, _P]),
+    "moe_matmul_q_prepacked_dev": (_I, [_I, _P, _I, _I, _I, _I, _P]),
     "moe_silu_mul_dev": (_I, [_P, _P, _P, _SZ]),
     "moe_expf_dev": (_I, [_P, _P, _SZ]),
     "moe_expf_bits_dev": (_I, [ctypes.c_uint32, _P, _SZ]),

@@ -135,3 +135,43 @@ def test_variant_selection(moehip):
     assert moehip.gemv_variant(3, 1, 2048, 768).startswith("tiled")
     assert moehip.gemv_variant(3, 1, 768, 2048).startswith("tiled")
     assert moehip.gemv_variant(3, 1, 4, 9) == "generic"
+
+
+@pytest.mark.parametrize("dtype,N,K,M,scale", [(2, 768, 2048, 1, 1.0), (3, 2048, 768, 3, 1.0),
+                                               (3, 768, 2048, 5, 40.0), (2, 512, 1024, 2, 400.0)])
+def test_prepacked_matches_oracle(moehip, dtype, N, K, M, scale):
+    """Pack once, run several products from the same tables.  scale 40 / 400
+    pushes Q4 / Q8 activations into the 2- and 4-byte limb ranges."""
+    L = moehip.lib()
+    nj = 3
+    A = O.normal(M * K, 900 + M, 0.0, scale).reshape(M, K)
+    dA = moehip.DeviceBuffer.from_array(A)
+    tb = L.moe_act_table_bytes(K)
+    assert tb % 16 == 0 and tb >= 16 + K
+    tabs = moehip.DeviceBuffer(tb * M)
+    moehip.check(L.moe_act_pack_dev(dtype, dA.ptr, M, K, tabs.ptr), "pack")
+    jobs = (moehip.QJob * nj)()
+    keep, outs, wants = [], [], []
+    for j in range(nj):
+        W = O.normal(N * K, 910 + j, 0.0, 0.02).reshape(N, K)
+        q, s = (O.quant_q8 if dtype == 2 else O.quant_q4)(W)
+        wants.append((O.gemv_q8 if dtype == 2 else O.gemv_q4)(A, q, s, N, K))
+        dq, ds, dC = (moehip.DeviceBuffer.from_array(q), moehip.DeviceBuffer.from_array(s),
+                      moehip.DeviceBuffer(M * N * 4))
+        keep += [dq, ds]
+        outs.append(dC)
+        jobs[j] = moehip.QJob(dq.ptr, ds.ptr, dA.ptr, dC.ptr)
+    djobs = moehip.DeviceBuffer(ctypes.sizeof(jobs))
+    moehip.check(L.moe_memcpy_h2d(djobs.ptr, ctypes.addressof(jobs), ctypes.sizeof(jobs)))
+    moehip.check(L.moe_matmul_q_prepacked_dev(dtype, djobs.ptr, nj, M, N, K, tabs.ptr), "prepacked")
+    for j in range(nj):
+        np.testing.assert_array_equal(bits(outs[j].download((M, N), np.float32)), bits(wants[j]))
+
+
+def test_prepacked_rejects_untiled_shapes(moehip):
+    L = moehip.lib()
+    buf = moehip.DeviceBuffer(4096)
+    assert L.moe_act_pack_dev(3, buf.ptr, 1, 9, buf.ptr) != 0        # odd Q4 K
+    assert L.moe_matmul_q_prepacked_dev(2, buf.ptr, 1, 1, 4, 100, buf.ptr) != 0
+    assert b"tiled" in L.moe_last_error()
+    assert L.moe_act_pack_dev(2, buf.ptr, 1, 2048, buf.ptr + 4) != 0  # misaligned tables
