@@ -23,3 +23,18 @@ def test_quantize_rows(moehip, dtype, N, K):
     s = ds.download(s_want.shape, np.float32)
     np.testing.assert_array_equal(s.view(np.uint32), s_want.view(np.uint32))
     np.testing.assert_array_equal(q, q_want)
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_quantize_ties(moehip, dtype):
+    """Rows whose w/s lands exactly on k + 0.5 round to the even neighbour."""
+    if dtype == 2:
+        W = np.array([[127.0, 2.5, -2.5, 3.5, -3.5, 0.5, -0.5, 126.5]], np.float32)
+    else:
+        W = np.array([[7.0, 2.5, -2.5, 3.5, -6.5, 0.5, -0.5, 1.5]], np.float32)
+    q_want, s_want = (O.quant_q8 if dtype == 2 else O.quant_q4)(W)
+    dW = moehip.DeviceBuffer.from_array(W)
+    dq, ds = moehip.DeviceBuffer(q_want.nbytes), moehip.DeviceBuffer(4)
+    moehip.check(moehip.lib().moe_quantize_rows_dev(dtype, dW.ptr, 1, 8, dq.ptr, ds.ptr), "quantize")
+    np.testing.assert_array_equal(dq.download(q_want.shape, q_want.dtype), q_want)
+    assert ds.download((1,), np.float32)[0] == 1.0

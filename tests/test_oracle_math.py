@@ -235,3 +235,19 @@ def test_moe_dominant_expert():
     _, idx, p, _ = O.moe_block(x, None, rw, rb, ex)
     assert idx[0, 0] == 11
     assert p[0, 0] > 0.999999 and np.all(p[0, 1:] < 1e-20)
+
+
+def test_quantizer_ties_round_half_even():
+    """export.py rounds with torch.round, documented as round-half-to-even.
+    Rows built so that fl(w / s) lands exactly on k + 0.5: the oracle must
+    pick the even neighbour (a half-away-from-zero rounding would not)."""
+    # amax 127 gives s = 1.0 exactly (Q8) and 7 gives s = 1.0 (Q4)
+    row8 = np.array([127.0, 2.5, -2.5, 3.5, -3.5, 0.5, -0.5, 126.5], np.float32)
+    q8, s8 = O.quant_q8(row8[None, :])
+    assert s8[0] == 1.0
+    assert q8[0].tolist() == [127, 2, -2, 4, -4, 0, 0, 126]
+    row4 = np.array([7.0, 2.5, -2.5, 3.5, -6.5, 0.5, -0.5, 1.5], np.float32)
+    q4, s4 = O.quant_q4(row4[None, :])
+    assert s4[0] == 1.0
+    w4 = unpack_q4(q4, 1, 8)[0].tolist()
+    assert w4 == [7, 2, -2, 4, -6, 0, 0, 2]
