@@ -210,6 +210,12 @@ moe_status moe_layer_create_raw(int dtype, int D, int d_ff, int E, int top_k,
                                 const void* dq, const float* ds, int src_on_device,
                                 moe_layer** out);
 moe_status moe_layer_destroy(moe_layer* layer);
+/* Forwards of at least min_tokens tokens run expert-major (every routed
+ * expert's rows read once for all its tokens, int8 MFMA tiles); fewer
+ * tokens run the per-(token, rank) decode kernels.  0 = library default
+ * (env MOEHIP_GROUPED_MIN_T, else 32).  Both give identical results.
+ * Expert-major needs D and d_ff multiples of 128 (Q8) or 256 (Q4). */
+moe_status moe_layer_set_grouped_min_tokens(moe_layer* layer, int min_tokens);
 /* test_model_trace.c:463-517 on device arrays:
  *   out[t] = x_resid[t] + sum_j p[t,j] * down_e(silu(gate_e x) * up_e x),
  *   e = idx[t,j], the top_k experts of logits = x_norm Wr^T (+ b), p their

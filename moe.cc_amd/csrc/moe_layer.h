@@ -1,0 +1,138 @@
+// moe_layer.h - device state of one MoE layer and the routing helpers shared
+// by the decode kernels (moe_layer.hip) and the grouped multi-token kernels
+// (moe_grouped.hip).  Internal; the public ABI is include/moehip.h.
+#pragma once
+#include <stdint.h>
+
+#include "moe_device.h"
+#include "moe_lib.h"
+
+namespace moe {
+
+constexpr int kMaxTopK = 32;
+
+struct LayerDev {
+  int dtype = 2, D = 0, dff = 0, E = 0, topk = 0;
+  long long rbg = 0, rbd = 0;          // row bytes of gate/up and of down
+  float* router_w = nullptr;           // [E][D]
+  float* router_b = nullptr;           // [E] or null
+  float* rms2_w = nullptr;             // [D] or null
+  uint8_t* gq = nullptr; float* gs = nullptr;   // [E][dff][rbg], [E][dff]
+  uint8_t* uq = nullptr; float* us = nullptr;
+  uint8_t* dq = nullptr; float* ds = nullptr;   // [E][D][rbd], [E][D]
+  int grouped_min_T = 0;               // 0: library default
+  // per-forward scratch, grown to the largest T seen
+  int capT = 0;
+  float* logits = nullptr;   // [T][E]
+  int* idx = nullptr;        // [T][topk]
+  float* p = nullptr;        // [T][topk]
+  uint8_t* xtab = nullptr;   // [T] packed x_norm rows
+  uint8_t* htab = nullptr;   // [T*topk] packed h rows
+  float* h = nullptr;        // [T*topk][dff] (decode kernels)
+  float* xn = nullptr;       // [T][D] normed input (block forward)
+  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables
+  uint32_t* hpart = nullptr; // [T*topk][h segments][2] partial headers of the h tables
+  // completion counter of the router's last-block step, zero between launches
+  unsigned* counters = nullptr;
+  // grouped kernels: pairs per expert, first pair of each expert in `perm`,
+  // pair ids (t * topk + j) grouped by expert, expert outputs per pair
+  int* ecount = nullptr;     // [E]
+  int* eoff = nullptr;       // [E]
+  int* perm = nullptr;       // [T*topk]
+  float* y = nullptr;        // [T*topk][D]
+};
+
+// Grouped (expert-major) forward for many tokens; requires grouped_ok(L).
+bool grouped_ok(const LayerDev* L);
+moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
+                                 float* out, int32_t* idx_out, float* p_out);
+moe_status ensure_grouped_scratch(LayerDev* L, int T);
+
+// ---- routing: top-k by the insertion rule, softmax over the selection ----
+
+// (v, i) beats (w, j): valid and larger, or equal with the lower index.
+__device__ __forceinline__ bool beats(float v, int i, float w, int j) {
+  if (i < 0) return false;
+  if (j < 0) return true;
+  return v > w || (v == w && i < j);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step_dpp(float& bv, int& bi) {
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bv), CTRL, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_update_dpp(-1, bi, CTRL, 0xF, 0xF, false);
+  if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+}
+
+// Wave-wide arg-max of (value, index) pairs under `beats`; every lane ends
+// with the winner.  DPP within rows of 16, then two cross-row exchanges.
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+  argmax_step_dpp<0xB1>(bv, bi);    // quad_perm [1,0,3,2]
+  argmax_step_dpp<0x4E>(bv, bi);    // quad_perm [2,3,0,1]
+  argmax_step_dpp<0x141>(bv, bi);   // row_half_mirror
+  argmax_step_dpp<0x140>(bv, bi);   // row_mirror
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+}
+
+// One wave selects the experts of one token and their gates:
+//   top-k by repeated arg-max (the largest remaining logit, lowest index
+//   among equals) = the insertion rule of test_model_trace.c:275-288; NaN
+//   and -inf never selected, slots left over keep index -1;
+//   p_i = expf(v_i - max) / (sum + 1e-9f), sum in slot order (:482-487).
+// C = candidates per lane (E <= 64*C).  sidx/sval/sexp: this wave's LDS
+// slots (kMaxTopK each).  Outputs are per-token rows of K entries; the user
+// copies may be null.
+template <int C>
+__device__ void select_token(const float* __restrict__ logit_row, int E, int K, int* sidx,
+                             float* sval, float* sexp, int* idx, float* p, int* idx_user,
+                             float* p_user) {
+  const int lane = threadIdx.x % kWave;
+  float v[C];
+  bool live[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int e = lane + kWave * c;
+    v[c] = e < E ? logit_row[e] : -__builtin_inff();
+    live[c] = e < E && v[c] > -__builtin_inff();   // false for NaN and -inf
+  }
+  for (int r = 0; r < K; ++r) {
+    float bv = -__builtin_inff();
+    int bi = -1;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (live[c] && beats(v[c], lane + kWave * c, bv, bi)) { bv = v[c]; bi = lane + kWave * c; }
+    wave_argmax(bv, bi);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (bi == lane + kWave * c) live[c] = false;
+    if (lane == 0) { sidx[r] = bi; sval[r] = bi >= 0 ? bv : -__builtin_inff(); }
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  if (lane < K) {
+    float mx = sval[0];
+    for (int i = 1; i < K; ++i) if (sval[i] > mx) mx = sval[i];
+    sexp[lane] = expf_glibc(sval[lane] - mx);
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  float sum = 0.0f;
+  for (int i = 0; i < K; ++i) sum = sum + sexp[i];
+  const float inv = 1.0f / (sum + 1e-9f);
+  if (lane < K) {
+    const float pv = sexp[lane] * inv;
+    idx[lane] = sidx[lane];
+    p[lane] = pv;
+    if (idx_user) idx_user[lane] = sidx[lane];
+    if (p_user) p_user[lane] = pv;
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+}
+
+}  // namespace moe

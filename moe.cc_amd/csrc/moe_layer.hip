@@ -18,9 +18,10 @@
 //               its own (:513, :517).
 // Cross-block hand-offs go through kernel boundaries (and one last-block
 // step in the 16-block router), never through per-block device fences.
-// The router's sequential sum runs as one add chain per (token, expert):
-// 8 lanes hold 32 consecutive products and lane 0 of the group adds them in
-// k order through DPP row shifts (v_add_f32_dpp), so a wave carries 8 chains.
+// The router's sequential sum runs as one add chain per (token, expert) and
+// lane, over rows staged in LDS (seq_dot_lane).
+// These kernels serve few tokens (decode); many tokens go through the
+// expert-major kernels of moe_grouped.hip.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -29,34 +30,11 @@
 #include <vector>
 
 #include "moe_device.h"
+#include "moe_layer.h"
 #include "moe_lib.h"
 #include "moe_qtile.h"
 
 namespace moe {
-
-struct LayerDev {
-  int dtype = 2, D = 0, dff = 0, E = 0, topk = 0;
-  long long rbg = 0, rbd = 0;          // row bytes of gate/up and of down
-  float* router_w = nullptr;           // [E][D]
-  float* router_b = nullptr;           // [E] or null
-  float* rms2_w = nullptr;             // [D] or null
-  uint8_t* gq = nullptr; float* gs = nullptr;   // [E][dff][rbg], [E][dff]
-  uint8_t* uq = nullptr; float* us = nullptr;
-  uint8_t* dq = nullptr; float* ds = nullptr;   // [E][D][rbd], [E][D]
-  // per-forward scratch, grown to the largest T seen
-  int capT = 0;
-  float* logits = nullptr;   // [T][E]
-  int* idx = nullptr;        // [T][topk]
-  float* p = nullptr;        // [T][topk]
-  uint8_t* xtab = nullptr;   // [T] packed x_norm rows
-  uint8_t* htab = nullptr;   // [T*topk] packed h rows
-  float* h = nullptr;        // [T*topk][dff]
-  float* xn = nullptr;       // [T][D] normed input (block forward)
-  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables
-  uint32_t* hpart = nullptr; // [T*topk][gate/up chunks][2] partial headers of the h tables
-  // completion counter of the router's last-block step, zero between launches
-  unsigned* counters = nullptr;
-};
 
 namespace {
 
@@ -64,7 +42,6 @@ constexpr int kRouterThreads = 512;            // 8 waves
 constexpr int kRouterWaves = kRouterThreads / kWave;
 constexpr int kRouterExperts = 8;              // experts per router block
 constexpr int kRouterTokens = 8;               // tokens per router block: 64 chains = 1 wave
-constexpr int kMaxTopK = 32;
 constexpr size_t kMaxLds = 160 * 1024 - 2048;  // dynamic LDS budget (static LDS fits in the rest)
 
 // Sequential fp32 dot of x[0..D) with w, k ascending, each product and each
@@ -145,35 +122,6 @@ struct RouterArgs {
   int cols;              // x columns packed per block (multiple of 8)
 };
 
-// (v, i) beats (w, j): valid and larger, or equal with the lower index.
-__device__ __forceinline__ bool beats(float v, int i, float w, int j) {
-  if (i < 0) return false;
-  if (j < 0) return true;
-  return v > w || (v == w && i < j);
-}
-
-template <int CTRL>
-__device__ __forceinline__ void argmax_step_dpp(float& bv, int& bi) {
-  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bv), CTRL, 0xF, 0xF, true));
-  const int oi = __builtin_amdgcn_update_dpp(-1, bi, CTRL, 0xF, 0xF, false);
-  if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-}
-
-// Wave-wide arg-max of (value, index) pairs under `beats`; every lane ends
-// with the winner.  DPP within rows of 16, then two cross-row exchanges.
-__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
-  argmax_step_dpp<0xB1>(bv, bi);    // quad_perm [1,0,3,2]
-  argmax_step_dpp<0x4E>(bv, bi);    // quad_perm [2,3,0,1]
-  argmax_step_dpp<0x141>(bv, bi);   // row_half_mirror
-  argmax_step_dpp<0x140>(bv, bi);   // row_mirror
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    const float ov = __shfl_xor(bv, off, kWave);
-    const int oi = __shfl_xor(bi, off, kWave);
-    if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-  }
-}
-
 // Runs in the last router block.  Headers of the packed x rows; then, one
 // wave per token, top-k by repeated arg-max (the largest remaining value,
 // lowest index among equals: the result of the insertion rule of
@@ -209,48 +157,10 @@ __device__ void router_finish(const RouterArgs& a) {
     }
   }
   for (int t = wave; t < a.T; t += kRouterWaves) {
-    float v[C];
-    bool live[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int e = lane + kWave * c;
-      v[c] = e < E ? a.logits[(size_t)t * E + e] : -__builtin_inff();
-      live[c] = e < E && v[c] > -__builtin_inff();   // false for NaN and -inf
-    }
-    for (int r = 0; r < K; ++r) {
-      float bv = -__builtin_inff();
-      int bi = -1;
-#pragma unroll
-      for (int c = 0; c < C; ++c)
-        if (live[c] && beats(v[c], lane + kWave * c, bv, bi)) { bv = v[c]; bi = lane + kWave * c; }
-      wave_argmax(bv, bi);
-#pragma unroll
-      for (int c = 0; c < C; ++c)
-        if (bi == lane + kWave * c) live[c] = false;
-      if (lane == 0) { sidx[wave][r] = bi; sval[wave][r] = bi >= 0 ? bv : -__builtin_inff(); }
-    }
-    __threadfence_block();
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) {
-      float mx = sval[wave][0];
-      for (int i = 1; i < K; ++i) if (sval[wave][i] > mx) mx = sval[wave][i];
-      sexp[wave][lane] = expf_glibc(sval[wave][lane] - mx);
-    }
-    __threadfence_block();
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    for (int i = 0; i < K; ++i) sum = sum + sexp[wave][i];
-    const float inv = 1.0f / (sum + 1e-9f);
-    if (lane < K) {
-      const size_t q = (size_t)t * K + lane;
-      const float pv = sexp[wave][lane] * inv;
-      a.idx[q] = sidx[wave][lane];
-      a.p[q] = pv;
-      if (a.idx_user) a.idx_user[q] = sidx[wave][lane];
-      if (a.p_user) a.p_user[q] = pv;
-    }
-    __threadfence_block();
-    __builtin_amdgcn_wave_barrier();
+    const size_t q = (size_t)t * K;
+    select_token<C>(a.logits + (size_t)t * E, E, K, sidx[wave], sval[wave], sexp[wave],
+                    a.idx + q, a.p + q, a.idx_user ? a.idx_user + q : nullptr,
+                    a.p_user ? a.p_user + q : nullptr);
   }
 }
 
@@ -338,7 +248,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
   else router_finish<Q4, 16>(a);
 }
 
-constexpr int kMTok = 4;   // token slots per block pass in the GEMV kernels
 
 // Marks the untiled expert path: one wave per row, int32 arithmetic on the
 // fp32 activations (any row size; used for small or irregular layers).
@@ -535,6 +444,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 
 // ---- host helpers ----
 template <class T>
+void dfree(T* p) {
+  if (p) (void)hipFree((void*)p);
+}
+
+template <class T>
 moe_status dev_alloc(T** p, size_t count) {
   *p = nullptr;
   if (count == 0) return MOE_OK;
@@ -545,8 +459,8 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   if (T <= L->capT) return MOE_OK;
   moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
   if (st) return st;
-  hipFree(L->logits); hipFree(L->idx); hipFree(L->p); hipFree(L->xtab); hipFree(L->htab);
-  hipFree(L->h); hipFree(L->xn); hipFree(L->xpart); hipFree(L->hpart);
+  dfree(L->logits); dfree(L->idx); dfree(L->p); dfree(L->xtab); dfree(L->htab);
+  dfree(L->h); dfree(L->xn); dfree(L->xpart); dfree(L->hpart);
   L->capT = 0;
   const size_t np = (size_t)T * L->topk;
   if ((st = dev_alloc(&L->logits, (size_t)T * L->E))) return st;
@@ -559,6 +473,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   const size_t nbx = (size_t)(L->E + kRouterExperts - 1) / kRouterExperts;
   if ((st = dev_alloc(&L->xpart, (size_t)T * nbx * 2))) return st;
   if ((st = dev_alloc(&L->hpart, np * (size_t)((L->dff + 7) / 8) * 2))) return st;
+  if (grouped_ok(L) && (st = ensure_grouped_scratch(L, T))) return st;
   if (!L->counters) {
     if ((st = dev_alloc(&L->counters, 1))) return st;
     if ((st = check_hip(hipMemsetAsync(L->counters, 0, 4, stream()), "counter init"))) return st;
@@ -635,11 +550,20 @@ void with_geom(long long rb, F&& f) {
 
 }  // namespace
 
+// Tokens from which the expert-major kernels replace the per-pair decode
+// kernels (layer setting, else MOEHIP_GROUPED_MIN_T, else 32).
+int grouped_min_tokens(const LayerDev* L) {
+  static const int dflt = env_int("MOEHIP_GROUPED_MIN_T", 32);
+  return L->grouped_min_T > 0 ? L->grouped_min_T : dflt;
+}
+
 moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T, float* out,
                          int32_t* idx_out, float* p_out) {
   if (T <= 0) return MOE_OK;
   moe_status st = ensure_scratch(L, T);
   if (st) return st;
+  if (T >= grouped_min_tokens(L) && grouped_ok(L))
+    return layer_forward_grouped(L, xn, resid, T, out, idx_out, p_out);
   hipStream_t s = stream();
   const bool q4 = L->dtype == 3;
   RouterArgs ra;
@@ -704,10 +628,11 @@ moe_status upload(void* dst, const void* src, size_t bytes, int on_device) {
 }
 
 void free_layer(LayerDev& L) {
-  hipFree(L.router_w); hipFree(L.router_b); hipFree(L.rms2_w);
-  hipFree(L.gq); hipFree(L.gs); hipFree(L.uq); hipFree(L.us); hipFree(L.dq); hipFree(L.ds);
-  hipFree(L.logits); hipFree(L.idx); hipFree(L.p); hipFree(L.xtab); hipFree(L.htab);
-  hipFree(L.h); hipFree(L.xn); hipFree(L.xpart); hipFree(L.hpart); hipFree(L.counters);
+  dfree(L.router_w); dfree(L.router_b); dfree(L.rms2_w);
+  dfree(L.gq); dfree(L.gs); dfree(L.uq); dfree(L.us); dfree(L.dq); dfree(L.ds);
+  dfree(L.logits); dfree(L.idx); dfree(L.p); dfree(L.xtab); dfree(L.htab);
+  dfree(L.h); dfree(L.xn); dfree(L.xpart); dfree(L.hpart); dfree(L.counters);
+  dfree(L.ecount); dfree(L.eoff); dfree(L.perm); dfree(L.y);
 }
 
 }  // namespace
@@ -826,6 +751,13 @@ moe_status moe_rmsnorm_dev(const float* x, const float* w, float* y, int T, int 
   if (st) return st;
   if (!x || !y || T < 0 || D <= 0) return set_error(MOE_ERR_ARG, "rmsnorm: bad argument");
   return rmsnorm_dev(x, w, y, T, D, eps);
+}
+
+moe_status moe_layer_set_grouped_min_tokens(moe_layer* layer, int min_tokens) {
+  if (!layer) return set_error(MOE_ERR_ARG, "set_grouped_min_tokens: null layer");
+  if (min_tokens < 0) return set_error(MOE_ERR_ARG, "set_grouped_min_tokens: %d < 0", min_tokens);
+  layer->L.grouped_min_T = min_tokens;
+  return MOE_OK;
 }
 
 moe_status moe_layer_debug_buffers(moe_layer* layer, const float** logits, const float** h,

@@ -88,6 +88,7 @@ _SIGS = {
     "moe_layer_create_raw": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                                   ctypes.POINTER(_P)]),
     "moe_layer_destroy": (_I, [_P]),
+    "moe_layer_set_grouped_min_tokens": (_I, [_P, _I]),
     "moe_layer_forward": (_I, [_P, _P, _P, _I, _P, _P, _P]),
     "moe_block_forward": (_I, [_P, _P, _I, _P, ctypes.c_float]),
     "moe_rmsnorm_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
@@ -250,6 +251,11 @@ class MoeLayer:
             keep[1].ctypes.data, keep[2].ctypes.data, keep[3].ctypes.data, keep[4].ctypes.data,
             keep[5].ctypes.data, keep[6].ctypes.data, 0, ctypes.byref(h)), "moe_layer_create_raw")
         return cls(h.value, dtype, D, d_ff, E, top_k)
+
+    def set_grouped_min_tokens(self, min_tokens: int):
+        """Token count from which forwards run expert-major (0 = default)."""
+        check(lib().moe_layer_set_grouped_min_tokens(self.h, min_tokens),
+              "moe_layer_set_grouped_min_tokens")
 
     def forward_dev(self, x_norm_ptr, x_resid_ptr, T, out_ptr, idx_ptr=None, p_ptr=None):
         check(lib().moe_layer_forward(self.h, x_norm_ptr, x_resid_ptr, T, out_ptr, idx_ptr, p_ptr),

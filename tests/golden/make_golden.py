@@ -179,8 +179,10 @@ def main():
                              "sha_w": sha(W), "sha_q": sha(q), "sha_s": sha(s), "sha_x": sha(x),
                              "sha_C": sha(C), "pick": pick.tolist(),
                              "C_pick": [float(v) for v in C[0, pick]]})
-    # one decode layer at the real shape (Q8, T=4) and one Q4 (T=2)
-    for tag, dtype, T, seed in [("layer_q8_T4", 2, 4, 2001), ("layer_q4_T2", 3, 2, 2002)]:
+    # layers at the real shape: decode (Q8 T=4, Q4 T=2) and multi-token
+    # (Q8 T=64, Q4 T=128: the expert-major kernels)
+    for tag, dtype, T, seed in [("layer_q8_T4", 2, 4, 2001), ("layer_q4_T2", 3, 2, 2002),
+                                ("layer_q8_T64", 2, 64, 2004), ("layer_q4_T128", 3, 128, 2003)]:
         D, dff, E = 2048, 768, 128
         ex = O.make_experts(dtype, E, D, dff, seed)
         x = O.normal(T * D, seed + 1, 0.0, 1.0).reshape(T, D)

@@ -66,7 +66,7 @@ def test_golden_small_layers(moehip, tag):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("tag", ["layer_q8_T4", "layer_q4_T2"])
+@pytest.mark.parametrize("tag", ["layer_q8_T4", "layer_q4_T2", "layer_q8_T64", "layer_q4_T128"])
 def test_config_layers_vs_reference_digest(moehip, tag):
     with open(os.path.join(GOLD, "ref_config.json")) as f:
         c = next(c for c in json.load(f)["cases"] if c["tag"] == tag)
@@ -155,3 +155,59 @@ def test_repeated_forward_and_growing_T(moehip):
         got, idx, _ = layer.forward(xn, xn)
         np.testing.assert_array_equal(idx, widx)
         np.testing.assert_array_equal(bits(got), bits(want))
+
+
+GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
+    (2, 1, 128, 2048, 768, False, True, 1.0),
+    (3, 3, 128, 2048, 768, True, True, 1.0),
+    (2, 40, 128, 2048, 768, False, True, 1.0),
+    (3, 96, 128, 2048, 768, False, False, 1.0),
+    (2, 21, 32, 1024, 512, True, True, 1.0),
+    (3, 130, 16, 512, 256, False, True, 1.0),    # > 64 pairs per expert: several passes
+    (3, 17, 64, 1024, 512, False, True, 40.0),   # 2-limb Q4 activations
+    (2, 9, 64, 1024, 256, True, True, 400.0),    # 4-limb Q8 activations (and h)
+    (3, 70, 8, 512, 256, False, True, 3000.0),   # 4-limb Q4, > 32 pairs per expert
+]
+
+
+@pytest.mark.parametrize("dtype,T,E,D,dff,bias,resid,scale", GROUPED)
+def test_grouped_vs_oracle(moehip, dtype, T, E, D, dff, bias, resid, scale):
+    """The expert-major kernels (forced at every T) against the oracle."""
+    seed = 8100 + dtype * 100 + T
+    print("grouped case", dtype, T, E, D, dff, bias, resid, scale, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    rb = O.normal(E, seed + 11, 0.0, 0.05) if bias else None
+    xn = O.normal(T * D, seed + 12, 0.0, scale).reshape(T, D)
+    xr = O.normal(T * D, seed + 13, 0.0, 1.0).reshape(T, D) if resid else None
+    want, widx, wp, wlog = O.moe_block(xn, xr, rw, rb, ex)
+    layer = make_layer(moehip, dtype, ex, rw, rb)
+    layer.set_grouped_min_tokens(1)
+    got, idx, p = layer.forward(xn, xr)
+    dbg = layer.debug(T)
+    np.testing.assert_array_equal(bits(dbg["logits"]), bits(wlog))
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+def test_grouped_and_decode_agree_ties_nan(moehip):
+    """Both paths on the same layer and tokens: tied and NaN router logits."""
+    dtype, T, E, D, dff = 2, 12, 32, 256, 128
+    ex = random_experts(dtype, E, D, dff, 77)
+    rw = O.normal(E * D, 78, 0.0, 0.02).reshape(E, D)
+    rw[5] = rw[17]
+    rw[3, 0] = np.nan
+    xn = O.normal(T * D, 79, 0.0, 1.0).reshape(T, D)
+    xn[:, :] += rw[17] * 50
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    layer = make_layer(moehip, dtype, ex, rw)
+    outs = []
+    for mt in (1, 1000):
+        layer.set_grouped_min_tokens(mt)
+        got, idx, p = layer.forward(xn, xn)
+        np.testing.assert_array_equal(idx, widx)
+        np.testing.assert_array_equal(bits(p), bits(wp))
+        np.testing.assert_array_equal(bits(got), bits(want))
+        outs.append(got)
+    assert 3 not in widx

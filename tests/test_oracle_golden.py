@@ -122,7 +122,7 @@ def test_config_gemvs(cfg):
         np.testing.assert_array_equal(C[0, c["pick"]], np.array(c["C_pick"], np.float32))
 
 
-@pytest.mark.parametrize("tag", ["layer_q8_T4", "layer_q4_T2"])
+@pytest.mark.parametrize("tag", ["layer_q8_T4", "layer_q4_T2", "layer_q8_T64", "layer_q4_T128"])
 def test_config_layers(cfg, tag):
     c = next(c for c in cfg["cases"] if c["tag"] == tag)
     ex = O.make_experts(c["dtype"], c["E"], c["D"], c["d_ff"], c["seed"], c["std_w"])
