@@ -283,7 +283,7 @@ def run_decode(dtype, Ts, n_layers, steps, warmup):
         M.check(M.lib().moe_fill_normal_dev(xs.ptr, n_in * T * D, 4242 + T, 0.0, 1.0))
         out = M.DeviceBuffer(T * D * 4)
         idx = M.DeviceBuffer(steps * T * 8 * 4)
-        for i in range(warmup):
+        for i in range(max(warmup, n_layers)):
             lay = pool.layers[i % n_layers]
             lay.forward_dev(xs.ptr + (i % n_in) * T * D * 4, xs.ptr + (i % n_in) * T * D * 4, T,
                             out.ptr)
@@ -316,6 +316,54 @@ def run_decode(dtype, Ts, n_layers, steps, warmup):
     return res
 
 
+def run_prefill(dtype, Ts, n_layers, steps, warmup):
+    """One MoE layer forward per step at prefill (configs[3]: Q4 experts,
+    T tokens, x = RMSNorm(N(0,1)) with eps 1e-6 and weight 1, residual x);
+    layers rotate so expert weights stream from HBM."""
+    M.init(0)
+    pool = LayerPool(dtype, n_layers)
+    D = pool.D
+    L = M.lib()
+    res = []
+    for T in Ts:
+        x = M.DeviceBuffer(T * D * 4)
+        xn = M.DeviceBuffer(T * D * 4)
+        M.check(L.moe_fill_normal_dev(x.ptr, T * D, 5151 + T, 0.0, 1.0))
+        M.check(L.moe_rmsnorm_dev(x.ptr, None, xn.ptr, T, D, 1e-6))
+        out = M.DeviceBuffer(T * D * 4)
+        idx = M.DeviceBuffer(T * 8 * 4)
+        for i in range(max(warmup, n_layers)):
+            pool.layers[i % n_layers].forward_dev(xn.ptr, x.ptr, T, out.ptr)
+        M.synchronize()
+        ev = [(M.Event(), M.Event()) for _ in range(steps)]
+        t0, t1 = M.Event(), M.Event()
+        t0.record()
+        for i in range(steps):
+            ev[i][0].record()
+            pool.layers[i % n_layers].forward_dev(xn.ptr, x.ptr, T, out.ptr, idx.ptr)
+            ev[i][1].record()
+        t1.record()
+        M.synchronize()
+        per = [a.elapsed_ms(b) for a, b in ev]
+        ids = idx.download((T * 8,), np.int32)
+        U = len(set(ids.tolist()) - {-1})
+        algo = 1048576 + U * expert_bytes(dtype, D, pool.dff) + 2 * T * D * 4
+        ops = T * 76021760
+        med = float(np.median(per))
+        res.append({"T": T, "layers_in_pool": n_layers, "steps": steps,
+                    "us_per_layer_median": round(med * 1e3, 2),
+                    "us_per_layer_mean": round(t0.elapsed_ms(t1) / steps * 1e3, 2),
+                    "tokens_per_s_one_layer": round(T / (med * 1e-3), 1),
+                    "distinct_experts_last_step": U, "algorithmic_bytes": int(algo),
+                    "GBs": round(algo / (med * 1e-3) / 1e9, 1),
+                    "pct_hbm_peak": round(100 * algo / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                    "int_TOPs": round(ops / (med * 1e-3) / 1e12, 2)})
+        log(f"[bench] prefill T={T}: {res[-1]}")
+        for b in (x, xn, out, idx):
+            b.free()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -328,6 +376,8 @@ def main():
     ap.add_argument("--decode", default="1,4,16",
                     help="also time one Q8 MoE decode layer at these T (configs[2]); '' to skip")
     ap.add_argument("--decode-layers", type=int, default=6)
+    ap.add_argument("--prefill", default="128,512,2048",
+                    help="also time one Q4 MoE prefill layer at these T (configs[3]); '' to skip")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the expert path on a single MI355X "
@@ -344,6 +394,9 @@ def main():
         Ts = [int(t) for t in args.decode.split(",") if t]
         out["moe_decode_q8"] = run_decode(2, Ts, args.decode_layers, max(args.steps, 20),
                                           args.warmup)
+    if args.prefill:
+        Ts = [int(t) for t in args.prefill.split(",") if t]
+        out["moe_prefill_q4"] = run_prefill(3, Ts, args.decode_layers, 10, 2)
     print(json.dumps(out), flush=True)
 
 

@@ -184,6 +184,11 @@ moe_status moe_expf_dev(const float* x, float* y, size_t n);
 /* Verification hook: y[i] = expf(bits_as_float(start_bits + i)), so that all
  * 2^32 inputs can be checked against the host libm without uploading them. */
 moe_status moe_expf_bits_dev(uint32_t start_bits, float* y, size_t n);
+/* Verification hook: the epilogue division of every int32 dot by 127.0f
+ * (dtype 2) or 7.0f (dtype 3) as the kernels compute it (kernels.c:71,
+ * :125), compared with the IEEE quotient on all 2^32 inputs; writes the
+ * number of mismatching results (0 expected) to *mismatches (host). */
+moe_status moe_selfcheck_qdot_dev(int dtype, unsigned long long* mismatches);
 
 /* Synthetic data: out[i] ~ N(mean, std^2), counter-based (seed, i) -> value. */
 moe_status moe_fill_normal_dev(float* out, size_t n, uint64_t seed, float mean, float stdv);

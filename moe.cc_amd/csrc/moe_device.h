@@ -73,11 +73,23 @@ __device__ __forceinline__ uint32_t group_sum_u32(uint32_t v) {
   return v;
 }
 
+// Correctly rounded x / d for x = (float) of an int32 and d = 127 or 7:
+// q = RN(x * RN(1/d)), one exact remainder r = x - q*d (fma), q + r * RN(1/d)
+// rounded once (Markstein's correction step).  Equal to the IEEE quotient for
+// every int32 x and both divisors (exhaustive check on the device:
+// moe_selfcheck_qdot_dev; on the host the same identity holds for all 2^32
+// inputs).  Three operations instead of a full division sequence.
+__device__ __forceinline__ float div_int_by_const(float x, float d) {
+  const float inv = 1.0f / d;   // folded for the constant divisors
+  const float q = x * inv;
+  const float r = __builtin_fmaf(-q, d, x);
+  return __builtin_fmaf(r, inv, q);
+}
+
 // kernels.c:71 / kernels.c:125 epilogue: ((float)dot / div) * scale, each
-// operation rounded on its own (IEEE division).
+// operation rounded on its own.
 __device__ __forceinline__ float qdot_epilogue(uint32_t dot, float div, float scale) {
-  float f = (float)(int32_t)dot;
-  f = f / div;
+  const float f = div_int_by_const((float)(int32_t)dot, div);
   return f * scale;
 }
 

@@ -244,18 +244,28 @@ __device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Columns per step and slices per step of one lane group (see file header).
+// Columns per step, 16-column slices per lane group, and 16-byte B units
+// per (pair, limb) and step (see the file header for the column order).
 template <bool Q4> struct Step {
-  static constexpr int COLS = Q4 ? 256 : 128;   // columns per step
-  static constexpr int SL = Q4 ? 4 : 2;         // 16-column slices per lane group
+  static constexpr int COLS = Q4 ? 256 : 128;
+  static constexpr int SL = Q4 ? 4 : 2;
+  static constexpr int UPS = 4 * SL;
 };
 
+// B (activation) columns live in LDS, for the up to 64 pairs of a pass:
+// [slot][limb][16-column unit][16 bytes], slot stride NL * kch + 16 bytes
+// (the padding starts consecutive slots 4 banks apart), kch columns at a
+// time.  kMmaLds bytes hold all 2048 columns of one limb for 64 slots.
+constexpr int kMmaLds = 64 * (2048 + 16);
+// Row stride (uint32) of the gate/up dots in LDS: rows 4 apart (the lane
+// groups of an MFMA result) land 16 banks apart.
+constexpr int kDotRow = 68;
+static_assert(2 * kMmaRows * kDotRow * 4 <= kMmaLds, "dots fit the staging area");
 // Weight fragment of one step for one matrix: 32 bytes of the lane's row.
 struct WFrag {
   u32x4 w[2];
 };
 
-template <bool Q4>
 __device__ __forceinline__ WFrag load_wfrag(const uint8_t* row, int step, int g) {
   // Q8: columns step*128 + 32g .. +31 = bytes at the same offset;
   // Q4: columns step*256 + 64g .. +63 = bytes step*128 + 32g .. +31
@@ -286,60 +296,152 @@ __device__ __forceinline__ v4i a_slice(const WFrag& f, int s) {
   return r;
 }
 
-// B operand of slice s, limb l, from one activation table (K columns).
+// 16-byte B unit c (columns 16c .. 16c + 15) of limb l of one activation
+// table with K columns: Q8 plane bytes 16c .. 16c + 15; Q4 the 8 even-plane
+// bytes at 8c, then the 8 odd-plane bytes of the same columns.
+// The table pointers come from LDS, so the compiler cannot tell they are
+// global memory; the loads say so (global loads, not flat ones, which would
+// also hold up every LDS wait).
+typedef __attribute__((address_space(1))) const uint8_t gbyte;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
 template <bool Q4>
-__device__ __forceinline__ v4i b_slice(const uint8_t* tab, int K, int l, int step, int g, int s) {
-  const uint8_t* plane = reinterpret_cast<const uint8_t*>(act_plane(tab, K, l));
-  v4i r;
+__device__ __forceinline__ u32x4 b_unit_load(const uint8_t* tab, int K, int l, int c) {
+  gbyte* plane = (gbyte*)(reinterpret_cast<const uint8_t*>(act_plane(tab, K, l)));
   if constexpr (!Q4) {
-    const uint4 v = *reinterpret_cast<const uint4*>(plane + (size_t)step * 128 + 32 * g + 16 * s);
-    r[0] = (int)v.x; r[1] = (int)v.y; r[2] = (int)v.z; r[3] = (int)v.w;
+    return *(__attribute__((address_space(1))) const u32x4*)(plane + (size_t)c * 16);
   } else {
-    const int c0 = step * 256 + 64 * g + 16 * s;
-    const uint2 e = *reinterpret_cast<const uint2*>(plane + c0 / 2);
-    const uint2 o = *reinterpret_cast<const uint2*>(plane + K / 2 + c0 / 2);
-    r[0] = (int)e.x; r[1] = (int)e.y; r[2] = (int)o.x; r[3] = (int)o.y;
+    const u32x2 e = *(__attribute__((address_space(1))) const u32x2*)(plane + (size_t)c * 8);
+    const u32x2 o = *(__attribute__((address_space(1))) const u32x2*)(plane + K / 2 + (size_t)c * 8);
+    u32x4 r;
+    r[0] = e[0]; r[1] = e[1]; r[2] = o[0]; r[3] = o[1];
+    return r;
   }
-  return r;
 }
 
-// acc[m][tt][l] += W_m[rows] x tables[tt] over all K columns, for NM weight
-// matrices (gate, up) sharing the activations, nt live 16-pair tiles (of NT)
-// and NL limbs.  W[m] points at this lane's row.  Weights are prefetched
-// one step ahead.
-template <bool Q4, int NM, int NL, int NT>
-__device__ __forceinline__ void mma_rows(const uint8_t* const W[NM], int K,
-                                         const uint8_t* const tab[NT], int nt,
-                                         v4i acc[NM][NT][NL]) {
-  const int g = (threadIdx.x % kWave) / 16;
-  const int nsteps = K / Step<Q4>::COLS;
-  WFrag cur[NM], nxt[NM];
+// n / d and n % d for n * d < 2^32 (both small here): q = hi32(n * m) with
+// m = ceil(2^32 / d), exact in that range.
+struct DivMod {
+  uint32_t d, m;
+  __device__ explicit DivMod(uint32_t dd) : d(dd), m((uint32_t)((0xFFFFFFFFull + dd) / dd)) {}
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return __umulhi(n, m); }
+};
+
+// Copies columns [c0, c0 + kch) of the first nlive slots' tables (NL limbs)
+// into the LDS layout above; 8 loads in flight per thread.
+template <bool Q4, int NL>
+__device__ __forceinline__ void stage_b(uint8_t* bbuf, const uint8_t* const* slot_tab, int nlive,
+                                        int K, int c0, int kch, int slot_bytes) {
+  const int upl = kch / 16;                 // units per limb
+  const int ups = NL * upl;                 // units per slot
+  const int total = nlive * ups;
+  const DivMod by_ups((uint32_t)ups), by_upl((uint32_t)upl);
+  for (int base = 0; base < total; base += kMmaThreads * 8) {
+    u32x4 r[8];
+    int off[8];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) cur[m] = load_wfrag<Q4>(W[m], 0, g);
-  for (int st = 0; st < nsteps; ++st) {
-    if (st + 1 < nsteps) {
-#pragma unroll
-      for (int m = 0; m < NM; ++m) nxt[m] = load_wfrag<Q4>(W[m], st + 1, g);
+    for (int i = 0; i < 8; ++i) {
+      const int u = min(base + (int)threadIdx.x + kMmaThreads * i, total - 1);
+      const int p = (int)by_ups.div((uint32_t)u), rem = u - p * ups;
+      const int l = (int)by_upl.div((uint32_t)rem), c = rem - l * upl;
+      r[i] = b_unit_load<Q4>(slot_tab[p], K, l, c0 / 16 + c);
+      off[i] = p * slot_bytes + l * kch + c * 16;
     }
 #pragma unroll
-    for (int s = 0; s < Step<Q4>::SL; ++s) {
-      v4i av[NM];
-#pragma unroll
-      for (int m = 0; m < NM; ++m) av[m] = a_slice<Q4>(cur[m], s);
-#pragma unroll
-      for (int tt = 0; tt < NT; ++tt) {
-        if (tt >= nt) break;
-#pragma unroll
-        for (int l = 0; l < NL; ++l) {
-          const v4i bv = b_slice<Q4>(tab[tt], K, l, st, g, s);
-#pragma unroll
-          for (int m = 0; m < NM; ++m) acc[m][tt][l] = mfma16(av[m], bv, acc[m][tt][l]);
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m) cur[m] = nxt[m];
+    for (int i = 0; i < 8; ++i)
+      if (base + (int)threadIdx.x + kMmaThreads * i < total)
+        *reinterpret_cast<u32x4*>(bbuf + off[i]) = r[i];
   }
+}
+
+// One step (COLS columns) of a pass for ring slot R: at the first step of a
+// later chunk, restage B (block-wide, between barriers); issue the weight
+// loads of step st + 2 into the slot consumed at step st - 1 (past the last
+// step, the last step's bytes again, just loaded and cached, so that every
+// step has the same loads in flight); then the MFMAs of step st from slot R
+// and the staged B columns.  The ring slot is a template argument so that every
+// slot keeps its registers: the only wait before the MFMAs is for slot R's
+// own loads.
+template <bool Q4, int NM, int NL, int NT, int R>
+__device__ __forceinline__ void mma_step(WFrag (&wb)[3][NM], const uint8_t* const W[NM], int st,
+                                         int nsteps, int g, const uint8_t* B, int cs,
+                                         int slot_bytes, int kch, const uint8_t* const* slot_tab,
+                                         int nlive, int K, uint8_t* bbuf, v4i (&acc)[NM][NT][NL]) {
+  constexpr int SL = Step<Q4>::SL, UPS = Step<Q4>::UPS, COLS = Step<Q4>::COLS;
+  const int sc = st % cs;
+  if (sc == 0 && st > 0) {
+    __syncthreads();   // the previous chunk is consumed
+    stage_b<Q4, NL>(bbuf, slot_tab, nlive, K, st * COLS, kch, slot_bytes);
+    __syncthreads();
+  }
+  const int stl = st + 2 < nsteps ? st + 2 : nsteps - 1;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) wb[(R + 2) % 3][m] = load_wfrag(W[m], stl, g);
+  const uint8_t* Bst = B + sc * UPS * 16;
+#pragma unroll
+  for (int s = 0; s < SL; ++s) {
+    v4i bv[NT][NL];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int l = 0; l < NL; ++l)
+        bv[tt][l] = *reinterpret_cast<const v4i*>(Bst + tt * 16 * slot_bytes + l * kch + s * 16);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const v4i av = a_slice<Q4>(wb[R][m], s);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int l = 0; l < NL; ++l) acc[m][tt][l] = mfma16(av, bv[tt][l], acc[m][tt][l]);
+    }
+    // keep the next slice's LDS reads after these MFMAs (bounds live B registers)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// One pass of a block over up to 16*NT pairs (slot p's activation table at
+// slot_tab[p], p < nlive): acc[m][tt][l] = sum over all K columns of
+// W_m[lane's row] x table[tt*16 + lane % 16], per limb l.  The activation
+// columns are staged in LDS chunk by chunk (as many columns as fit, all K
+// of them for one limb); between the two barriers of a chunk the waves run
+// free, each streaming its weight rows through a 3-step register ring.
+// Every thread of the block calls this.
+template <bool Q4, int NM, int NL, int NT>
+__device__ __forceinline__ void mma_pass(const uint8_t* const W[NM], int K,
+                                         const uint8_t* const* slot_tab, int nlive,
+                                         uint8_t* bbuf, v4i (&acc)[NM][NT][NL]) {
+  constexpr int COLS = Step<Q4>::COLS, SL = Step<Q4>::SL;
+  const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+  const int nsteps = K / COLS;
+  // steps per chunk: the largest divisor of nsteps whose columns fit
+  int cs = nsteps;
+  while (cs > 1 && (nsteps % cs != 0 || 64 * (NL * cs * COLS + 16) > kMmaLds)) --cs;
+  const int kch = cs * COLS, slot_bytes = NL * kch + 16;
+  const uint8_t* B = bbuf + j * slot_bytes + g * SL * 16;
+  // chunk 0 is staged before the weight ring starts, so that waiting for
+  // the staging loads does not wait for weight loads
+  stage_b<Q4, NL>(bbuf, slot_tab, nlive, K, 0, kch, slot_bytes);
+  WFrag wb[3][NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    wb[0][m] = load_wfrag(W[m], 0, g);
+    wb[1][m] = load_wfrag(W[m], nsteps > 1 ? 1 : 0, g);
+  }
+  __syncthreads();
+  // three steps per iteration, step st reading ring slot st % 3; the loop
+  // is left only between steps, so the back edge always sees the same loads
+  for (int st = 0;;) {
+    mma_step<Q4, NM, NL, NT, 0>(wb, W, st, nsteps, g, B, cs, slot_bytes, kch, slot_tab, nlive, K,
+                                bbuf, acc);
+    if (++st >= nsteps) break;
+    mma_step<Q4, NM, NL, NT, 1>(wb, W, st, nsteps, g, B, cs, slot_bytes, kch, slot_tab, nlive, K,
+                                bbuf, acc);
+    if (++st >= nsteps) break;
+    mma_step<Q4, NM, NL, NT, 2>(wb, W, st, nsteps, g, B, cs, slot_bytes, kch, slot_tab, nlive, K,
+                                bbuf, acc);
+    if (++st >= nsteps) break;
+  }
+  __syncthreads();   // LDS free for the next pass
 }
 
 template <int NL>
@@ -348,11 +450,6 @@ __device__ __forceinline__ uint32_t limb_dot(const v4i* acc_l, int r) {
 #pragma unroll
   for (int l = 0; l < NL; ++l) v[l] = acc_l[l][r];
   return combine_limbs<NL == 3 ? 4 : NL>(v);
-}
-
-// Pair of column j of tile tt in a pass over an expert's pairs, or -1.
-__device__ __forceinline__ int pass_pair(const int* perm, int first, int n, int idx) {
-  return idx < n ? perm[first + idx] : -1;
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -367,25 +464,19 @@ struct GateUpGArgs {
   int nseg;
 };
 
-// Tiles tile0 .. tile0 + NT - 1 of a pass over up to 64 of expert e's pairs.
+// Pairs base .. base + n - 1 (n <= 16*NT) of a pass over expert e's pairs
+// (tables in slot_tab[]), NT 16-pair tiles: the gate and up dots of this
+// block's 128 rows, written to LDS as dots[m][row][pair] (uint32, rows
+// kDotRow apart) once the pass has released the staging area.
 template <bool Q4, int NL, int NT>
-__device__ void gate_up_pass(const GateUpGArgs& a, int e, int first, int n, int tile0,
-                             uint32_t xsum_lane, int* red_nl, unsigned* red_sum) {
+__device__ void gate_up_mma(const GateUpGArgs& a, int e, const uint8_t* const* slot_tab, int base,
+                            int n, uint8_t* bbuf) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 16, j = lane % 16;
   const int rowA = blockIdx.x * kMmaRows + wave * 16 + j;   // this lane's A row
   const int rowA_c = rowA < a.dff ? rowA : a.dff - 1;
   const uint8_t* W[2] = {a.gq + ((size_t)e * a.dff + rowA_c) * a.rb,
                          a.uq + ((size_t)e * a.dff + rowA_c) * a.rb};
-  const int nt = min(NT, (n - tile0 * 16 + 15) / 16);
-  const uint8_t* tab[NT];
-  int pair[NT];
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    pair[tt] = pass_pair(a.perm, first, n, (tile0 + tt) * 16 + j);
-    const int q = pair[tt] >= 0 ? pair[tt] : a.perm[first];
-    tab[tt] = a.xtab + (size_t)(q / a.topk) * a.xtab_bytes;
-  }
   v4i acc[2][NT][NL];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -393,32 +484,76 @@ __device__ void gate_up_pass(const GateUpGArgs& a, int e, int first, int n, int 
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
       for (int l = 0; l < NL; ++l) acc[m][tt][l] = v4i{0, 0, 0, 0};
-  mma_rows<Q4, 2, NL, NT>(W, a.D, tab, nt, acc);
-  const float div = Q4 ? 7.0f : 127.0f;
-  const int rbase = blockIdx.x * kMmaRows + wave * 16 + 4 * g;   // rows of this lane's results
+  mma_pass<Q4, 2, NL, NT>(W, a.D, slot_tab + base, n, bbuf, acc);
+  uint32_t* dots = reinterpret_cast<uint32_t*>(bbuf);
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    if (tt >= nt) break;
-    const int q = pair[tt];
-    const int col = (tile0 + tt) * 16 + j;   // pair index within the pass
-    // activation sum of this column's token (Q4 offset correction)
-    const uint32_t xs = (uint32_t)__shfl((int)xsum_lane, col, kWave);
-    int nl = 1;
-    uint32_t hs = 0;
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dots[(m * kMmaRows + wave * 16 + 4 * g + r) * kDotRow + base + tt * 16 + j] =
+            limb_dot<NL>(acc[m][tt], r);
+}
+
+template <bool Q4>
+__device__ void gate_up_epilogue(const GateUpGArgs& a, int e, const int* pass_pair,
+                                 const uint32_t* xsum, int base, int n, const uint32_t* dots,
+                                 int* red_nl, unsigned* red_sum);
+
+// Live-tile dispatch: 1..4 tiles of 16 pairs; two-limb activations run at
+// most two tiles at a time and four-limb ones one tile (the accumulators
+// stay in registers).  Each sub-pass's dots go through LDS to the SwiGLU
+// epilogue before the next sub-pass restages LDS.
+template <bool Q4, int NL>
+__device__ __forceinline__ void gate_up_nt(const GateUpGArgs& a, int e, const int* pass_pair,
+                                           const uint8_t* const* slot_tab, const uint32_t* xsum,
+                                           int n, uint8_t* bbuf, int* red_nl, unsigned* red_sum) {
+  constexpr int MAXT = NL == 1 ? 4 : (NL == 2 ? 2 : 1);
+  for (int base = 0; base < n; base += 16 * MAXT) {
+    const int nb = min(n - base, 16 * MAXT);
+    const int nt = (nb + 15) / 16;
+    if (nt == 1 || MAXT == 1) gate_up_mma<Q4, NL, 1>(a, e, slot_tab, base, nb, bbuf);
+    else if (nt == 2 || MAXT == 2) gate_up_mma<Q4, NL, (MAXT < 2 ? MAXT : 2)>(a, e, slot_tab, base, nb, bbuf);
+    else if (nt == 3) gate_up_mma<Q4, NL, (MAXT < 3 ? MAXT : 3)>(a, e, slot_tab, base, nb, bbuf);
+    else gate_up_mma<Q4, NL, MAXT>(a, e, slot_tab, base, nb, bbuf);
+    __syncthreads();
+    gate_up_epilogue<Q4>(a, e, pass_pair, xsum, base, nb, reinterpret_cast<const uint32_t*>(bbuf),
+                         red_nl, red_sum);
+    __syncthreads();
+  }
+}
+
+// SwiGLU epilogue of pairs base .. base + n - 1 of a pass (:496-501): wave w
+// takes rows 16w .. 16w + 15 of the block, lane p the pass's pair p.  h = (g / (1 + expf(-g))) * u is
+// quantized for down, written into the pair's table, and the rows' limb
+// count and activation sum go to red_nl / red_sum.
+template <bool Q4>
+__device__ void gate_up_epilogue(const GateUpGArgs& a, int e, const int* pass_pair,
+                                 const uint32_t* xsum, int base, int n, const uint32_t* dots,
+                                 int* red_nl, unsigned* red_sum) {
+  const int p = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (p < base || p >= base + n) return;
+  const int q = pass_pair[p];
+  const uint32_t xs = xsum[p];
+  const float div = Q4 ? 7.0f : 127.0f;
+  uint8_t* tabq = a.htab + (size_t)q * a.htab_bytes;
+  int nl = 1;
+  uint32_t hs = 0;
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int rl = wave * 16 + 4 * r4;                 // local row of 4 consecutive
+    const int row0 = blockIdx.x * kMmaRows + rl;
+    if (row0 >= a.dff) break;
     uint32_t bytes[4][4];   // [limb][r]
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = rbase + r;
-      uint32_t dg = limb_dot<NL>(acc[0][tt], r);
-      uint32_t du = limb_dot<NL>(acc[1][tt], r);
+      uint32_t dg = dots[(rl + r) * kDotRow + p];
+      uint32_t du = dots[(kMmaRows + rl + r) * kDotRow + p];
       if (Q4) { dg -= 8u * xs; du -= 8u * xs; }
-      int32_t hv = 0;
-      if (q >= 0 && row < a.dff) {
-        const float gv = qdot_epilogue(dg, div, a.gs[(size_t)e * a.dff + row]);
-        const float uv = qdot_epilogue(du, div, a.us[(size_t)e * a.dff + row]);
-        const float h = silu_mul(gv, uv);
-        hv = f2i_trunc_x86(h * div);
-      }
+      const float gv = qdot_epilogue(dg, div, a.gs[(size_t)e * a.dff + row0 + r]);
+      const float uv = qdot_epilogue(du, div, a.us[(size_t)e * a.dff + row0 + r]);
+      const int32_t hv = f2i_trunc_x86(silu_mul(gv, uv) * div);
       const int nn = limbs_needed(hv);
       nl = nn > nl ? nn : nl;
       hs += (uint32_t)hv;
@@ -427,41 +562,32 @@ __device__ void gate_up_pass(const GateUpGArgs& a, int e, int first, int n, int 
 #pragma unroll
       for (int l = 0; l < 4; ++l) bytes[l][r] = b[l];
     }
-    if (q >= 0 && rbase < a.dff) {
-      uint8_t* tabq = a.htab + (size_t)q * a.htab_bytes;
 #pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        uint8_t* plane = reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.dff, l)));
-        if constexpr (!Q4) {
-          *reinterpret_cast<uint32_t*>(plane + rbase) =
-              pack4(bytes[l][0], bytes[l][1], bytes[l][2], bytes[l][3]);
-        } else {
-          *reinterpret_cast<uint16_t*>(plane + rbase / 2) =
-              (uint16_t)(bytes[l][0] | (bytes[l][2] << 8));
-          *reinterpret_cast<uint16_t*>(plane + a.dff / 2 + rbase / 2) =
-              (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
-        }
+    for (int l = 0; l < 4; ++l) {
+      uint8_t* plane = reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.dff, l)));
+      if constexpr (!Q4) {
+        *reinterpret_cast<uint32_t*>(plane + row0) =
+            pack4(bytes[l][0], bytes[l][1], bytes[l][2], bytes[l][3]);
+      } else {
+        *reinterpret_cast<uint16_t*>(plane + row0 / 2) = (uint16_t)(bytes[l][0] | (bytes[l][2] << 8));
+        *reinterpret_cast<uint16_t*>(plane + a.dff / 2 + row0 / 2) =
+            (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
       }
     }
-    // partial header of this block's rows for the column's pair: reduce the
-    // 4 lane groups, then the waves through LDS
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-      const int on = __shfl_xor(nl, off, kWave);
-      nl = on > nl ? on : nl;
-      hs += (uint32_t)__shfl_xor((int)hs, off, kWave);
-    }
-    if (g == 0 && q >= 0) {
-      atomicMax(&red_nl[col], nl);
-      atomicAdd(&red_sum[col], hs);
-    }
   }
+  atomicMax(&red_nl[p], nl);
+  atomicAdd(&red_sum[p], hs);
 }
 
 template <bool Q4>
 __global__ __launch_bounds__(kMmaThreads) void gate_up_grouped_kernel(GateUpGArgs a) {
+  extern __shared__ u32x4 lds_b[];
+  __shared__ int pass_pair[kPairsPerPass];
+  __shared__ const uint8_t* slot_tab[kPairsPerPass];
   __shared__ int red_nl[kPairsPerPass];
   __shared__ unsigned red_sum[kPairsPerPass];
+  __shared__ uint32_t pass_xsum[kPairsPerPass];
+  uint8_t* bbuf = reinterpret_cast<uint8_t*>(lds_b);
   const int e = blockIdx.y;
   const int n_all = a.ecount[e];
   if (n_all == 0) return;
@@ -484,19 +610,21 @@ __global__ __launch_bounds__(kMmaThreads) void gate_up_grouped_kernel(GateUpGArg
       const int on = __shfl_xor(nl, off, kWave);
       nl = on > nl ? on : nl;
     }
-    if (threadIdx.x < kPairsPerPass) { red_nl[threadIdx.x] = 1; red_sum[threadIdx.x] = 0; }
-    __syncthreads();
-    if (nl == 1) {
-      gate_up_pass<Q4, 1, 4>(a, e, first, n, 0, xsum, red_nl, red_sum);
-    } else if (nl == 2) {
-      gate_up_pass<Q4, 2, 4>(a, e, first, n, 0, xsum, red_nl, red_sum);
-    } else {   // four limbs: two tiles at a time keeps the accumulators in registers
-      gate_up_pass<Q4, 4, 2>(a, e, first, n, 0, xsum, red_nl, red_sum);
-      if (n > 32) gate_up_pass<Q4, 4, 2>(a, e, first, n, 2, xsum, red_nl, red_sum);
+    if (threadIdx.x < kPairsPerPass) {
+      const int i = threadIdx.x;
+      const int q = i < n ? a.perm[first + i] : -1;
+      pass_pair[i] = q;
+      slot_tab[i] = q >= 0 ? a.xtab + (size_t)(q / a.topk) * a.xtab_bytes : nullptr;
+      pass_xsum[i] = xsum;
+      red_nl[i] = 1;
+      red_sum[i] = 0;
     }
     __syncthreads();
+    if (nl == 1) gate_up_nt<Q4, 1>(a, e, pass_pair, slot_tab, pass_xsum, n, bbuf, red_nl, red_sum);
+    else if (nl == 2) gate_up_nt<Q4, 2>(a, e, pass_pair, slot_tab, pass_xsum, n, bbuf, red_nl, red_sum);
+    else gate_up_nt<Q4, 4>(a, e, pass_pair, slot_tab, pass_xsum, n, bbuf, red_nl, red_sum);
     if (threadIdx.x < n) {
-      const int q = a.perm[first + threadIdx.x];
+      const int q = pass_pair[threadIdx.x];
       uint32_t* pp = a.hpart + ((size_t)q * a.nseg + blockIdx.x) * 2;
       pp[0] = (uint32_t)red_nl[threadIdx.x];
       pp[1] = red_sum[threadIdx.x];
@@ -517,35 +645,27 @@ struct DownGArgs {
 };
 
 template <bool Q4, int NL, int NT>
-__device__ void down_pass(const DownGArgs& a, int e, int first, int n, int tile0,
-                          uint32_t hsum_lane) {
+__device__ void down_pass(const DownGArgs& a, int e, const int* pass_pair,
+                          const uint8_t* const* slot_tab, int base, int n, uint32_t hsum_lane,
+                          uint8_t* bbuf) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 16, j = lane % 16;
   const int rowA = blockIdx.x * kMmaRows + wave * 16 + j;
   const int rowA_c = rowA < a.D ? rowA : a.D - 1;
   const uint8_t* W[1] = {a.dq + ((size_t)e * a.D + rowA_c) * a.rb};
-  const int nt = min(NT, (n - tile0 * 16 + 15) / 16);
-  const uint8_t* tab[NT];
-  int pair[NT];
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    pair[tt] = pass_pair(a.perm, first, n, (tile0 + tt) * 16 + j);
-    const int q = pair[tt] >= 0 ? pair[tt] : a.perm[first];
-    tab[tt] = a.htab + (size_t)q * a.htab_bytes;
-  }
   v4i acc[1][NT][NL];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
     for (int l = 0; l < NL; ++l) acc[0][tt][l] = v4i{0, 0, 0, 0};
-  mma_rows<Q4, 1, NL, NT>(W, a.dff, tab, nt, acc);
+  mma_pass<Q4, 1, NL, NT>(W, a.dff, slot_tab + base, n, bbuf, acc);
   const float div = Q4 ? 7.0f : 127.0f;
   const int rbase = blockIdx.x * kMmaRows + wave * 16 + 4 * g;
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    if (tt >= nt) break;
-    const int q = pair[tt];
-    const uint32_t hs = (uint32_t)__shfl((int)hsum_lane, (tile0 + tt) * 16 + j, kWave);
+    const int col = base + tt * 16 + j;
+    const int q = tt * 16 + j < n ? pass_pair[col] : -1;
+    const uint32_t hs = (uint32_t)__shfl((int)hsum_lane, col, kWave);
     if (q < 0 || rbase >= a.D) continue;
     float yv[4];
 #pragma unroll
@@ -558,8 +678,27 @@ __device__ void down_pass(const DownGArgs& a, int e, int first, int n, int tile0
   }
 }
 
+template <bool Q4, int NL>
+__device__ __forceinline__ void down_nt(const DownGArgs& a, int e, const int* pass_pair,
+                                        const uint8_t* const* slot_tab, int n, uint32_t hsum,
+                                        uint8_t* bbuf) {
+  constexpr int MAXT = NL == 4 ? 2 : 4;
+  for (int base = 0; base < n; base += 16 * MAXT) {
+    const int nb = min(n - base, 16 * MAXT);
+    const int nt = (nb + 15) / 16;
+    if (nt == 1) down_pass<Q4, NL, 1>(a, e, pass_pair, slot_tab, base, nb, hsum, bbuf);
+    else if (nt == 2 || MAXT == 2) down_pass<Q4, NL, 2>(a, e, pass_pair, slot_tab, base, nb, hsum, bbuf);
+    else if (nt == 3) down_pass<Q4, NL, 3 < MAXT ? 3 : MAXT>(a, e, pass_pair, slot_tab, base, nb, hsum, bbuf);
+    else down_pass<Q4, NL, MAXT>(a, e, pass_pair, slot_tab, base, nb, hsum, bbuf);
+  }
+}
+
 template <bool Q4>
 __global__ __launch_bounds__(kMmaThreads) void down_grouped_kernel(DownGArgs a) {
+  extern __shared__ u32x4 lds_b[];
+  __shared__ int pass_pair[kPairsPerPass];
+  __shared__ const uint8_t* slot_tab[kPairsPerPass];
+  uint8_t* bbuf = reinterpret_cast<uint8_t*>(lds_b);
   const int e = blockIdx.y;
   const int n_all = a.ecount[e];
   if (n_all == 0) return;
@@ -584,14 +723,17 @@ __global__ __launch_bounds__(kMmaThreads) void down_grouped_kernel(DownGArgs a) 
       const int on = __shfl_xor(nl, off, kWave);
       nl = on > nl ? on : nl;
     }
-    if (nl == 1) {
-      down_pass<Q4, 1, 4>(a, e, first, n, 0, hsum);
-    } else if (nl == 2) {
-      down_pass<Q4, 2, 4>(a, e, first, n, 0, hsum);
-    } else {
-      down_pass<Q4, 4, 2>(a, e, first, n, 0, hsum);
-      if (n > 32) down_pass<Q4, 4, 2>(a, e, first, n, 2, hsum);
+    if (threadIdx.x < kPairsPerPass) {
+      const int i = threadIdx.x;
+      const int q = i < n ? a.perm[first + i] : -1;
+      pass_pair[i] = q;
+      slot_tab[i] = q >= 0 ? a.htab + (size_t)q * a.htab_bytes : nullptr;
     }
+    __syncthreads();
+    if (nl == 1) down_nt<Q4, 1>(a, e, pass_pair, slot_tab, n, hsum, bbuf);
+    else if (nl == 2) down_nt<Q4, 2>(a, e, pass_pair, slot_tab, n, hsum, bbuf);
+    else down_nt<Q4, 4>(a, e, pass_pair, slot_tab, n, hsum, bbuf);
+    __syncthreads();
   }
 }
 
@@ -625,13 +767,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *reinterpret_cast<float4*>(out + oi) = acc;
 }
 
-template <class T>
-moe_status galloc(T** p, size_t count) {
-  *p = nullptr;
-  if (count == 0) return MOE_OK;
-  return check_hip(hipMalloc((void**)p, count * sizeof(T)), "hipMalloc(grouped)");
-}
-
 bool is16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 template <int CT, int CE, int KC>
@@ -651,27 +786,27 @@ moe_status launch_router_tile(const RouterTileArgs& a, hipStream_t s) {
   return check_hip(hipGetLastError(), "router tile launch");
 }
 
+// Dynamic LDS above 64 KB needs the per-kernel attribute (set once).
+moe_status mma_lds_attributes() {
+  static bool done = false;
+  if (done) return MOE_OK;
+  const void* fns[4] = {(const void*)gate_up_grouped_kernel<true>, (const void*)down_grouped_kernel<true>,
+                        (const void*)gate_up_grouped_kernel<false>, (const void*)down_grouped_kernel<false>};
+  for (int i = 0; i < 4; ++i) {
+    moe_status st = check_hip(hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  kMmaLds), "grouped LDS attribute");
+    if (st) return st;
+  }
+  done = true;
+  return MOE_OK;
+}
+
 }  // namespace
 
 bool grouped_ok(const LayerDev* L) {
   const int step = L->dtype == 3 ? 256 : 128;
   return L->D % step == 0 && L->dff % step == 0 && L->D % 128 == 0 && L->E <= kGroupThreads &&
          is16(L->router_w);
-}
-
-moe_status ensure_grouped_scratch(LayerDev* L, int T) {
-  // grown together with the decode scratch (capT), see ensure_scratch
-  moe_status st;
-  const size_t np = (size_t)T * L->topk;
-  if (!L->ecount && (st = galloc(&L->ecount, (size_t)L->E))) return st;
-  if (!L->eoff && (st = galloc(&L->eoff, (size_t)L->E))) return st;
-  if (L->perm) (void)hipFree(L->perm);
-  if (L->y) (void)hipFree(L->y);
-  L->perm = nullptr;
-  L->y = nullptr;
-  if ((st = galloc(&L->perm, np))) return st;
-  if ((st = galloc(&L->y, np * L->D))) return st;
-  return MOE_OK;
 }
 
 moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
@@ -711,15 +846,20 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
                  L->ecount, L->eoff, L->perm, L->xtab, act_table_bytes(L->D),
                  L->htab, act_table_bytes(L->dff), L->hpart, nseg};
   dim3 gg((unsigned)nseg, (unsigned)L->E);
-  if (q4) hipLaunchKernelGGL(gate_up_grouped_kernel<true>, gg, dim3(kMmaThreads), 0, s, ga);
-  else hipLaunchKernelGGL(gate_up_grouped_kernel<false>, gg, dim3(kMmaThreads), 0, s, ga);
+  if ((st = mma_lds_attributes())) return st;
+  if (q4)
+    hipLaunchKernelGGL(gate_up_grouped_kernel<true>, gg, dim3(kMmaThreads), kMmaLds, s, ga);
+  else
+    hipLaunchKernelGGL(gate_up_grouped_kernel<false>, gg, dim3(kMmaThreads), kMmaLds, s, ga);
   if ((st = check_hip(hipGetLastError(), "grouped gate/up launch"))) return st;
   // 6. down
   DownGArgs da{L->dq, L->ds, L->rbd, L->D, L->dff, L->ecount, L->eoff, L->perm,
                L->htab, act_table_bytes(L->dff), L->hpart, nseg, L->y};
   dim3 dg((unsigned)((L->D + kMmaRows - 1) / kMmaRows), (unsigned)L->E);
-  if (q4) hipLaunchKernelGGL(down_grouped_kernel<true>, dg, dim3(kMmaThreads), 0, s, da);
-  else hipLaunchKernelGGL(down_grouped_kernel<false>, dg, dim3(kMmaThreads), 0, s, da);
+  if (q4)
+    hipLaunchKernelGGL(down_grouped_kernel<true>, dg, dim3(kMmaThreads), kMmaLds, s, da);
+  else
+    hipLaunchKernelGGL(down_grouped_kernel<false>, dg, dim3(kMmaThreads), kMmaLds, s, da);
   if ((st = check_hip(hipGetLastError(), "grouped down launch"))) return st;
   // 7. ordered combine + residual
   dim3 cg((unsigned)((L->D / 4 + 255) / 256), (unsigned)T);

@@ -21,7 +21,8 @@ struct LayerDev {
   uint8_t* uq = nullptr; float* us = nullptr;
   uint8_t* dq = nullptr; float* ds = nullptr;   // [E][D][rbd], [E][D]
   int grouped_min_T = 0;               // 0: library default
-  // per-forward scratch, grown to the largest T seen
+  // per-forward scratch: views of the process-wide shared scratch, set by
+  // ensure_scratch before every forward
   int capT = 0;
   float* logits = nullptr;   // [T][E]
   int* idx = nullptr;        // [T][topk]
@@ -46,7 +47,6 @@ struct LayerDev {
 bool grouped_ok(const LayerDev* L);
 moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
                                  float* out, int32_t* idx_out, float* p_out);
-moe_status ensure_grouped_scratch(LayerDev* L, int T);
 
 // ---- routing: top-k by the insertion rule, softmax over the selection ----
 

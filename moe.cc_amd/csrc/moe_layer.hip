@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <type_traits>
 #include <vector>
@@ -455,29 +456,65 @@ moe_status dev_alloc(T** p, size_t count) {
   return check_hip(hipMalloc((void**)p, count * sizeof(T)), "hipMalloc(layer)");
 }
 
-moe_status ensure_scratch(LayerDev* L, int T) {
-  if (T <= L->capT) return MOE_OK;
-  moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
-  if (st) return st;
-  dfree(L->logits); dfree(L->idx); dfree(L->p); dfree(L->xtab); dfree(L->htab);
-  dfree(L->h); dfree(L->xn); dfree(L->xpart); dfree(L->hpart);
-  L->capT = 0;
-  const size_t np = (size_t)T * L->topk;
-  if ((st = dev_alloc(&L->logits, (size_t)T * L->E))) return st;
-  if ((st = dev_alloc(&L->idx, np))) return st;
-  if ((st = dev_alloc(&L->p, np))) return st;
-  if ((st = dev_alloc(&L->xtab, (size_t)T * act_table_bytes(L->D)))) return st;
-  if ((st = dev_alloc(&L->htab, np * act_table_bytes(L->dff)))) return st;
-  if ((st = dev_alloc(&L->h, np * L->dff))) return st;
-  if ((st = dev_alloc(&L->xn, (size_t)T * L->D))) return st;
-  const size_t nbx = (size_t)(L->E + kRouterExperts - 1) / kRouterExperts;
-  if ((st = dev_alloc(&L->xpart, (size_t)T * nbx * 2))) return st;
-  if ((st = dev_alloc(&L->hpart, np * (size_t)((L->dff + 7) / 8) * 2))) return st;
-  if (grouped_ok(L) && (st = ensure_grouped_scratch(L, T))) return st;
-  if (!L->counters) {
-    if ((st = dev_alloc(&L->counters, 1))) return st;
-    if ((st = check_hip(hipMemsetAsync(L->counters, 0, 4, stream()), "counter init"))) return st;
+// Per-forward scratch is shared by every layer of the process: forwards are
+// enqueued on the one library stream under g_layer_mu, so they never overlap
+// on the device.  Each buffer grows to the largest need seen (after the
+// stream drains) and is kept until the process ends.
+struct ScratchBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+struct SharedScratch {
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, xpart, hpart, ecount, eoff, perm, y;
+  unsigned* counters = nullptr;   // router last-block counter, zero between launches
+};
+SharedScratch g_scratch;
+std::mutex g_layer_mu;
+
+moe_status grow(ScratchBuf& b, size_t need, bool* synced) {
+  if (need <= b.bytes) return MOE_OK;
+  if (!*synced) {
+    moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
+    if (st) return st;
+    *synced = true;
   }
+  dfree(b.p);
+  b.p = nullptr;
+  b.bytes = 0;
+  const size_t cap = need + need / 4;
+  moe_status st = check_hip(hipMalloc(&b.p, cap), "hipMalloc(layer scratch)");
+  if (st) return st;
+  b.bytes = cap;
+  return MOE_OK;
+}
+
+moe_status ensure_scratch(LayerDev* L, int T) {
+  SharedScratch& S = g_scratch;
+  bool synced = false;
+  moe_status st;
+  const size_t np = (size_t)T * L->topk;
+  const size_t nbx = (size_t)(L->E + kRouterExperts - 1) / kRouterExperts;
+  if ((st = grow(S.logits, (size_t)T * L->E * 4, &synced)) || (st = grow(S.idx, np * 4, &synced)) ||
+      (st = grow(S.p, np * 4, &synced)) ||
+      (st = grow(S.xtab, (size_t)T * act_table_bytes(L->D), &synced)) ||
+      (st = grow(S.htab, np * act_table_bytes(L->dff), &synced)) ||
+      (st = grow(S.h, np * L->dff * 4, &synced)) || (st = grow(S.xn, (size_t)T * L->D * 4, &synced)) ||
+      (st = grow(S.xpart, (size_t)T * nbx * 8, &synced)) ||
+      (st = grow(S.hpart, np * (size_t)((L->dff + 7) / 8) * 8, &synced)))
+    return st;
+  if (grouped_ok(L) &&
+      ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
+       (st = grow(S.perm, np * 4, &synced)) || (st = grow(S.y, np * L->D * 4, &synced))))
+    return st;
+  if (!S.counters) {
+    if ((st = dev_alloc(&S.counters, 1))) return st;
+    if ((st = check_hip(hipMemsetAsync(S.counters, 0, 4, stream()), "counter init"))) return st;
+  }
+  L->logits = (float*)S.logits.p; L->idx = (int*)S.idx.p; L->p = (float*)S.p.p;
+  L->xtab = (uint8_t*)S.xtab.p; L->htab = (uint8_t*)S.htab.p; L->h = (float*)S.h.p;
+  L->xn = (float*)S.xn.p; L->xpart = (uint32_t*)S.xpart.p; L->hpart = (uint32_t*)S.hpart.p;
+  L->ecount = (int*)S.ecount.p; L->eoff = (int*)S.eoff.p; L->perm = (int*)S.perm.p;
+  L->y = (float*)S.y.p; L->counters = S.counters;
   L->capT = T;
   return MOE_OK;
 }
@@ -630,9 +667,7 @@ moe_status upload(void* dst, const void* src, size_t bytes, int on_device) {
 void free_layer(LayerDev& L) {
   dfree(L.router_w); dfree(L.router_b); dfree(L.rms2_w);
   dfree(L.gq); dfree(L.gs); dfree(L.uq); dfree(L.us); dfree(L.dq); dfree(L.ds);
-  dfree(L.logits); dfree(L.idx); dfree(L.p); dfree(L.xtab); dfree(L.htab);
-  dfree(L.h); dfree(L.xn); dfree(L.xpart); dfree(L.hpart); dfree(L.counters);
-  dfree(L.ecount); dfree(L.eoff); dfree(L.perm); dfree(L.y);
+  // scratch pointers belong to the shared per-process scratch
 }
 
 }  // namespace
@@ -731,6 +766,7 @@ moe_status moe_layer_forward(moe_layer* layer, const float* x_norm, const float*
   if (st) return st;
   if (!layer || !x_norm || !out) return set_error(MOE_ERR_ARG, "layer_forward: null argument");
   if (T < 0) return set_error(MOE_ERR_ARG, "layer_forward: T < 0");
+  std::lock_guard<std::mutex> lk(g_layer_mu);
   return layer_forward(&layer->L, x_norm, x_resid, T, out, idx_out, p_out);
 }
 
@@ -741,6 +777,7 @@ moe_status moe_block_forward(moe_layer* layer, const float* x, int T, float* out
   if (T < 0) return set_error(MOE_ERR_ARG, "block_forward: T < 0");
   LayerDev* L = &layer->L;
   if (T == 0) return MOE_OK;
+  std::lock_guard<std::mutex> lk(g_layer_mu);
   if ((st = ensure_scratch(L, T))) return st;
   if ((st = rmsnorm_dev(x, L->rms2_w, L->xn, T, L->D, eps))) return st;
   return layer_forward(L, L->xn, x, T, out, nullptr, nullptr);

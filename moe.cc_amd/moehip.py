@@ -82,6 +82,7 @@ _SIGS = {
     "moe_silu_mul_dev": (_I, [_P, _P, _P, _SZ]),
     "moe_expf_dev": (_I, [_P, _P, _SZ]),
     "moe_expf_bits_dev": (_I, [ctypes.c_uint32, _P, _SZ]),
+    "moe_selfcheck_qdot_dev": (_I, [_I, ctypes.POINTER(ctypes.c_ulonglong)]),
     "moe_fill_normal_dev": (_I, [_P, _SZ, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
     "moe_quantize_rows_dev": (_I, [_I, _P, ctypes.c_longlong, _I, _P, _P]),
     "moe_layer_create": (_I, [_P, _P, ctypes.POINTER(_P)]),

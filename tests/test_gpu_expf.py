@@ -2,6 +2,7 @@
 SiLU*up equals the reference formula bit for bit (test_model_trace.c:229-236,
 :500).  The host side of the comparison is the oracle's libm call, run in
 threads over 2^26-input chunks."""
+import ctypes
 import concurrent.futures as cf
 
 import numpy as np
@@ -53,3 +54,12 @@ def test_silu_mul_matches_oracle(moehip):
     want = (O.silu(g) * u).astype(np.float32)
     same = (bits(h) == bits(want)) | (np.isnan(h) & np.isnan(want))
     assert same.all()
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_epilogue_division_exhaustive(moehip, dtype):
+    """The kernels' (float)dot / 127.0f (or 7.0f) equals the IEEE quotient for
+    every int32 dot (kernels.c:71, :125)."""
+    bad = ctypes.c_ulonglong(123)
+    moehip.check(moehip.lib().moe_selfcheck_qdot_dev(dtype, ctypes.byref(bad)), "selfcheck")
+    assert bad.value == 0
