@@ -364,6 +364,119 @@ def run_prefill(dtype, Ts, n_layers, steps, warmup):
     return res
 
 
+QWEN3_30B_A3B = dict(D=2048, L=48, hd=128, nq=32, nkv=4, dff=768, E=128, top_k=8, V=151936)
+
+
+def model_decode_bytes(c, ctx, dtype=3):
+    """Algorithmic bytes of one decode token at context length ctx: every
+    dense weight once (q/k/v/o, norms, router, lm_head), the 8 routed
+    experts of every layer, the embedding row, and the K/V cache read."""
+    D, L, hd, nq, nkv, V = c["D"], c["L"], c["hd"], c["nq"], c["nkv"], c["V"]
+    attn = (nq + 2 * nkv) * hd * D * 4 + D * nq * hd * 4
+    norms = (2 * D + 2 * hd) * 4
+    router = c["E"] * D * 4
+    experts = c["top_k"] * expert_bytes(dtype, D, c["dff"])
+    kv = 2 * nkv * ctx * hd * 4
+    return L * (attn + norms + router + experts + kv) + V * D * 4 + 2 * D * 4
+
+
+def run_model(args):
+    """the 48-layer Qwen3-30B-A3B-shaped model, random init
+    (N(0, 0.02^2), norms 1, Q4 experts), a prompt of 512 uniform-random ids,
+    then greedy decode steps with a 2048-position fp32 KV cache."""
+    M.init(0)
+    c = QWEN3_30B_A3B
+    cfg = M.qwen_config(c["D"], c["L"], c["hd"], c["nq"], c["nkv"], c["dff"], c["E"], c["top_k"],
+                        c["V"])
+    t0 = time.perf_counter()
+    model = M.Model.synthetic(cfg, expert_dtype=3, untied_head=True, seed=2024, std=0.02,
+                              max_seq=2048)
+    log(f"[bench] model built in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(512)
+    prompt = rng.integers(0, c["V"], args.model_prompt).astype(np.int32)
+    # warm-up run (kernel loading, scratch growth), then the measured one
+    model.generate(prompt[:16], 4)
+    ids, ms_p, ms_d = model.generate(prompt, args.model_steps + 1)
+    steps = args.model_steps
+    ctx_avg = args.model_prompt + steps / 2
+    per_tok = model_decode_bytes(c, ctx_avg)
+    res = {"prompt_tokens": int(args.model_prompt), "decode_steps": steps,
+           "prefill_ms": round(ms_p, 2), "prefill_tok_s": round(args.model_prompt / (ms_p * 1e-3), 1),
+           "decode_ms_total": round(ms_d, 2), "decode_ms_per_token": round(ms_d / steps, 3),
+           "decode_tok_s": round(steps / (ms_d * 1e-3), 2),
+           "algorithmic_bytes_per_token": int(per_tok),
+           "decode_GBs": round(per_tok * steps / (ms_d * 1e-3) / 1e9, 1),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
+           "generated_head": ids[:8].tolist(),
+           "arithmetic": "bit-identical to the reference (sequential fp32 chains, exact integer "
+                         "expert dots)"}
+    model.close()
+    log(f"[bench] model decode: {res}")
+    return res
+
+
+def model_cpu_baseline(budget_s: float):
+    """The oracle's KV-cached restatement (oracle/model_oracle.c, the
+    reference's loops) on one host thread: one full-size layer's decode
+    step at context 512 and the 151936-row head, timed separately and
+    combined as 48 layers + head per token (the full model does not fit a
+    bounded CPU sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    c = QWEN3_30B_A3B
+    D, hd, nq, nkv, dff, E, V = c["D"], c["hd"], c["nq"], c["nkv"], c["dff"], c["E"], c["V"]
+    rng = np.random.default_rng(7)
+
+    def w(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
+
+    ex = O.ExpertSet(3, rng.integers(0, 256, (E, dff, D // 2), dtype=np.uint8),
+                     np.full((E, dff), 1e-3, np.float32),
+                     rng.integers(0, 256, (E, dff, D // 2), dtype=np.uint8),
+                     np.full((E, dff), 1e-3, np.float32),
+                     rng.integers(0, 256, (E, D, dff // 2), dtype=np.uint8),
+                     np.full((E, D), 1e-3, np.float32), D, dff)
+    lw = {"Wq": w(nq * hd, D), "Wk": w(nkv * hd, D), "Wv": w(nkv * hd, D), "Wo": w(D, nq * hd),
+          "q_norm": np.ones(hd, np.float32), "k_norm": np.ones(hd, np.float32),
+          "rms1_w": np.ones(D, np.float32), "rms2_w": np.ones(D, np.float32), "router_w": w(E, D)}
+    keep = []
+
+    def ptr(a):
+        if a is None:
+            return None
+        keep.append(a)
+        return a.ctypes.data
+
+    layer = O.OrcLayer(*[ptr(lw.get(k)) for k in (
+        "Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm", "k_norm", "rms1_w", "rms2_w",
+        "router_w", "router_b")], ctypes.addressof(ex.Wg), ctypes.addressof(ex.Wu),
+        ctypes.addressof(ex.Wd))
+    cfg = O.OrcConfig(D, 1, hd, nq, nkv, dff, E, 8, V, 1, 1e7, 1e-6)
+    ctx, max_seq = 512, 520
+    kc = rng.standard_normal((nkv, max_seq, hd), dtype=np.float32)
+    vc = rng.standard_normal((nkv, max_seq, hd), dtype=np.float32)
+    x = rng.standard_normal((1, D), dtype=np.float32)
+    n_layer, t_layer = 0, 0.0
+    while t_layer < budget_s * 0.6:
+        xx = x.copy()
+        t0 = time.perf_counter()
+        O.orc().orc_layer_rows(ctypes.byref(cfg), ctypes.byref(layer), xx.ctypes.data, 1, ctx,
+                               kc.ctypes.data, vc.ctypes.data, max_seq)
+        t_layer += time.perf_counter() - t0
+        n_layer += 1
+    head = w(V, D)
+    out = np.empty((1, V), np.float32)
+    t0 = time.perf_counter()
+    O.orc().orc_matmul_f32(x.ctypes.data, head.ctypes.data, out.ctypes.data, 1, V, D)
+    t_head = time.perf_counter() - t0
+    per_token = c["L"] * t_layer / n_layer + t_head
+    return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_layer} decode steps of one full-size layer at context {ctx} "
+                      f"({t_layer / n_layer * 1e3:.1f} ms each) and one lm_head product "
+                      f"({t_head * 1e3:.1f} ms), per token = 48 layers + head, 1 thread of "
+                      f"{os.cpu_count()} host cores"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -378,6 +491,9 @@ def main():
     ap.add_argument("--decode-layers", type=int, default=6)
     ap.add_argument("--prefill", default="128,512,2048",
                     help="also time one Q4 MoE prefill layer at these T (configs[3]); '' to skip")
+    ap.add_argument("--model-steps", type=int, default=256,
+                    help="greedy decode steps of the 48-layer model (configs[4]); 0 to skip")
+    ap.add_argument("--model-prompt", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the expert path on a single MI355X "
@@ -397,6 +513,11 @@ def main():
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
         out["moe_prefill_q4"] = run_prefill(3, Ts, args.decode_layers, 10, 2)
+    if args.model_steps > 0:
+        out["model_decode_q4"] = run_model(args)
+        if not args.no_cpu:
+            log("[bench] model cpu baseline ...")
+            out["model_decode_q4"]["cpu_baseline"] = model_cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

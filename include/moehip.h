@@ -77,6 +77,14 @@ typedef struct {
   QuantizedWeight* Wd_q;
   int experts_quantized;
 } QwenLayerWeights;
+
+/* model.h:60-69; lm_head NULL = tied to tok_emb */
+typedef struct {
+  const float* tok_emb;
+  const float* final_norm_w;
+  const float* lm_head;
+  QwenLayerWeights* layers;
+} QwenWeights;
 #endif
 
 /* ==== 1. drop-in ==================================================== */
@@ -238,6 +246,55 @@ moe_status moe_rmsnorm_dev(const float* x, const float* w, float* y, int T, int 
  * outputs h [T*top_k x d_ff] and expert outputs y [T*top_k x D] (for tests). */
 moe_status moe_layer_debug_buffers(moe_layer* layer, const float** logits, const float** h,
                                    const float** y);
+
+/* ---- the whole model (test_model_trace.c:526-579) with a KV cache ---- */
+typedef struct moe_model moe_model;
+
+/* Uploads a model from the reference's structures (model.h:9-69, filled by
+ * load_all_weights model.h:107-323); host pointers, copied.  Experts must be
+ * quantized (Q8 or Q4).  max_seq: KV-cache length (1..16384).  Only causal
+ * attention (model.h:161 sets causal = 1). */
+moe_status moe_model_create(const QwenConfig* cfg, const QwenWeights* w, int max_seq,
+                            moe_model** out);
+/* Reads a QW3W file (all_q8.bin / all_q4.bin; io.c:193-285) and infers the
+ * config from its tensor shapes as load_all_weights does (model.h:110-163),
+ * then moe_model_create.  Replaces bin_load + load_all_weights + the
+ * reference's per-call host loops. */
+moe_status moe_model_load_file(const char* path, int max_seq, moe_model** out);
+/* A synthetic model generated on the device: every weight ~ N(0, std^2)
+ * (counter-based, seeded), norm weights 1, experts quantized with the
+ * exporter's rule (export.py:23-36), no biases; lm_head untied if
+ * untied_head.  For benchmarks at the real shape without a checkpoint. */
+moe_status moe_model_create_synthetic(const QwenConfig* cfg, int expert_dtype, int untied_head,
+                                      uint64_t seed, float stdv, int max_seq, moe_model** out);
+moe_status moe_model_destroy(moe_model* m);
+moe_status moe_model_config(const moe_model* m, QwenConfig* cfg);
+/* Empties the KV cache (next forward starts at position 0). */
+moe_status moe_model_reset(moe_model* m);
+/* Number of positions in the KV cache. */
+int moe_model_position(const moe_model* m);
+/* T new tokens at the current position (ids on the device if ids_on_device,
+ * else host ids checked against [0, vocab)); K/V appended to the cache.
+ * The last row's logits go to logits_dev [vocab] and its greedy choice (first
+ * index of the largest logit) to next_dev [1] (device int32); either may be
+ * NULL.  Bit-identical to the reference's last-row logits for the whole
+ * sequence so far. */
+moe_status moe_model_forward(moe_model* m, const int32_t* ids, int T, int ids_on_device,
+                             float* logits_dev, int32_t* next_dev);
+/* model_forward_f32 (test_model_trace.c:526-579) semantics: resets the
+ * cache, runs ids[0..T) (host), writes the last row's logits to out_last
+ * (host, [vocab]), softmaxed (softmax_rows, :260-272) if apply_softmax.
+ * Synchronous. */
+moe_status moe_model_forward_full(moe_model* m, const int32_t* ids, int T, int apply_softmax,
+                                  float* out_last);
+/* Greedy decoding on the device: resets the cache, runs the prompt (host
+ * ids), then n_new - 1 single-token steps, each fed the previous step's
+ * choice from device memory (no host round trip).  out_ids (host, n_new):
+ * the choice after the prompt and after every step.  ms_prompt / ms_decode
+ * (host, may be NULL): HIP-event time of the prompt and of the n_new - 1
+ * decode steps.  Synchronous. */
+moe_status moe_model_generate(moe_model* m, const int32_t* prompt, int n_prompt, int n_new,
+                              int32_t* out_ids, float* ms_prompt, float* ms_decode);
 
 /* Name of the kernel variant the GEMV entry points use for a shape. */
 const char* moe_gemv_variant(int dtype, int M, int N, int K);

@@ -15,6 +15,7 @@
 #include <unordered_map>
 
 #include "../../include/moehip.h"
+#include "dense.h"
 #include "moe_internal.h"
 #include "moe_lib.h"
 
@@ -294,7 +295,9 @@ moe_status moe_matmul_f32_dev(const float* A, const float* W, float* C, int M, i
   if (K < 0) K = 0;
   if (M == 0 || N == 0) return MOE_OK;
   if (!A || !W || !C) return set_error(MOE_ERR_ARG, "matmul_f32: null pointer");
-  return check_hip(launch_f32gemv(A, W, C, M, N, K, K, K, N, g_stream), "f32gemv launch");
+  if (K == 0) return check_hip(launch_f32gemv(A, W, C, M, N, K, K, K, N, g_stream), "f32gemv launch");
+  DenseArgs a{A, K, W, K, nullptr, nullptr, 0, C, N, M, N, K};
+  return dense_matmul(a, g_stream);
 }
 
 moe_status moe_matmul_adaptive_dev(const float* A, const float* W_fp32, const QuantizedWeight* W_q,

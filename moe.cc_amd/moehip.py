@@ -95,6 +95,18 @@ _SIGS = {
     "moe_rmsnorm_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
     "moe_layer_debug_buffers": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P),
                                      ctypes.POINTER(_P)]),
+    "moe_model_create": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "moe_model_load_file": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
+    "moe_model_create_synthetic": (_I, [_P, _I, _I, ctypes.c_uint64, ctypes.c_float, _I,
+                                        ctypes.POINTER(_P)]),
+    "moe_model_destroy": (_I, [_P]),
+    "moe_model_config": (_I, [_P, _P]),
+    "moe_model_reset": (_I, [_P]),
+    "moe_model_position": (_I, [_P]),
+    "moe_model_forward": (_I, [_P, _P, _I, _I, _P, _P]),
+    "moe_model_forward_full": (_I, [_P, _P, _I, _I, _P]),
+    "moe_model_generate": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(ctypes.c_float),
+                                ctypes.POINTER(ctypes.c_float)]),
 }
 
 
@@ -308,3 +320,151 @@ class MoeLayer:
                 _lib.moe_layer_destroy(self.h)
         except Exception:
             pass
+
+
+# ---------------- the whole model (test_model_trace.c:526-579) ----------------
+
+class QwenConfig(ctypes.Structure):
+    """model.h:9-23 layout."""
+
+    _fields_ = [("d_model", _I), ("n_layers", _I), ("head_dim", _I), ("n_q", _I), ("n_kv", _I),
+                ("d_ff", _I), ("n_experts", _I), ("top_k", _I), ("vocab_size", _I),
+                ("causal", _I), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+class QwenLayerWeights(ctypes.Structure):
+    """model.h:34-58 layout."""
+
+    _fields_ = [(n, _P) for n in ("Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm",
+                                  "k_norm", "rms1_w", "rms2_w", "router_w", "router_b",
+                                  "Wg", "bg", "Wu", "bu", "Wd", "bd", "Wg_q", "Wu_q", "Wd_q")] + \
+               [("experts_quantized", _I)]
+
+
+class QwenWeights(ctypes.Structure):
+    """model.h:60-69 layout."""
+
+    _fields_ = [("tok_emb", _P), ("final_norm_w", _P), ("lm_head", _P), ("layers", _P)]
+
+
+def qwen_config(D, L, hd, nq, nkv, dff, E, top_k, V, theta=1e7, eps=1e-6) -> QwenConfig:
+    return QwenConfig(D, L, hd, nq, nkv, dff, E, top_k, V, 1, float(theta), float(eps))
+
+
+class Model:
+    """A whole Qwen3-MoE model on the device with a KV cache."""
+
+    def __init__(self, handle):
+        self.h = handle
+        cfg = QwenConfig()
+        check(lib().moe_model_config(self.h, ctypes.byref(cfg)), "moe_model_config")
+        self.cfg = cfg
+        self.V = cfg.vocab_size
+
+    @classmethod
+    def synthetic(cls, cfg: QwenConfig, expert_dtype=3, untied_head=True, seed=1, std=0.02,
+                  max_seq=2048):
+        h = _P()
+        check(lib().moe_model_create_synthetic(ctypes.byref(cfg), expert_dtype, int(untied_head),
+                                               seed, std, max_seq, ctypes.byref(h)),
+              "moe_model_create_synthetic")
+        return cls(h.value)
+
+    @classmethod
+    def load_file(cls, path: str, max_seq=2048):
+        h = _P()
+        check(lib().moe_model_load_file(path.encode(), max_seq, ctypes.byref(h)),
+              "moe_model_load_file")
+        return cls(h.value)
+
+    @classmethod
+    def from_host(cls, cfg: QwenConfig, tok_emb, final_norm_w, lm_head, layers, max_seq=2048):
+        """layers: list of dicts of numpy arrays with the QwenLayerWeights
+        names (Wq, bq, ..., router_b) plus "experts": an object with gq, gs,
+        uq, us, dq, ds arrays [E, rows, bytes] and `dtype` (the oracle's
+        ExpertSet has this shape)."""
+        keep = []
+
+        def p(a, dt=np.float32):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        n = len(layers)
+        lws = (QwenLayerWeights * n)()
+        for i, lw in enumerate(layers):
+            ex = lw["experts"]
+            E = ex.gq.shape[0]
+            qdt = np.int8 if ex.dtype == 2 else np.uint8
+            arrs = []
+            for q, s, rows, cols in ((ex.gq, ex.gs, cfg.d_ff, cfg.d_model),
+                                     (ex.uq, ex.us, cfg.d_ff, cfg.d_model),
+                                     (ex.dq, ex.ds, cfg.d_model, cfg.d_ff)):
+                qa = (QuantizedWeight * E)()
+                for e in range(E):
+                    qa[e] = QuantizedWeight(p(q[e], qdt), p(s[e]), rows, cols, ex.dtype)
+                keep.append(qa)
+                arrs.append(ctypes.addressof(qa))
+            lws[i] = QwenLayerWeights(*[p(lw.get(k)) for k in (
+                "Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm", "k_norm", "rms1_w",
+                "rms2_w", "router_w", "router_b")], None, None, None, None, None, None,
+                arrs[0], arrs[1], arrs[2], 1)
+        w = QwenWeights(p(tok_emb), p(final_norm_w), p(lm_head), ctypes.addressof(lws))
+        h = _P()
+        check(lib().moe_model_create(ctypes.byref(cfg), ctypes.byref(w), max_seq, ctypes.byref(h)),
+              "moe_model_create")
+        return cls(h.value)
+
+    def reset(self):
+        check(lib().moe_model_reset(self.h), "moe_model_reset")
+
+    @property
+    def position(self) -> int:
+        return lib().moe_model_position(self.h)
+
+    def forward(self, ids):
+        """New tokens (host ids) at the current position -> (last-row logits, greedy id)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        lg = DeviceBuffer(self.V * 4)
+        nx = DeviceBuffer(4)
+        check(lib().moe_model_forward(self.h, ids.ctypes.data, ids.size, 0, lg.ptr, nx.ptr),
+              "moe_model_forward")
+        return lg.download((self.V,), np.float32), int(nx.download((1,), np.int32)[0])
+
+    def forward_full(self, ids, apply_softmax=False):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.V, np.float32)
+        check(lib().moe_model_forward_full(self.h, ids.ctypes.data, ids.size, int(apply_softmax),
+                                           out.ctypes.data), "moe_model_forward_full")
+        return out
+
+    def generate(self, prompt, n_new):
+        """-> (ids [n_new], ms_prompt, ms_decode)"""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_new, np.int32)
+        a, b = ctypes.c_float(), ctypes.c_float()
+        check(lib().moe_model_generate(self.h, prompt.ctypes.data, prompt.size, n_new,
+                                       out.ctypes.data, ctypes.byref(a), ctypes.byref(b)),
+              "moe_model_generate")
+        return out, a.value, b.value
+
+    def close(self):
+        if self.h:
+            check(lib().moe_model_destroy(self.h), "moe_model_destroy")
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and _lib is not None:
+                _lib.moe_model_destroy(self.h)
+        except Exception:
+            pass
+
+
+def model_from_tiny(tm, max_seq=64) -> Model:
+    """A Model from an object with TinyModel's attributes (oracle test models)."""
+    cfg = qwen_config(tm.D, tm.L, tm.hd, tm.nq, tm.nkv, tm.dff, tm.E, tm.top_k, tm.V, tm.theta,
+                      tm.eps)
+    return Model.from_host(cfg, tm.tok_emb, tm.final_norm_w, tm.lm_head, tm.layers, max_seq)

@@ -70,6 +70,45 @@ void orc_moe_block(const float* x_norm, const float* x_resid, int T, int D,
                    const orc_qweight* Wg, const orc_qweight* Wu, const orc_qweight* Wd,
                    float* out, int* idx_out, float* p_out, float* logits_out);
 
+/* ---- the dense fp32 half of the model (model_oracle.c) ---- */
+
+/* QwenConfig (model.h:9-23), same field order and types */
+typedef struct {
+  int d_model, n_layers, head_dim, n_q, n_kv, d_ff, n_experts, top_k, vocab_size, causal;
+  float rope_theta, rms_eps;
+} orc_config;
+
+/* One layer's tensors (model.h:34-58, quantized experts only); biases and
+ * q/k norms may be NULL. */
+typedef struct {
+  const float *Wq, *bq, *Wk, *bk, *Wv, *bv, *Wo, *bo;
+  const float *q_norm, *k_norm, *rms1_w, *rms2_w, *router_w, *router_b;
+  const orc_qweight *Wg, *Wu, *Wd;   /* [n_experts] each */
+} orc_layer;
+
+/* QwenWeights (model.h:60-69); lm_head NULL = tied to tok_emb */
+typedef struct {
+  const float* tok_emb;
+  const float* final_norm_w;
+  const float* lm_head;
+  const orc_layer* layers;
+} orc_weights;
+
+/* test_model_trace.c:433-521 for T rows at positions pos0.., KV cached */
+void orc_layer_rows(const orc_config* cfg, const orc_layer* lw, float* x, int T, int pos0,
+                    float* kc, float* vc, int max_seq);
+/* test_model_trace.c:526-579 for the new rows; kc/vc [L][n_kv][max_seq][hd] */
+void orc_model_forward_kv(const orc_config* cfg, const orc_weights* w, const int* ids, int T,
+                          int pos0, float* kc, float* vc, int max_seq, float* out_last,
+                          float* x_out);
+/* RoPE cos/sin of test_model_trace.c:310-336 for positions 0..n_pos-1:
+ * [n_pos][hd/2] each */
+void orc_rope_tables(int hd, float theta, int n_pos, float* cos_out, float* sin_out);
+/* test_model_trace.c:260-272, rows of cols values in place */
+void orc_softmax_rows(float* mat, int rows, int cols);
+/* first index of the maximum (test_model_trace.c:742-746) */
+int orc_argmax(const float* v, int n);
+
 /* export.py:23-27 rowwise Q8: s = max(amax,1e-8)/127, q = round-half-even(w/s) */
 void orc_quant_q8_rows(const float* W, int N, int K, int8_t* q, float* s);
 /* export.py:29-36 rowwise Q4: s = max(amax,1e-8)/7, q = clamp(rne(w/s),-8,7)+8,

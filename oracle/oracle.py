@@ -50,6 +50,11 @@ _ORC_SIGS = {
     "orc_expf_array": (None, [_P, _P, ctypes.c_size_t]),
     "orc_expf_mismatch_u32range": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, _P,
                                                      ctypes.POINTER(ctypes.c_uint32)]),
+    "orc_layer_rows": (None, [_P, _P, _P, _I, _I, _P, _P, _I]),
+    "orc_model_forward_kv": (None, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P]),
+    "orc_rope_tables": (None, [_I, ctypes.c_float, _I, _P, _P]),
+    "orc_argmax": (_I, [_P, _I]),
+    "orc_softmax_rows": (None, [_P, _I, _I]),
 }
 
 _orc = None
@@ -270,3 +275,129 @@ def expf_mismatches(lo: int, dev: np.ndarray):
     dev = np.ascontiguousarray(dev, dtype=np.float32)
     n = orc().orc_expf_mismatch_u32range(lo, dev.size, _c(dev), ctypes.byref(first))
     return int(n), int(first.value)
+
+
+# ---------------- the whole model (model_oracle.c) ----------------
+
+class OrcConfig(ctypes.Structure):
+    """QwenConfig (model.h:9-23) / orc_config."""
+
+    _fields_ = [("d_model", _I), ("n_layers", _I), ("head_dim", _I), ("n_q", _I), ("n_kv", _I),
+                ("d_ff", _I), ("n_experts", _I), ("top_k", _I), ("vocab_size", _I),
+                ("causal", _I), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+class OrcLayer(ctypes.Structure):
+    _fields_ = [(n, _P) for n in ("Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm",
+                                  "k_norm", "rms1_w", "rms2_w", "router_w", "router_b",
+                                  "Wg", "Wu", "Wd")]
+
+
+class OrcWeights(ctypes.Structure):
+    _fields_ = [("tok_emb", _P), ("final_norm_w", _P), ("lm_head", _P), ("layers", _P)]
+
+
+def _ptr(a):
+    return None if a is None else _c(a)
+
+
+class TinyModel:
+    """A seeded synthetic Qwen3-MoE model (config 5's recipe at any size):
+    weights ~ N(0, std^2), norm weights 1 (or N(1, 0.1^2) with
+    `random_norms`), quantized experts, optional biases and untied head.
+
+    Attributes follow QwenWeights: tok_emb, final_norm_w, lm_head (None =
+    tied), layers[L] = dict of numpy arrays plus an ExpertSet."""
+
+    def __init__(self, D=64, L=2, hd=16, nq=4, nkv=2, dff=32, E=16, top_k=8, V=97, dtype=3,
+                 seed=1, std=0.02, theta=1e7, eps=1e-6, untied=True, bias=False, qk_norm=True,
+                 random_norms=False, expert_std=None):
+        self.D, self.L, self.hd, self.nq, self.nkv, self.dff = D, L, hd, nq, nkv, dff
+        self.E, self.top_k, self.V, self.expert_dtype = E, top_k, V, dtype
+        self.theta, self.eps = float(theta), float(eps)
+        self.cfg = OrcConfig(D, L, hd, nq, nkv, dff, E, top_k, V, 1, self.theta, self.eps)
+        sd = [seed * 7919]
+
+        def nrm(*shape, mean=0.0, s=std):
+            sd[0] += 1
+            return normal(int(np.prod(shape)), sd[0], mean, s).reshape(shape)
+
+        def norm_w(n):
+            return nrm(n, mean=1.0, s=0.1) if random_norms else np.ones(n, np.float32)
+
+        self.tok_emb = nrm(V, D)
+        self.final_norm_w = norm_w(D)
+        self.lm_head = nrm(V, D) if untied else None
+        Dq, Dkv = nq * hd, nkv * hd
+        self.layers = []
+        for li in range(L):
+            lw = {"Wq": nrm(Dq, D), "Wk": nrm(Dkv, D), "Wv": nrm(Dkv, D), "Wo": nrm(D, Dq),
+                  "bq": nrm(Dq, s=0.1) if bias else None, "bk": nrm(Dkv, s=0.1) if bias else None,
+                  "bv": nrm(Dkv, s=0.1) if bias else None, "bo": nrm(D, s=0.1) if bias else None,
+                  "q_norm": norm_w(hd) if qk_norm else None,
+                  "k_norm": norm_w(hd) if qk_norm else None,
+                  "rms1_w": norm_w(D), "rms2_w": norm_w(D), "router_w": nrm(E, D),
+                  "router_b": nrm(E, s=0.05) if bias else None}
+            sd[0] += 1
+            lw["experts"] = make_experts(dtype, E, D, dff, sd[0],
+                                         std if expert_std is None else expert_std)
+            self.layers.append(lw)
+        self._build_structs()
+
+    def _build_structs(self):
+        self._layers = (OrcLayer * self.L)()
+        for i, lw in enumerate(self.layers):
+            ex = lw["experts"]
+            self._layers[i] = OrcLayer(*[_ptr(lw[k]) for k in (
+                "Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm", "k_norm", "rms1_w",
+                "rms2_w", "router_w", "router_b")],
+                ctypes.addressof(ex.Wg), ctypes.addressof(ex.Wu), ctypes.addressof(ex.Wd))
+        self._w = OrcWeights(_c(self.tok_emb), _c(self.final_norm_w), _ptr(self.lm_head),
+                             ctypes.addressof(self._layers))
+
+    def new_cache(self, max_seq):
+        shape = (self.L, self.nkv, max_seq, self.hd)
+        return np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+
+    def forward_kv(self, ids, pos0, cache, return_x=False):
+        """New rows at positions pos0..: returns the last row's logits
+        (and the hidden states after the last layer)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        kc, vc = cache
+        out = np.empty(self.V, np.float32)
+        x = np.empty((ids.size, self.D), np.float32) if return_x else None
+        orc().orc_model_forward_kv(ctypes.byref(self.cfg), ctypes.byref(self._w), _c(ids), ids.size,
+                                   pos0, _c(kc), _c(vc), kc.shape[2], _c(out), _ptr(x))
+        return (out, x) if return_x else out
+
+    def generate(self, prompt, steps, max_seq):
+        """Greedy decode: prefill the prompt, then `steps` tokens (argmax)."""
+        cache = self.new_cache(max_seq)
+        logits = self.forward_kv(prompt, 0, cache)
+        out = []
+        pos = len(prompt)
+        for _ in range(steps):
+            nxt = argmax(logits)
+            out.append(nxt)
+            logits = self.forward_kv([nxt], pos, cache)
+            pos += 1
+        return np.array(out, np.int32), logits
+
+
+def argmax(v) -> int:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return int(orc().orc_argmax(_c(v), v.size))
+
+
+def softmax_rows(m):
+    """test_model_trace.c:260-272 on a copy of a 2-D array."""
+    m = np.array(m, dtype=np.float32, copy=True, ndmin=2)
+    orc().orc_softmax_rows(_c(m), m.shape[0], m.shape[1])
+    return m
+
+
+def rope_tables(hd, theta, n_pos):
+    c = np.empty((n_pos, hd // 2), np.float32)
+    s = np.empty((n_pos, hd // 2), np.float32)
+    orc().orc_rope_tables(hd, float(theta), n_pos, _c(c), _c(s))
+    return c, s

@@ -12,7 +12,11 @@ Small cases store full inputs and outputs (ref_small.npz).  Cases at the
 BASELINE.json shapes store seeds, SHA-256 digests of the inputs and outputs and
 a sample of output values (ref_config.json), regenerated at test time.
 
-Usage:  python tests/golden/make_golden.py
+Tiny whole models (ref_model.json) store the model's seeds and keyword set,
+the prompt, the reference's greedy continuation and a digest of every step's
+logits (``--model`` writes only this file).
+
+Usage:  python tests/golden/make_golden.py [--model]
 """
 from __future__ import annotations
 
@@ -200,7 +204,55 @@ def main():
     with open(os.path.join(OUT_DIR, "ref_config.json"), "w") as f:
         json.dump(cfg, f, indent=1)
     print("wrote", os.path.join(OUT_DIR, "ref_small.npz"), "and ref_config.json")
+    model_fixtures()
+
+
+# Tiny whole models (oracle.TinyModel keyword sets) for ref_model.json: the
+# reference's model_forward_f32 (test_model_trace.c:526-579) on a QW3W file
+# written by moe.cc_amd/qw3w.py, greedy over a growing sequence.
+MODEL_CASES = [
+    ("q4_small", dict(dtype=3, seed=11), 6, 5),
+    ("q8_bias_tied", dict(dtype=2, seed=12, bias=True, untied=False), 4, 4),
+    ("q4_norms_L3", dict(dtype=3, seed=13, random_norms=True, L=3, D=128, hd=32, nq=4, nkv=2,
+                         dff=64, E=16, V=211), 9, 4),
+]
+
+
+def model_fixtures():
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "moe.cc_amd"))
+    import qw3w
+    rt = O.ref_trace()
+    out = {"generator": "oracle.TinyModel (orc_fill_normal seeds), written with qw3w.write",
+           "cases": []}
+    with tempfile.TemporaryDirectory() as d:
+        for tag, kw, n_prompt, steps in MODEL_CASES:
+            m = O.TinyModel(**kw)
+            path = os.path.join(d, tag + ".bin")
+            qw3w.write(path, qw3w.model_entries(m))
+            seq = [int(v) for v in (O.uniform_u32(n_prompt, 500 + len(tag)) % m.V)]
+            prompt = list(seq)
+            logits_sha, picks, argmaxes = [], [], []
+            for _ in range(steps + 1):
+                ids = np.array(seq, np.int32)
+                lg = np.empty(m.V, np.float32)
+                assert rt.ref_model_forward_file(path.encode(), ids.ctypes.data, ids.size,
+                                                 lg.ctypes.data, m.V) == m.V
+                logits_sha.append(sha(lg))
+                picks.append([float(v) for v in lg[:8]])
+                nxt = int(O.argmax(lg))
+                argmaxes.append(nxt)
+                seq.append(nxt)
+            out["cases"].append({"tag": tag, "model": kw, "prompt": prompt,
+                                 "greedy": argmaxes, "logits_sha": logits_sha,
+                                 "logits_first8": picks})
+    with open(os.path.join(OUT_DIR, "ref_model.json"), "w") as f:
+        json.dump(out, f, indent=1)
+    print("wrote", os.path.join(OUT_DIR, "ref_model.json"))
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["--model"]:
+        model_fixtures()
+    else:
+        main()
