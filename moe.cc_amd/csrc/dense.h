@@ -19,8 +19,40 @@ struct DenseArgs {
   const float* resid; long long ldr;
   float* C; long long ldc;
   int M, N, K;
+  // Optional rmsnorm of the A rows inside the product (few tokens only, see
+  // dense_norm_ok): A is replaced by rmsnorm(A, norm_w, eps)
+  // (test_model_trace.c:241-255, norm_w NULL = weight 1).  Each block then
+  // writes a column slice of the normalized rows to xn_out [M][K] (if given)
+  // and, with the fused selection below, packs that slice into activation
+  // tables for the expert GEMVs (pack_dtype 2 / 3, tables of
+  // act_table_bytes(K) bytes at pack_tabs; pack_part: scratch of
+  // M * gridDim.x * 2 words for the slices' headers, reduced by the last
+  // block).
+  int norm = 0;
+  const float* norm_w = nullptr;
+  float eps = 0.0f;
+  float* xn_out = nullptr;
+  int pack_dtype = 0;
+  uint8_t* pack_tabs = nullptr;
+  uint32_t* pack_part = nullptr;
+  // Optional expert selection after the product (few tokens, C = router
+  // logits [M][N]): the last block to finish picks each token's top
+  // sel_topk of the N logits by the insertion rule and their softmax gates
+  // (test_model_trace.c:275-288, :482-487) into sel_idx / sel_p ([M][topk])
+  // and the caller's copies (may be null).  sel_counter: a device counter
+  // that is zero between launches (the last block resets it).
+  unsigned* sel_counter = nullptr;
+  int sel_topk = 0;
+  int* sel_idx = nullptr;
+  float* sel_p = nullptr;
+  int32_t* sel_idx_user = nullptr;
+  float* sel_p_user = nullptr;
 };
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s);
+// Whether dense_matmul can fuse the rmsnorm for M rows of K columns.
+bool dense_norm_ok(int M, int K);
+// Whether dense_matmul can fuse the expert selection (M tokens, N experts).
+bool dense_select_ok(int M, int N);
 
 // x[t] = emb[ids[t]] (ids clamped to [0, V)), T rows of D floats.
 moe_status embed_rows(const int32_t* ids, int T, const float* emb, int V, int D, float* x,
@@ -44,10 +76,16 @@ moe_status heads_norm_rope(const HeadArgs& a, hipStream_t s);
 // the weighted V sum into H [T][nq*hd].  S is scratch [T][nq][max_seq].
 struct AttnArgs {
   const float* qkv; int ld;
-  const float* kc; const float* vc;
+  float* kc; float* vc;
   float* S; float* H;
   int T, pos0, nq, nkv, hd, max_seq;
   float scale;
+  // T == 1 only: the score launch also does heads_norm_rope's work for its
+  // row (q/k norm, RoPE, K and V into the caches); qkv holds the raw
+  // projections then and heads_norm_rope is not called.
+  int fuse_heads = 0;
+  const float* q_norm = nullptr; const float* k_norm = nullptr; float eps = 0.0f;
+  const float* rope_cos = nullptr; const float* rope_sin = nullptr;
 };
 moe_status attention_rows(const AttnArgs& a, hipStream_t s);
 

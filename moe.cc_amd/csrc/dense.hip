@@ -14,8 +14,13 @@
 // products of the softmax) run across lanes.
 #include <math.h>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "dense.h"
 #include "moe_device.h"
+#include "moe_layer.h"
+#include "moe_qtile.h"
 
 namespace moe {
 namespace {
@@ -62,76 +67,215 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 
 // ---------------------------------------------------------------- products
 
-// Few tokens (M <= 64 / RW): one wave per block owns RW output rows; lane
-// m * RW + r runs the chain of token m and row n0 + r.  The RW weight rows
-// and the M token rows stream through two LDS buffers in chunks of KC
-// columns (RW * KC = 4096 floats), the next chunk held in registers while
-// the current one is consumed.  Columns past K are zero in both operands:
-// 0 * 0 = +0 and adding +0 leaves a chain unchanged (a chain that starts at
-// +0 and adds round-to-nearest sums is never -0).  Rows past N read row
-// N - 1 and are not stored.  K % 4 == 0, 16-byte aligned rows.
-template <int RW>
-__global__ __launch_bounds__(64) void dense_gemv_kernel(DenseArgs a) {
+// Few tokens (M <= 64 / RW): a block owns RW output rows; wave 0 is the
+// consumer, waves 1..NP are producers.  The weight rows and the M token rows
+// stream in chunks of KC columns with coalesced 16-byte loads; producer p
+// owns chunks p, p + NP, ... and keeps its next chunk in registers, so each
+// load has NP chunk-times to arrive (HBM latency, not bandwidth, limits a
+// GEMV with this few bytes in flight).  A producer writes its chunk's
+// products x[m][k] * w[r][k] into one of NP + 1 LDS buffers; the consumer
+// lane m * RW + r sums token m's products with row n0 + r in column order.
+// Splitting the roles keeps multiplies and loads out of the chain's wave: a
+// pure add chain issues an add every 8 clocks, a chain that also multiplies
+// every 12-13 (measured on gfx950).  Columns past K are zero in both
+// operands: 0 * 0 = +0 and adding +0 leaves a chain unchanged (a chain that
+// starts at +0 and adds round-to-nearest sums is never -0).  Rows past N read
+// row N - 1 and are not stored.  K % 4 == 0, 16-byte aligned rows.  Dynamic
+// LDS: NP + 1 buffers of M*RW rows of KC + 4 floats, then (NORM) the rows.
+//
+// NORM: the token rows are staged whole in LDS and rmsnorm'ed first
+// (test_model_trace.c:241-255): squares x*x by all threads, one pure add
+// chain per token in the consumer lanes, msq / K, 1 / sqrtf(msq + eps), then
+// x = (x * inv) * w; the producers' first weight chunks load meanwhile.
+// Each block also writes a column slice of the normalized rows and
+// (PACK = 2 / 3) packs the slice into the activation tables; the last block
+// (fused selection) writes the tables' headers.
+template <int RW, bool NORM, int PACK, int NP>
+__global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) {
   constexpr int KC = 4096 / RW;
   constexpr int V4 = KC / 4;                 // float4 per row chunk (<= 64)
   constexpr int LD = KC + 4;                 // padded LDS row (floats)
   constexpr int RPL = 64 / V4;               // rows one load instruction covers
-  constexpr int NW = RW / RPL;               // W float4 per lane per chunk
-  constexpr int MM = 64 / RW;                // token rows staged
-  constexpr int NX = (MM + RPL - 1) / RPL;   // A float4 per lane per chunk
-  __shared__ float wl[2][RW * LD];
-  __shared__ float xl[2][MM * LD];
-  const int lane = threadIdx.x;
-  const int n0 = blockIdx.x * RW;
-  const int c4 = lane % V4, r0 = lane / V4;
+  constexpr int NW = RW / RPL;               // W float4 per producer lane per chunk
+  constexpr int NB = NP + 1;                 // LDS product buffers
+  constexpr int NT = 64 * (NP + 1);
+  extern __shared__ float4 pl4[];
+  float* pl = reinterpret_cast<float*>(pl4);
+  __shared__ float inv_s[4];
+  __shared__ int pack_scratch[2];
   const int M = a.M, N = a.N, K = a.K;
   const int nc = (K + KC - 1) / KC;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int prod = wave - 1;                 // producer index, -1 for the consumer
+  const int n0 = blockIdx.x * RW;
+  const int bufsz = M * RW * LD;
+  float* xs = pl + NB * bufsz;               // NORM: [M][K] token rows
+  const int c4 = lane % V4, r0 = lane / V4;
+  float4 rw[NW], rx[4];
   const float* wsrc[NW];
 #pragma unroll
-  for (int v = 0; v < NW; ++v) {
-    const int n = min(n0 + r0 + v * RPL, N - 1);
-    wsrc[v] = a.W + (size_t)n * a.ldw + 4 * c4;
-  }
-  const float* xsrc[NX];
-#pragma unroll
-  for (int v = 0; v < NX; ++v) {
-    const int m = min(r0 + v * RPL, M - 1);
-    xsrc[v] = a.A + (size_t)m * a.lda + 4 * c4;
-  }
-  float4 rw[NW], rx[NX];
-  auto load = [&](int c) {
-    const int k = c * KC + 4 * c4;
-    const bool in = k < K;
+  for (int v = 0; v < NW; ++v)
+    wsrc[v] = a.W + (size_t)min(n0 + r0 + v * RPL, N - 1) * a.ldw + 4 * c4;
+  auto loadW = [&](int c) {
+    const bool in = c * KC + 4 * c4 < K;
 #pragma unroll
     for (int v = 0; v < NW; ++v)
       rw[v] = in ? *reinterpret_cast<const float4*>(wsrc[v] + (size_t)c * KC) : zero4();
-#pragma unroll
-    for (int v = 0; v < NX; ++v)
-      rx[v] = in ? *reinterpret_cast<const float4*>(xsrc[v] + (size_t)c * KC) : zero4();
   };
-  auto store = [&](int b) {
+  auto loadX = [&](int c) {
+    const int k = c * KC + 4 * c4;
+    const bool in = k < K;
 #pragma unroll
-    for (int v = 0; v < NW; ++v)
-      *reinterpret_cast<float4*>(&wl[b][(r0 + v * RPL) * LD + 4 * c4]) = rw[v];
-#pragma unroll
-    for (int v = 0; v < NX; ++v)
-      if (r0 + v * RPL < MM) *reinterpret_cast<float4*>(&xl[b][(r0 + v * RPL) * LD + 4 * c4]) = rx[v];
+    for (int m = 0; m < 4; ++m)
+      if (m < M) {
+        if constexpr (NORM)
+          rx[m] = in ? *reinterpret_cast<const float4*>(xs + (size_t)m * K + k) : zero4();
+        else
+          rx[m] = in ? *reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda + k) : zero4();
+      }
   };
-  load(0);
-  store(0);
-  if (nc > 1) load(1);
-  const int m = lane / RW, r = lane % RW;
-  float acc = 0.0f;
-  for (int c = 0; c < nc; ++c) {
-    __syncthreads();
-    if (c + 1 < nc) {
-      store((c + 1) & 1);
-      if (c + 2 < nc) load(c + 2);
+  auto produce = [&](int c) {
+    float* P = pl + (c % NB) * bufsz;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m >= M) break;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) {
+        const float4 w = rw[v], x = rx[m];
+        *reinterpret_cast<float4*>(P + (m * RW + r0 + v * RPL) * LD + 4 * c4) =
+            make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w);
+      }
     }
-    acc = chain_dot(acc, &xl[c & 1][m * LD], &wl[c & 1][r * LD], V4);
+  };
+  if (prod >= 0 && prod < nc) loadW(prod);
+  if constexpr (NORM) {
+    const int k4 = K / 4;
+    for (int i = threadIdx.x; i < M * k4; i += NT) {
+      const int m = i / k4, j = i % k4;
+      const float4 v = *reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda + 4 * j);
+      reinterpret_cast<float4*>(xs)[i] = v;
+      reinterpret_cast<float4*>(pl)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
+    __syncthreads();
+    if (wave == 0 && lane < M) {
+      const float msq = chain_sum(0.0f, pl + (size_t)lane * K, k4);
+      const float mean = msq / (float)K;
+      inv_s[lane] = 1.0f / sqrtf(mean + a.eps);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < M * K; i += NT) {
+      const float v = xs[i] * inv_s[i / K];
+      xs[i] = a.norm_w ? v * a.norm_w[i % K] : v * 1.0f;
+    }
+    __syncthreads();
+    // this block's column slice [c0, c1) (a multiple of 8 columns)
+    const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
+    const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
+    if (a.xn_out)
+      for (int m = 0; m < M; ++m)
+        for (int i = c0 + threadIdx.x; i < c1; i += NT) a.xn_out[(size_t)m * K + i] = xs[(size_t)m * K + i];
+    if constexpr (PACK != 0) {
+      const size_t tb = act_table_bytes(K);
+      for (int m = 0; m < M; ++m) {
+        if (threadIdx.x == 0) { pack_scratch[0] = 1; pack_scratch[1] = 0; }
+        __syncthreads();
+        int nl;
+        uint32_t sum;
+        pack_act_cols<PACK == 3>(xs + (size_t)m * K, K, c0, c1, a.pack_tabs + m * tb, threadIdx.x, NT,
+                                 nl, sum);
+        // wave reductions, then one LDS atomic per wave
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+          const int on = __shfl_xor(nl, off, kWave);
+          nl = on > nl ? on : nl;
+          sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+        }
+        if (lane == 0) {
+          atomicMax(&pack_scratch[0], nl);
+          atomicAdd(reinterpret_cast<unsigned*>(&pack_scratch[1]), sum);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          uint32_t* pp = a.pack_part + ((size_t)m * gridDim.x + blockIdx.x) * 2;
+          pp[0] = (uint32_t)pack_scratch[0];
+          pp[1] = (uint32_t)pack_scratch[1];
+        }
+      }
+    }
   }
-  const int n = n0 + r;
-  if (m < M && n < N) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
+  if (prod >= 0) {
+    if (prod < nc) loadX(prod);
+    if (prod == 0) {
+      produce(0);
+      if (NP < nc) {
+        loadW(NP);
+        loadX(NP);
+      }
+    }
+    for (int c = 0; c < nc; ++c) {
+      __syncthreads();
+      const int k = c + 1;
+      if (k < nc && k % NP == prod) {
+        produce(k);
+        if (k + NP < nc) {
+          loadW(k + NP);
+          loadX(k + NP);
+        }
+      }
+    }
+  } else {
+    const int m = lane / RW, r = lane % RW;
+    const bool live = m < M;
+    float acc = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+      __syncthreads();
+      if (live) acc = chain_sum(acc, pl + (c % NB) * bufsz + lane * LD, V4);
+    }
+    const int n = n0 + r;
+    if (live && n < N) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
+  }
+  if constexpr (RW == 16) {
+    if (a.sel_counter) {
+      // the last block to finish selects the experts of every token (and
+      // writes the activation tables' headers from the slices' partials)
+      __shared__ int last;
+      __shared__ int sidx[kMaxTopK];
+      __shared__ float sval[kMaxTopK], sexp[kMaxTopK];
+      __threadfence();
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(a.sel_counter, 1u);
+        last = prev == gridDim.x - 1;
+        if (last) *a.sel_counter = 0u;
+      }
+      __syncthreads();
+      if (last) {
+        __threadfence();
+        if constexpr (PACK != 0) {
+          if (threadIdx.x < M) {
+            const int m = threadIdx.x;
+            uint32_t nl = 1, sum = 0;
+            for (unsigned b = 0; b < gridDim.x; ++b) {
+              const uint32_t* pp = a.pack_part + ((size_t)m * gridDim.x + b) * 2;
+              nl = pp[0] > nl ? pp[0] : nl;
+              sum += pp[1];
+            }
+            uint32_t* hh = reinterpret_cast<uint32_t*>(a.pack_tabs + m * act_table_bytes(K));
+            hh[0] = nl;
+            hh[1] = sum;
+          }
+        }
+        float* sv = pl;   // the product buffers are free now
+        for (int m = 0; m < M; ++m) {
+          const size_t o = (size_t)m * a.sel_topk;
+          select_token_block(a.C + (size_t)m * a.ldc, N, a.sel_topk, sv, sidx, sval, sexp,
+                             a.sel_idx + o, a.sel_p + o,
+                             a.sel_idx_user ? a.sel_idx_user + o : nullptr,
+                             a.sel_p_user ? a.sel_p_user + o : nullptr);
+        }
+      }
+    }
+  }
 }
 
 // Many tokens: a block computes a tile of 16*CT tokens x 16*CE rows; thread
@@ -238,56 +382,96 @@ __global__ __launch_bounds__(256) void dense_generic_kernel(DenseArgs a) {
 
 constexpr int kMaxHd = 512;
 
+// Up to two head rows (v0 and, if v1, v1; LDS, hd values each) through the
+// per-head RMSNorm of test_model_trace.c:381-402 (when the weight is given:
+// squares by all lanes, the sequential sum in lane 0 (row 0) and lane 1
+// (row 1) side by side, inv = 1/sqrtf(msq/hd + eps), v = (v*inv)*w) and
+// RoPE (:326-336: the pair (i, i + hd/2) turned by cos/sin of the row's
+// position, each product rounded, then one subtraction / addition) into
+// out0 / out1 (global or LDS).  Everything the rows need (weights, cos/sin)
+// is read from LDS or registers, so no global load sits between the steps.
+// Called by all 64 threads of a one-wave block; sq: LDS scratch [2][hd].
+__device__ void heads_prep(float* v0, float* v1, const float* w0, const float* w1, float eps,
+                           int hd, const float* cs, const float* sn, float* sq, float* inv_s,
+                           float* out0, float* out1) {
+  const int lane = threadIdx.x, d2 = hd / 2;
+  const bool n0 = w0 != nullptr, n1 = v1 && w1;
+  if (n0 || n1) {
+    for (int d = lane; d < hd; d += 64) {
+      if (n0) sq[d] = v0[d] * v0[d];
+      if (n1) sq[hd + d] = v1[d] * v1[d];
+    }
+    __syncthreads();
+    if ((lane == 0 && n0) || (lane == 1 && n1)) {
+      const float msq = chain_sum(0.0f, sq + lane * hd, hd / 4);
+      const float mean = msq / (float)hd;
+      inv_s[lane] = 1.0f / sqrtf(mean + eps);
+    }
+    __syncthreads();
+    for (int d = lane; d < hd; d += 64) {
+      if (n0) {
+        const float s = v0[d] * inv_s[0];
+        v0[d] = s * w0[d];
+      }
+      if (n1) {
+        const float s = v1[d] * inv_s[1];
+        v1[d] = s * w1[d];
+      }
+    }
+    __syncthreads();
+  }
+  for (int i = lane; i < d2; i += 64) {
+    const float c = cs[i], s = sn[i];
+    {
+      const float e = v0[i], o = v0[i + d2];
+      const float ec = e * c, os = o * s, oc = o * c, es = e * s;
+      out0[i] = ec - os;
+      out0[i + d2] = oc + es;
+    }
+    if (v1) {
+      const float e = v1[i], o = v1[i + d2];
+      const float ec = e * c, os = o * s, oc = o * c, es = e * s;
+      out1[i] = ec - os;
+      out1[i + d2] = oc + es;
+    }
+  }
+}
+
 // Block (t, h) over the heads of row t of [Q | K | V] (each head hd wide, so
-// head h starts at h * hd): q/k heads get the per-head RMSNorm of
-// test_model_trace.c:381-402 (sequential sum of squares in lane 0,
-// inv = 1/sqrtf(msq/hd + eps), v = (v*inv)*w) and RoPE (:326-336: the pair
-// (i, i + hd/2) turned by the tabled cos/sin of position pos0 + t, each
-// product rounded, then one subtraction / addition); Q stays in place, K
-// and V rows are written to the caches.
+// head h starts at h * hd): q/k heads through heads_prep at position
+// pos0 + t (Q stays in place, K goes to the cache), V rows to the cache.
 __global__ __launch_bounds__(64) void heads_kernel(HeadArgs a) {
-  __shared__ float v[kMaxHd];
-  __shared__ float inv_s;
+  __shared__ float4 v4[kMaxHd / 4];
+  __shared__ float4 sq4[2 * kMaxHd / 4];
+  __shared__ float4 w4[kMaxHd / 4];
+  __shared__ float4 cs4[kMaxHd / 8], sn4[kMaxHd / 8];
+  __shared__ float inv_s[2];
   const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int hd = a.hd, d2 = hd / 2, pos = a.pos0 + t;
   float* row = a.qkv + (size_t)t * a.ld + (size_t)h * hd;
-  for (int d = lane; d < hd; d += 64) v[d] = row[d];
   if (h >= a.nq + a.nkv) {   // V head: into the cache unchanged
     float* dst = a.vc + ((size_t)(h - a.nq - a.nkv) * a.max_seq + pos) * hd;
-    for (int d = lane; d < hd; d += 64) dst[d] = v[d];
+    for (int d = lane; d < hd; d += 64) dst[d] = row[d];
     return;
   }
   const bool isq = h < a.nq;
-  const float* w = isq ? a.q_norm : a.k_norm;
-  __syncthreads();
-  if (w) {
-    if (lane == 0) {
-      float msq = 0.0f;
-      for (int d = 0; d < hd; ++d) {
-        const float z = v[d];
-        const float zz = z * z;
-        msq = msq + zz;
-      }
-      const float mean = msq / (float)hd;
-      inv_s = 1.0f / sqrtf(mean + a.eps);
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    for (int d = lane; d < hd; d += 64) {
-      const float s = v[d] * inv;
-      v[d] = s * w[d];
-    }
-    __syncthreads();
+  const float* wg = isq ? a.q_norm : a.k_norm;
+  float* v = reinterpret_cast<float*>(v4);
+  float* w = reinterpret_cast<float*>(w4);
+  float* cs = reinterpret_cast<float*>(cs4);
+  float* sn = reinterpret_cast<float*>(sn4);
+  for (int d = lane; d < hd; d += 64) {
+    v[d] = row[d];
+    if (wg) w[d] = wg[d];
   }
-  float* out = isq ? row : a.kc + ((size_t)(h - a.nq) * a.max_seq + pos) * hd;
-  const float* cs = a.rope_cos + (size_t)pos * d2;
-  const float* sn = a.rope_sin + (size_t)pos * d2;
   for (int i = lane; i < d2; i += 64) {
-    const float e = v[i], o = v[i + d2], c = cs[i], s = sn[i];
-    const float ec = e * c, os = o * s, oc = o * c, es = e * s;
-    out[i] = ec - os;
-    out[i + d2] = oc + es;
+    cs[i] = a.rope_cos[(size_t)pos * d2 + i];
+    sn[i] = a.rope_sin[(size_t)pos * d2 + i];
   }
+  __syncthreads();
+  float* out = isq ? row : a.kc + ((size_t)(h - a.nq) * a.max_seq + pos) * hd;
+  heads_prep(v, nullptr, wg ? w : nullptr, nullptr, a.eps, hd, cs, sn, reinterpret_cast<float*>(sq4),
+             inv_s, out, nullptr);
 }
 
 // ---------------------------------------------------------------- attention
@@ -295,25 +479,84 @@ __global__ __launch_bounds__(64) void heads_kernel(HeadArgs a) {
 // Scores of query row t, head h against cache positions tk0 .. tk0 + 63
 // (<= pos0 + t): the 64 K rows are staged in LDS, lane i runs the chain
 // dot = (((0 + q0 k0) + q1 k1) + ...) over hd and stores dot * scale.
+// fuse_heads (T == 1, position P = pos0): q is normed and rotated here; the
+// block holding position P computes K's row P the same way (the cache does
+// not have it yet) and, for the first query head of each KV group, writes
+// K and V row P into the caches.  All global loads are issued first.
 __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   extern __shared__ float lds[];
-  const int hd = a.hd, LD = hd + 4;
-  float* q = lds;               // [hd]
-  float* kt = lds + hd;         // [64][LD]
+  const int hd = a.hd, LD = hd + 4, d2 = hd / 2;
+  const int hdp = (hd + 3) & ~3;
+  float* q = lds;                       // [hd] the query (rotated)
+  float* kt = q + hdp;                  // [64][LD] K rows
+  float* qraw = kt + 64 * LD;           // [hd]
+  float* kraw = qraw + hdp;             // [hd]
+  float* wq = kraw + hdp;               // [hd]
+  float* wk = wq + hdp;                 // [hd]
+  float* cs = wk + hdp;                 // [hd/2]
+  float* sn = cs + hdp;                 // [hd/2]
+  float* sq = sn + hdp;                 // [2][hd]
+  __shared__ float inv_s[2];
   const int t = blockIdx.z, h = blockIdx.y, lane = threadIdx.x;
   const int P = a.pos0 + t;
   const int tk0 = blockIdx.x * 64;
   if (tk0 > P) return;
-  const int kvh = h / (a.nq / a.nkv);
+  const int group = a.nq / a.nkv;
+  const int kvh = h / group;
   const float* qrow = a.qkv + (size_t)t * a.ld + (size_t)h * hd;
-  for (int d = lane; d < hd; d += 64) q[d] = qrow[d];
   const float* kbase = a.kc + ((size_t)kvh * a.max_seq + tk0) * hd;
   const int rows = min(64, P + 1 - tk0);
+  const bool own_new = a.fuse_heads && P - tk0 < 64;   // this block holds row P
+  const int cached = own_new ? rows - 1 : rows;        // rows read from the cache
   const int h4 = hd / 4;
-  for (int i = lane; i < rows * h4; i += 64) {
-    const int rr = i / h4, c4 = i % h4;
-    *reinterpret_cast<float4*>(kt + rr * LD + 4 * c4) =
-        *reinterpret_cast<const float4*>(kbase + (size_t)rr * hd + 4 * c4);
+  const int total = cached * h4;
+  if (a.fuse_heads) {
+    const float* krow = a.qkv + (size_t)t * a.ld + (size_t)(a.nq + kvh) * hd;
+    for (int d = lane; d < hd; d += 64) {
+      qraw[d] = qrow[d];
+      if (a.q_norm) wq[d] = a.q_norm[d];
+      if (own_new) {
+        kraw[d] = krow[d];
+        if (a.k_norm) wk[d] = a.k_norm[d];
+      }
+    }
+    for (int i = lane; i < d2; i += 64) {
+      cs[i] = a.rope_cos[(size_t)P * d2 + i];
+      sn[i] = a.rope_sin[(size_t)P * d2 + i];
+    }
+    if (own_new && h % group == 0) {   // V row P into the cache unchanged
+      const float* vraw = a.qkv + (size_t)t * a.ld + (size_t)(a.nq + a.nkv + kvh) * hd;
+      float* vd = a.vc + ((size_t)kvh * a.max_seq + P) * hd;
+      for (int d = lane; d < hd; d += 64) vd[d] = vraw[d];
+    }
+  }
+  // 16 loads in flight per lane, then their stores
+  for (int base = 0; base < total; base += 64 * 16) {
+    float4 r[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + lane + 64 * u;
+      r[u] = i < total ? *reinterpret_cast<const float4*>(kbase + (size_t)(i / h4) * hd + 4 * (i % h4))
+                       : zero4();
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + lane + 64 * u;
+      if (i < total) *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
+    }
+  }
+  if (a.fuse_heads) {
+    __syncthreads();
+    float* knew = kt + (P - tk0) * LD;
+    heads_prep(qraw, own_new ? kraw : nullptr, a.q_norm ? wq : nullptr, a.k_norm ? wk : nullptr,
+               a.eps, hd, cs, sn, sq, inv_s, q, knew);
+    if (own_new && h % group == 0) {
+      __syncthreads();
+      float* kd = a.kc + ((size_t)kvh * a.max_seq + P) * hd;
+      for (int d = lane; d < hd; d += 64) kd[d] = knew[d];
+    }
+  } else {
+    for (int d = lane; d < hd; d += 64) q[d] = qrow[d];
   }
   __syncthreads();
   if (lane < rows) {
@@ -323,32 +566,67 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
 }
 
 constexpr int kPvThreads = 256;
-constexpr int kPvChunk = 128;   // positions per staged V tile
 
 // Softmax of the n = pos0 + t + 1 scores of (t, h) and the weighted V sum
-// for head dimensions 64g .. 64g + 63 (test_model_trace.c:408-426):
+// for head dimensions DPB*g .. DPB*g + DPB - 1 (test_model_trace.c:408-426):
 //   m = S[0], then every larger score (a NaN S[0] stays; later NaNs never
-//   win); e_i = expf(S_i - m); sum = (((0 + e_0) + e_1) + ...) in lane 0;
-//   p_i = e_i * (1 / (sum + 1e-9)); out_d = (((0 + p_0 v_0d) + p_1 v_1d) + ...)
-// in wave 0, lane d, with V tiles of kPvChunk positions staged in LDS by the
-// whole block a tile ahead.
+//   win); e_i = expf(S_i - m); sum = (((0 + e_0) + e_1) + ...) in thread 0;
+//   p_i = e_i * (1 / (sum + 1e-9)); out_d = (((0 + p_0 v_0d) + p_1 v_1d) + ...).
+// The weighted sum runs over chunks of CH positions: every thread forms
+// products p_i * v_id of the chunk into a transposed LDS tile [d][i] (the
+// next chunk's V loads already in flight), then lanes d < DPB sum their row
+// with pure dependent adds.  Products past n are 0 * 0 = +0 (no-ops).
+template <int DPB>
 __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a) {
+  constexpr int CH = 16384 / DPB;                  // positions per chunk
+  constexpr int Q4 = DPB / 4;                      // float4 per position
+  constexpr int NL = CH * Q4 / kPvThreads;         // float4 per thread per chunk
+  constexpr int LDT = CH + 4;
   extern __shared__ float lds[];
   const int hd = a.hd;
-  const int t = blockIdx.z, h = blockIdx.y, g = blockIdx.x;
+  const int t = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int n = a.pos0 + t + 1;
   float* es = lds;                                  // [max_seq, rounded up to 4]
-  float* vt = lds + ((a.max_seq + 3) & ~3);         // [2][kPvChunk][64]
+  float* pt = lds + ((a.max_seq + 3) & ~3);         // [DPB][LDT]
   __shared__ float red[kPvThreads / kWave];
   __shared__ float inv_s;
+  const int kvh = h / (a.nq / a.nkv);
+  const int d0 = DPB * blockIdx.x;
+  const int dl = min(DPB, hd - d0);
+  const float* vbase = a.vc + (size_t)kvh * a.max_seq * hd + d0;
+  const int nch = (n + CH - 1) / CH;
+  float4 rg[NL];
+  auto load = [&](int c) {
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + kPvThreads * u;
+      const int pos = c * CH + i / Q4, q4 = i % Q4;
+      rg[u] = (pos < n && 4 * q4 < dl) ? *reinterpret_cast<const float4*>(vbase + (size_t)pos * hd + 4 * q4)
+                                       : zero4();
+    }
+  };
+  auto store = [&](int c) {
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + kPvThreads * u;
+      const int lp = i / Q4, q4 = i % Q4, pos = c * CH + lp;
+      const float pk = pos < n ? es[pos] : 0.0f;
+      float* col = pt + 4 * q4 * LDT + lp;
+      col[0] = pk * rg[u].x;
+      col[LDT] = pk * rg[u].y;
+      col[2 * LDT] = pk * rg[u].z;
+      col[3 * LDT] = pk * rg[u].w;
+    }
+  };
+  // the first V tile loads while the softmax runs
+  load(0);
   const float* Srow = a.S + ((size_t)t * a.nq + h) * a.max_seq;
   float mx = -__builtin_inff();
-  bool any = false;
   for (int i = tid; i < n; i += kPvThreads) {
     const float s = Srow[i];
     es[i] = s;
-    if (s == s && (!any || s > mx)) { mx = s; any = true; }
+    if (s == s && s > mx) mx = s;
   }
   // order-free max over the non-NaN scores (-inf when there is none)
 #pragma unroll
@@ -363,86 +641,23 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   const float s0 = es[0];
   if (s0 != s0) m = s0;
   for (int i = tid; i < n; i += kPvThreads) es[i] = expf_glibc(es[i] - m);
+  for (int i = n + tid; i < ((n + 3) & ~3); i += kPvThreads) es[i] = 0.0f;
   __syncthreads();
-  if (tid == 0) {
-    const float4* e4 = reinterpret_cast<const float4*>(es);
-    float sum = 0.0f;
-    int i = 0;
-    for (; i + 64 <= n; i += 64) {
-      float4 ev[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) ev[j] = e4[i / 4 + j];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        sum = sum + ev[j].x;
-        sum = sum + ev[j].y;
-        sum = sum + ev[j].z;
-        sum = sum + ev[j].w;
-      }
-    }
-    for (; i < n; ++i) sum = sum + es[i];
-    inv_s = 1.0f / (sum + 1e-9f);
-  }
+  if (tid == 0) inv_s = 1.0f / (chain_sum(0.0f, es, (n + 3) / 4) + 1e-9f);
   __syncthreads();
   const float inv = inv_s;
   for (int i = tid; i < n; i += kPvThreads) es[i] = es[i] * inv;
-  // weighted V sum: tiles of kPvChunk positions x 64 dims, double buffered
-  const int kvh = h / (a.nq / a.nkv);
-  const int d0 = 64 * g;
-  const int dl = min(64, hd - d0);
-  const float* vbase = a.vc + (size_t)kvh * a.max_seq * hd + d0;
-  constexpr int NV = kPvChunk * 16 / kPvThreads;    // float4 per thread per tile
-  const int nch = (n + kPvChunk - 1) / kPvChunk;
-  float4 rg[NV];
-  auto load = [&](int c) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int i = tid + kPvThreads * v;
-      const int p = c * kPvChunk + i / 16, c4 = i % 16;
-      rg[v] = (p < n && 4 * c4 < dl) ? *reinterpret_cast<const float4*>(vbase + (size_t)p * hd + 4 * c4)
-                                     : zero4();
-    }
-  };
-  auto store = [&](int b) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int i = tid + kPvThreads * v;
-      *reinterpret_cast<float4*>(vt + (b * kPvChunk + i / 16) * 64 + 4 * (i % 16)) = rg[v];
-    }
-  };
-  load(0);
-  store(0);
-  if (nch > 1) load(1);
+  __syncthreads();
   float out = 0.0f;
   for (int c = 0; c < nch; ++c) {
+    store(c);
+    if (c + 1 < nch) load(c + 1);
     __syncthreads();
-    if (c + 1 < nch) {
-      store((c + 1) & 1);
-      if (c + 2 < nch) load(c + 2);
-    }
-    if (wave == 0) {
-      const float* tile = vt + (c & 1) * kPvChunk * 64 + lane;
-      const int p0 = c * kPvChunk;
-      const int np = min(kPvChunk, n - p0);
-      int j = 0;
-      for (; j + 16 <= np; j += 16) {
-        float pv[16], vv[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) { pv[u] = es[p0 + j + u]; vv[u] = tile[(j + u) * 64]; }
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          const float pr = pv[u] * vv[u];
-          out = out + pr;
-        }
-      }
-      for (; j < np; ++j) {
-        const float pr = es[p0 + j] * tile[j * 64];
-        out = out + pr;
-      }
-    }
+    const int np = min(CH, n - c * CH);
+    if (tid < dl) out = chain_sum(out, pt + tid * LDT, (np + 3) / 4);
+    __syncthreads();
   }
-  if (wave == 0 && lane < dl)
-    a.H[(size_t)t * a.nq * hd + (size_t)h * hd + d0 + lane] = out;
+  if (tid < dl) a.H[(size_t)t * a.nq * hd + (size_t)h * hd + d0 + tid] = out;
 }
 
 // ---------------------------------------------------------------- misc
@@ -551,11 +766,36 @@ __global__ __launch_bounds__(kSmThreads) void softmax_vec_kernel(float* v, int n
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Dynamic LDS above 64 KB needs the kernel's attribute raised; the largest
+// size set per kernel is remembered so the runtime is called once per size.
+std::mutex g_lds_mu;
+std::unordered_map<const void*, size_t> g_lds_set;
+
 template <class F>
 moe_status set_lds(F* fn, size_t bytes, const char* what) {
   if (bytes <= 65536) return MOE_OK;
-  return check_hip(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)bytes), what);
+  std::lock_guard<std::mutex> lk(g_lds_mu);
+  size_t& cur = g_lds_set[(const void*)fn];
+  if (bytes <= cur) return MOE_OK;
+  moe_status st = check_hip(hipFuncSetAttribute((const void*)fn,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes),
+                            what);
+  if (st == MOE_OK) cur = bytes;
+  return st;
+}
+
+size_t gemv_lds(int RW, int NP, int M, int K, bool norm) {
+  return ((size_t)(NP + 1) * M * RW * (4096 / RW + 4) + (norm ? (size_t)M * K : 0)) * 4;
+}
+
+template <int RW, bool NORM, int PACK, int NP>
+moe_status launch_gemv(const DenseArgs& a, hipStream_t s) {
+  const size_t lds = gemv_lds(RW, NP, a.M, a.K, NORM);
+  moe_status st = set_lds(dense_gemv_kernel<RW, NORM, PACK, NP>, lds, "gemv LDS attribute");
+  if (st) return st;
+  hipLaunchKernelGGL((dense_gemv_kernel<RW, NORM, PACK, NP>), dim3((unsigned)((a.N + RW - 1) / RW)),
+                     dim3(64 * (NP + 1)), lds, s, a);
+  return check_hip(hipGetLastError(), "dense gemv launch");
 }
 
 template <int CT, int CE, int KC>
@@ -568,21 +808,55 @@ moe_status launch_tile(const DenseArgs& a, hipStream_t s) {
 
 }  // namespace
 
+// Producer waves of the few-token GEMV: three for one token (the LDS of four
+// product buffers fits), one otherwise.
+constexpr int kNpOne = 3;
+
+bool dense_norm_ok(int M, int K) {
+  return M >= 1 && M <= 4 && K % 4 == 0 && K <= 8192 &&
+         gemv_lds(16, M == 1 ? kNpOne : 1, M, K, true) <= 150 * 1024;
+}
+
+bool dense_select_ok(int M, int N) { return M >= 1 && M <= 4 && N <= 1024; }
+
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return MOE_OK;
+  if (a.sel_counter && (!dense_select_ok(a.M, a.N) || a.sel_topk < 1 || a.sel_topk > kMaxTopK ||
+                        a.ldc != a.N))
+    return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs M <= 4, N <= 1024");
   if (a.K <= 0) return set_error(MOE_ERR_ARG, "dense matmul: K = %d", a.K);
   const bool vec = a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) && al16(a.W);
+  if (a.norm) {
+    if (!vec || !dense_norm_ok(a.M, a.K))
+      return set_error(MOE_ERR_ARG, "dense matmul: fused rmsnorm needs M <= 4 aligned rows");
+    if (a.pack_dtype && (!a.sel_counter || !a.pack_part || !a.pack_tabs))
+      return set_error(MOE_ERR_ARG, "dense matmul: packing needs the fused selection");
+    if (a.M == 1) {
+      if (a.pack_dtype == 2) return launch_gemv<16, true, 2, kNpOne>(a, s);
+      if (a.pack_dtype == 3) return launch_gemv<16, true, 3, kNpOne>(a, s);
+      return launch_gemv<16, true, 0, kNpOne>(a, s);
+    }
+    if (a.pack_dtype == 2) return launch_gemv<16, true, 2, 1>(a, s);
+    if (a.pack_dtype == 3) return launch_gemv<16, true, 3, 1>(a, s);
+    return launch_gemv<16, true, 0, 1>(a, s);
+  }
   if (!vec) {
     const long long total = (long long)a.M * a.N;
     hipLaunchKernelGGL(dense_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), "dense generic launch");
   }
+  if (a.sel_counter) {
+    if (!vec) return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs aligned rows");
+    return a.M == 1 ? launch_gemv<16, false, 0, kNpOne>(a, s) : launch_gemv<16, false, 0, 1>(a, s);
+  }
   if (a.M == 1 && a.N >= 65536) {
-    hipLaunchKernelGGL(dense_gemv_kernel<64>, dim3((unsigned)((a.N + 63) / 64)), dim3(64), 0, s, a);
+    return launch_gemv<64, false, 0, 1>(a, s);
   } else if (a.M <= 2 && a.N >= 32768) {
-    hipLaunchKernelGGL(dense_gemv_kernel<32>, dim3((unsigned)((a.N + 31) / 32)), dim3(64), 0, s, a);
+    return launch_gemv<32, false, 0, 1>(a, s);
+  } else if (a.M == 1) {
+    return launch_gemv<16, false, 0, kNpOne>(a, s);
   } else if (a.M <= 4) {
-    hipLaunchKernelGGL(dense_gemv_kernel<16>, dim3((unsigned)((a.N + 15) / 16)), dim3(64), 0, s, a);
+    return launch_gemv<16, false, 0, 1>(a, s);
   } else if (a.M >= 256) {
     return launch_tile<4, 4, 32>(a, s);
   } else {
@@ -608,17 +882,27 @@ moe_status heads_norm_rope(const HeadArgs& a, hipStream_t s) {
 moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   if (a.T <= 0) return MOE_OK;
   if (a.hd % 4 || a.hd > kMaxHd) return set_error(MOE_ERR_ARG, "attention: head_dim %d", a.hd);
+  if (a.fuse_heads && a.T != 1) return set_error(MOE_ERR_ARG, "attention: fused heads need T == 1");
   const int nmax = a.pos0 + a.T;   // positions of the last row
-  const size_t lds_s = (size_t)(a.hd + 64 * (a.hd + 4)) * 4;
+  const size_t hdp = (size_t)((a.hd + 3) & ~3);
+  const size_t lds_s = (9 * hdp + 64 * (size_t)(a.hd + 4)) * 4;
   moe_status st = set_lds(attn_scores_kernel, lds_s, "scores LDS attribute");
   if (st) return st;
   hipLaunchKernelGGL(attn_scores_kernel, dim3((unsigned)((nmax + 63) / 64), (unsigned)a.nq, (unsigned)a.T),
                      dim3(64), lds_s, s, a);
   if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
-  const size_t lds_p = ((size_t)((a.max_seq + 3) & ~3) + 2 * kPvChunk * 64) * 4;
-  if ((st = set_lds(attn_softmax_pv_kernel, lds_p, "softmax/pv LDS attribute"))) return st;
-  hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3((unsigned)((a.hd + 63) / 64), (unsigned)a.nq, (unsigned)a.T),
-                     dim3(kPvThreads), lds_p, s, a);
+  const size_t es_f = (size_t)((a.max_seq + 3) & ~3);
+  if (a.T <= 4) {
+    const size_t lds_p = (es_f + 16 * (16384 / 16 + 4)) * 4;
+    if ((st = set_lds(attn_softmax_pv_kernel<16>, lds_p, "softmax/pv LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_softmax_pv_kernel<16>, dim3((unsigned)((a.hd + 15) / 16), (unsigned)a.nq, (unsigned)a.T),
+                       dim3(kPvThreads), lds_p, s, a);
+  } else {
+    const size_t lds_p = (es_f + 128 * (16384 / 128 + 4)) * 4;
+    if ((st = set_lds(attn_softmax_pv_kernel<128>, lds_p, "softmax/pv LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_softmax_pv_kernel<128>, dim3((unsigned)((a.hd + 127) / 128), (unsigned)a.nq, (unsigned)a.T),
+                       dim3(kPvThreads), lds_p, s, a);
+  }
   return check_hip(hipGetLastError(), "softmax/pv launch");
 }
 

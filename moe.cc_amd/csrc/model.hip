@@ -207,18 +207,30 @@ moe_status forward_dev(moe_model* m, const int32_t* ids_d, int T, float* logits_
     DevLayer& L = m->layers[l];
     float* kc = m->kc + l * per_layer;
     float* vc = m->vc + l * per_layer;
-    // :449 norm1
-    if ((st = moe_rmsnorm_dev(x, L.rms1, xn, T, D, eps))) return st;
-    // :363-369 Q, K, V (+ biases)
+    // :449 norm1, :363-369 Q, K, V (+ biases); the norm fused into the
+    // product for few tokens
     DenseArgs qa{xn, D, L.wqkv, D, L.bqkv, nullptr, 0, qkv, m->nqkv, T, m->nqkv, D};
+    if (dense_norm_ok(T, D)) {
+      qa.A = x;
+      qa.norm = 1; qa.norm_w = L.rms1; qa.eps = eps;
+    } else if ((st = moe_rmsnorm_dev(x, L.rms1, xn, T, D, eps))) {
+      return st;
+    }
     if ((st = dense_matmul(qa, s))) return st;
     // :371-398 q/k norm, :400 RoPE, K/V into the cache
-    HeadArgs ha{qkv, m->nqkv, T, m->pos, c.n_q, c.n_kv, hd, m->max_seq, L.q_norm, L.k_norm, eps,
-                m->rope_cos, m->rope_sin, kc, vc};
-    if ((st = heads_norm_rope(ha, s))) return st;
-    // :402-426 causal attention
+    // (one token: done inside the score launch)
     AttnArgs aa{qkv, m->nqkv, kc, vc, (float*)m->S.p, (float*)m->H.p, T, m->pos, c.n_q, c.n_kv,
                 hd, m->max_seq, m->scale};
+    if (T == 1) {
+      aa.fuse_heads = 1;
+      aa.q_norm = L.q_norm; aa.k_norm = L.k_norm; aa.eps = eps;
+      aa.rope_cos = m->rope_cos; aa.rope_sin = m->rope_sin;
+    } else {
+      HeadArgs ha{qkv, m->nqkv, T, m->pos, c.n_q, c.n_kv, hd, m->max_seq, L.q_norm, L.k_norm,
+                  eps, m->rope_cos, m->rope_sin, kc, vc};
+      if ((st = heads_norm_rope(ha, s))) return st;
+    }
+    // :402-426 causal attention
     if ((st = attention_rows(aa, s))) return st;
     // :427-428 output projection (+ bias), :460 residual
     DenseArgs oa{(float*)m->H.p, m->Dq, L.wo, m->Dq, L.bo, x, D, xa, D, T, D, m->Dq};

@@ -142,6 +142,36 @@ __device__ __forceinline__ float expf_glibc(float x) {
   return (float)y;
 }
 
+// acc = ((acc + p0) + p1) + ... over 4*n4 values of an LDS row (16-byte
+// aligned): the sequential fp32 sum of the reference, as pure dependent adds
+// (operands formed beforehand, by other lanes); 16 float4 are read ahead of
+// their 64 adds.  A dependent v_add_f32 chain issues an add every 8 clocks
+// on gfx950; with a multiply feeding each add it takes 12-13.
+__device__ __forceinline__ float chain_sum(float acc, const float* p, int n4) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  int k4 = 0;
+  for (; k4 + 16 <= n4; k4 += 16) {
+    float4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = p4[k4 + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc = acc + v[i].x;
+      acc = acc + v[i].y;
+      acc = acc + v[i].z;
+      acc = acc + v[i].w;
+    }
+  }
+  for (; k4 < n4; ++k4) {
+    const float4 v = p4[k4];
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+  }
+  return acc;
+}
+
 // test_model_trace.c:233 then :500: h = (g / (1 + expf(-g))) * u
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float den = 1.0f + expf_glibc(-g);

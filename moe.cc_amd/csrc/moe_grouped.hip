@@ -803,6 +803,16 @@ moe_status mma_lds_attributes() {
 
 }  // namespace
 
+moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s) {
+  SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out};
+  dim3 sg((unsigned)((T + kSelectWaves - 1) / kSelectWaves));
+  if (L->E <= 64) hipLaunchKernelGGL(select_kernel<1>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
+  else if (L->E <= 128) hipLaunchKernelGGL(select_kernel<2>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
+  else if (L->E <= 256) hipLaunchKernelGGL(select_kernel<4>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
+  else hipLaunchKernelGGL(select_kernel<16>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
+  return check_hip(hipGetLastError(), "select launch");
+}
+
 bool grouped_ok(const LayerDev* L) {
   const int step = L->dtype == 3 ? 256 : 128;
   return L->D % step == 0 && L->dff % step == 0 && L->D % 128 == 0 && L->E <= kGroupThreads &&
@@ -828,13 +838,7 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   else st = launch_router_tile<1, 1, 128>(ra, s);
   if (st) return st;
   // 3. top-k and gates
-  SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out};
-  dim3 sg((unsigned)((T + kSelectWaves - 1) / kSelectWaves));
-  if (L->E <= 64) hipLaunchKernelGGL(select_kernel<1>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else if (L->E <= 128) hipLaunchKernelGGL(select_kernel<2>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else if (L->E <= 256) hipLaunchKernelGGL(select_kernel<4>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else hipLaunchKernelGGL(select_kernel<16>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  if ((st = check_hip(hipGetLastError(), "select launch"))) return st;
+  if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
   // 4. group pairs by expert
   const int npairs = T * L->topk;
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,

@@ -31,17 +31,19 @@ struct LayerDev {
   uint8_t* htab = nullptr;   // [T*topk] packed h rows
   float* h = nullptr;        // [T*topk][dff] (decode kernels)
   float* xn = nullptr;       // [T][D] normed input (block forward)
-  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables
   uint32_t* hpart = nullptr; // [T*topk][h segments][2] partial headers of the h tables
-  // completion counter of the router's last-block step, zero between launches
-  unsigned* counters = nullptr;
   // grouped kernels: pairs per expert, first pair of each expert in `perm`,
   // pair ids (t * topk + j) grouped by expert, expert outputs per pair
   int* ecount = nullptr;     // [E]
   int* eoff = nullptr;       // [E]
   int* perm = nullptr;       // [T*topk]
   float* y = nullptr;        // [T*topk][D]
+  unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };
+
+// Top-k and softmax gates of T tokens from L->logits into L->idx / L->p
+// (and the caller's copies, when given): one wave per token.
+moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s);
 
 // Grouped (expert-major) forward for many tokens; requires grouped_ok(L).
 bool grouped_ok(const LayerDev* L);
@@ -133,6 +135,74 @@ __device__ void select_token(const float* __restrict__ logit_row, int E, int K, 
   }
   __threadfence_block();
   __builtin_amdgcn_wave_barrier();
+}
+
+// Block-wide selection for one token (any block size, E <= 1024): every
+// thread ranks its candidates among all E logits, rank = number of live
+// logits that beat it (larger, or equal with a lower index; NaN and -inf
+// are never live), and a live candidate with rank < K takes slot `rank`.
+// This is the result of the insertion rule of test_model_trace.c:275-288
+// (ties keep the lower index first, NaN / -inf never enter, leftover slots
+// keep index -1), computed without a serial pass.  Then wave 0 forms the
+// softmax over the slots (:482-487) as select_token does.  sv: LDS scratch
+// of E floats, 16-byte aligned; all threads of the block must call this.
+__device__ __forceinline__ void select_token_block(const float* __restrict__ logit_row, int E,
+                                                  int K, float* sv, int* sidx, float* sval,
+                                                  float* sexp, int* idx, float* p,
+                                                  int* idx_user, float* p_user) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int e = tid; e < E; e += nt) sv[e] = logit_row[e];
+  if (tid < K) { sidx[tid] = -1; sval[tid] = -__builtin_inff(); }
+  __syncthreads();
+  for (int i = tid; i < E; i += nt) {
+    const float vi = sv[i];
+    if (!(vi > -__builtin_inff())) continue;
+    // w beats vi iff w > vi, or w == vi at a lower index; NaN and -inf
+    // never beat a live vi, so no liveness test is needed for w
+    int rank = 0;
+    int j = 0;
+    const float4* sv4 = reinterpret_cast<const float4*>(sv);
+    for (; j + 32 <= E; j += 32) {
+      float4 w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = sv4[j / 4 + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int jj = j + 4 * u;
+        rank += (int)((w[u].x > vi) | ((w[u].x == vi) & (jj < i)));
+        rank += (int)((w[u].y > vi) | ((w[u].y == vi) & (jj + 1 < i)));
+        rank += (int)((w[u].z > vi) | ((w[u].z == vi) & (jj + 2 < i)));
+        rank += (int)((w[u].w > vi) | ((w[u].w == vi) & (jj + 3 < i)));
+      }
+    }
+    for (; j < E; ++j) {
+      const float w = sv[j];
+      rank += (int)((w > vi) | ((w == vi) & (j < i)));
+    }
+    if (rank < K) { sidx[rank] = i; sval[rank] = vi; }
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    const int lane = tid;
+    if (lane < K) {
+      float mx = sval[0];
+      for (int i = 1; i < K; ++i) if (sval[i] > mx) mx = sval[i];
+      sexp[lane] = expf_glibc(sval[lane] - mx);
+    }
+    __threadfence_block();
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int i = 0; i < K; ++i) sum = sum + sexp[i];
+    const float inv = 1.0f / (sum + 1e-9f);
+    if (lane < K) {
+      const float pv = sexp[lane] * inv;
+      idx[lane] = sidx[lane];
+      p[lane] = pv;
+      if (idx_user) idx_user[lane] = sidx[lane];
+      if (p_user) p_user[lane] = pv;
+    }
+  }
+  __syncthreads();
 }
 
 }  // namespace moe

@@ -1,14 +1,15 @@
 // moe_layer.hip - the MoE block of one Qwen3-MoE layer on gfx950
 // (test_model_trace.c:460-517), bit-identical to the reference.
 //
-// Launch sequence of one forward (T tokens), three kernels:
+// Launch sequence of one forward (T tokens):
 //   [rmsnorm]   x_norm = rmsnorm(x, rms2_w)          (block forward only; :461)
+//   act_pack    x_norm rows -> packed limb tables for the expert GEMVs
 //   router      logits[t,e] = sum_k x_norm[t,k] * Wr[e,k], k ascending,
-//               separate roundings (:465 -> :213-227), + bias (:466-468).
-//               Blocks of 8 experts stage their rows in LDS; the last block
-//               to finish does top-k by the insertion rule (:480 -> :275-288)
-//               and the softmax over the selected logits (:482-487), and
-//               packs x_norm for the expert GEMVs.
+//               separate roundings (:465 -> :213-227), + bias (:466-468):
+//               the exact fp32 products of dense.hip
+//   select      top-k by the insertion rule (:480 -> :275-288) and the
+//               softmax over the selected logits (:482-487), a wave per token
+//               (in the router launch's last block for few tokens)
 //   gate_up     per (token, rank) pair and row chunk: g = Q(x Wg), u = Q(x Wu),
 //               exact integer dots; h = (g / (1 + expf(-g))) * u (:496-501),
 //               written straight into the pair's packed table for down.
@@ -16,12 +17,9 @@
 //               (:502-503) into LDS, then out = x_resid + (((0 + p0 y0) +
 //               p1 y1) + ...) in rank order, each product and sum rounded on
 //               its own (:513, :517).
-// Cross-block hand-offs go through kernel boundaries (and one last-block
-// step in the 16-block router), never through per-block device fences.
-// The router's sequential sum runs as one add chain per (token, expert) and
-// lane, over rows staged in LDS (seq_dot_lane).
-// These kernels serve few tokens (decode); many tokens go through the
-// expert-major kernels of moe_grouped.hip.
+// Cross-block hand-offs go through kernel boundaries, never through
+// per-block device fences.  These kernels serve few tokens (decode); many
+// tokens go through the expert-major kernels of moe_grouped.hip.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -30,7 +28,9 @@
 #include <type_traits>
 #include <vector>
 
+#include "dense.h"
 #include "moe_device.h"
+#include "moe_internal.h"
 #include "moe_layer.h"
 #include "moe_lib.h"
 #include "moe_qtile.h"
@@ -39,216 +39,9 @@ namespace moe {
 
 namespace {
 
-constexpr int kRouterThreads = 512;            // 8 waves
-constexpr int kRouterWaves = kRouterThreads / kWave;
-constexpr int kRouterExperts = 8;              // experts per router block
-constexpr int kRouterTokens = 8;               // tokens per router block: 64 chains = 1 wave
+constexpr int kCombineThreads = 512;           // 8 waves
+constexpr int kCombineWaves = kCombineThreads / kWave;
 constexpr size_t kMaxLds = 160 * 1024 - 2048;  // dynamic LDS budget (static LDS fits in the rest)
-
-// Sequential fp32 dot of x[0..D) with w, k ascending, each product and each
-// sum rounded on its own (test_model_trace.c:221-222), one chain per lane
-// with the products in the lane's own registers (a dependent v_add_f32 every
-// 8 clocks).  x and w point into LDS, 16-byte aligned, D % 16 == 0, and both
-// rows are readable (padding) up to index D + 15, so the next 16 values are
-// always prefetched without a branch.
-constexpr int kRowPad = 16;
-__device__ __forceinline__ float seq_dot_lane(const float* x, const float* w, int D) {
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  const float4* w4 = reinterpret_cast<const float4*>(w);
-  float acc = 0.0f;
-  int k4 = 0;
-  // 64 columns per step: all 32 LDS reads are issued first, so their latency
-  // is paid once per 64 dependent adds
-  for (; k4 + 16 <= D / 4; k4 += 16) {
-    float4 xv[16], wv[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { xv[i] = x4[k4 + i]; wv[i] = w4[k4 + i]; }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float p0 = xv[i].x * wv[i].x, p1 = xv[i].y * wv[i].y;
-      const float p2 = xv[i].z * wv[i].z, p3 = xv[i].w * wv[i].w;
-      acc = acc + p0;
-      acc = acc + p1;
-      acc = acc + p2;
-      acc = acc + p3;
-    }
-  }
-  for (; k4 < D / 4; ++k4) {
-    const float4 xv = x4[k4], wv = w4[k4];
-    const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
-    acc = acc + p0;
-    acc = acc + p1;
-    acc = acc + p2;
-    acc = acc + p3;
-  }
-  return acc;
-}
-
-// Block-level "am I the last block to finish this step" test: every thread
-// publishes its writes (agent-scope fence), one thread counts the block in,
-// and the block that brings the count to `total` gets true (after an acquire
-// fence, so it sees every other block's writes) and resets the counter.
-// Used only by the 16-block router: a device fence per block is expensive.
-__device__ __forceinline__ bool last_block_in(unsigned* counter, unsigned total) {
-  __shared__ int last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(counter, 1u);
-    last = prev == total - 1;
-    if (last) *counter = 0u;
-  }
-  __syncthreads();
-  if (!last) return false;
-  __threadfence();
-  return true;
-}
-
-struct RouterArgs {
-  const float* xn;
-  int T, D, E, topk;
-  const float* W;
-  const float* b;
-  float* logits;
-  int* idx;
-  float* p;
-  int* idx_user;
-  float* p_user;
-  uint8_t* xtab;         // packed x_norm rows
-  size_t tab_bytes;
-  uint32_t* xpart;       // [T][gridDim.x][2] partial (limbs, sum) of each column slice
-  unsigned* counter;
-  int tb;                // tokens per block
-  int staged;            // rows staged in LDS, one chain per lane
-  int cols;              // x columns packed per block (multiple of 8)
-};
-
-// Runs in the last router block.  Headers of the packed x rows; then, one
-// wave per token, top-k by repeated arg-max (the largest remaining value,
-// lowest index among equals: the result of the insertion rule of
-// test_model_trace.c:275-288; NaN and -inf never selected) and the softmax
-// over the selected logits (:482-487).  C = candidates per lane (E <= 64*C).
-template <bool Q4, int C>
-__device__ void router_finish(const RouterArgs& a) {
-  __shared__ int sidx[kRouterWaves][kMaxTopK];
-  __shared__ float sval[kRouterWaves][kMaxTopK];
-  __shared__ float sexp[kRouterWaves][kMaxTopK];
-  const int tid = threadIdx.x, E = a.E, K = a.topk;
-  const int nbx = gridDim.x;
-  const int wave = tid / kWave, lane = tid % kWave;
-  // headers of the packed x rows: one wave per token, lanes over the partials
-  for (int t = wave; t < a.T; t += kRouterWaves) {
-    int nl = 1;
-    uint32_t sum = 0;
-    for (int bx = lane; bx < nbx; bx += kWave) {
-      const uint32_t* pp = a.xpart + ((size_t)t * nbx + bx) * 2;
-      nl = (int)pp[0] > nl ? (int)pp[0] : nl;
-      sum += pp[1];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const int on = __shfl_xor(nl, off, kWave);
-      nl = on > nl ? on : nl;
-      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
-    }
-    if (lane == 0) {
-      uint32_t* hh = reinterpret_cast<uint32_t*>(a.xtab + (size_t)t * a.tab_bytes);
-      hh[0] = (uint32_t)nl;
-      hh[1] = sum;
-    }
-  }
-  for (int t = wave; t < a.T; t += kRouterWaves) {
-    const size_t q = (size_t)t * K;
-    select_token<C>(a.logits + (size_t)t * E, E, K, sidx[wave], sval[wave], sexp[wave],
-                    a.idx + q, a.p + q, a.idx_user ? a.idx_user + q : nullptr,
-                    a.p_user ? a.p_user + q : nullptr);
-  }
-}
-
-// Router logits (test_model_trace.c:465-468).  Block (bx, by) = 8 experts x
-// up to 8 tokens: the experts' rows and the tokens' x are staged in LDS
-// (rows padded by 16 bytes against bank conflicts); wave 0 runs the 64
-// sequential chains, one per lane, while the other waves pack column slice
-// bx of the tokens' x for the expert GEMVs.  The last block to finish
-// selects the experts (router_finish).
-template <bool Q4>
-__global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
-  extern __shared__ float lds[];
-  __shared__ int red_nl[kRouterTokens];
-  __shared__ unsigned red_sum[kRouterTokens];
-  const int tid = threadIdx.x, wave = tid / kWave;
-  const int e0 = blockIdx.x * kRouterExperts;
-  const int t0 = blockIdx.y * a.tb;
-  const int ntb = a.T - t0 < a.tb ? a.T - t0 : a.tb;
-  const int D = a.D, E = a.E, Dp = D + kRowPad;
-  float* Wl = lds;                           // [8][Dp]
-  float* Xl = lds + kRouterExperts * Dp;     // [tb][Dp]
-  if (a.staged) {
-    // per column block of blockDim float4: the 8 weight rows and the tokens'
-    // x rows are loaded into registers first, then stored (one memory latency)
-    const int d4 = D / 4, p4 = Dp / 4;
-    for (int c = tid; c < d4; c += blockDim.x) {
-      float4 vw[kRouterExperts], vx[kRouterTokens];
-#pragma unroll
-      for (int r = 0; r < kRouterExperts; ++r)
-        vw[r] = e0 + r < E ? reinterpret_cast<const float4*>(a.W + (size_t)(e0 + r) * D)[c]
-                           : make_float4(0, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < kRouterTokens; ++r)
-        vx[r] = reinterpret_cast<const float4*>(a.xn + (size_t)(t0 + (r < ntb ? r : 0)) * D)[c];
-#pragma unroll
-      for (int r = 0; r < kRouterExperts; ++r) reinterpret_cast<float4*>(Wl)[r * p4 + c] = vw[r];
-#pragma unroll
-      for (int r = 0; r < kRouterTokens; ++r)
-        if (r < ntb) reinterpret_cast<float4*>(Xl)[r * p4 + c] = vx[r];
-    }
-  }
-  if (tid < kRouterTokens) { red_nl[tid] = 1; red_sum[tid] = 0; }
-  __syncthreads();
-  if (wave == 0) {
-    const int tl = tid / kRouterExperts, g = tid % kRouterExperts;
-    const int t = t0 + tl, e = e0 + g;
-    if (tl < ntb && e < E) {
-      float acc;
-      if (a.staged) {
-        acc = seq_dot_lane(Xl + (size_t)tl * Dp, Wl + (size_t)g * Dp, D);
-      } else {
-        const float* x = a.xn + (size_t)t * D;
-        const float* w = a.W + (size_t)e * D;
-        acc = 0.0f;
-        for (int k = 0; k < D; ++k) {
-          const float pk = x[k] * w[k];
-          acc = acc + pk;
-        }
-      }
-      a.logits[(size_t)t * E + e] = a.b ? acc + a.b[e] : acc;
-    }
-  } else {
-    const int c0 = blockIdx.x * a.cols;
-    const int c1 = c0 + a.cols < D ? c0 + a.cols : D;
-    for (int tl = 0; tl < ntb; ++tl) {
-      const float* x = a.staged ? Xl + (size_t)tl * Dp : a.xn + (size_t)(t0 + tl) * D;
-      int nl;
-      uint32_t sum;
-      pack_act_cols<Q4>(x, D, c0, c1 > c0 ? c1 : c0, a.xtab + (size_t)(t0 + tl) * a.tab_bytes,
-                        tid - kWave, blockDim.x - kWave, nl, sum);
-      atomicMax(&red_nl[tl], nl);
-      atomicAdd(&red_sum[tl], sum);
-    }
-  }
-  __syncthreads();
-  if (tid < ntb) {
-    uint32_t* pp = a.xpart + ((size_t)(t0 + tid) * gridDim.x + blockIdx.x) * 2;
-    pp[0] = (uint32_t)red_nl[tid];
-    pp[1] = red_sum[tid];
-  }
-  if (!last_block_in(a.counter, gridDim.x * gridDim.y)) return;
-  if (E <= 64) router_finish<Q4, 1>(a);
-  else if (E <= 128) router_finish<Q4, 2>(a);
-  else if (E <= 256) router_finish<Q4, 4>(a);
-  else router_finish<Q4, 16>(a);
-}
-
 
 // Marks the untiled expert path: one wave per row, int32 arithmetic on the
 // fp32 activations (any row size; used for small or irregular layers).
@@ -357,13 +150,13 @@ struct DownEpiMaker {
 // y_j for ranks j = w, w+8, ... into LDS; then out[t, o] = x_resid +
 // (((0 + p0 y0) + p1 y1) + ...) in rank order (test_model_trace.c:502-517).
 template <bool Q4, class G>
-__global__ __launch_bounds__(kRouterThreads) void down_combine_kernel(DownArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs a) {
   extern __shared__ float yb[];   // [topk][rows_per_block]
   const int t = blockIdx.y;
   const int r0 = blockIdx.x * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.D ? r0 + a.rows_per_block : a.D;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  for (int j = wave; j < a.topk; j += kRouterWaves) {
+  for (int j = wave; j < a.topk; j += kCombineWaves) {
     const int q = t * a.topk + j;
     const int e = a.idx[q];
     if (e < 0) continue;
@@ -407,22 +200,25 @@ __global__ __launch_bounds__(kRouterThreads) void down_combine_kernel(DownArgs a
   }
 }
 
-// rmsnorm (test_model_trace.c:241-255): one block per token; the row is
-// staged in LDS and the sum of squares is one sequential chain in lane 0.
+// rmsnorm (test_model_trace.c:241-255): one block per token; the squares
+// x_i * x_i are formed by all threads into LDS and thread 0 sums them in
+// order with pure dependent adds (msq / D, 1 / sqrtf(msq + eps)).
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       float* __restrict__ y, int D, float eps,
                                                       int fast) {
-  extern __shared__ float xs[];
+  extern __shared__ float4 sq4[];
   __shared__ float inv_s;
   const int t = blockIdx.x;
   const float* xt = x + (size_t)t * D;
   if (fast) {
-    for (int i = threadIdx.x; i < D / 4; i += blockDim.x)
-      reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(xt)[i];
+    for (int i = threadIdx.x; i < D / 4; i += blockDim.x) {
+      const float4 v = reinterpret_cast<const float4*>(xt)[i];
+      sq4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-      const float acc = seq_dot_lane(xs, xs, D);
+      const float acc = chain_sum(0.0f, reinterpret_cast<const float*>(sq4), D / 4);
       const float msq = acc / (float)D;
       inv_s = 1.0f / sqrtf(msq + eps);
     }
@@ -465,8 +261,8 @@ struct ScratchBuf {
   size_t bytes = 0;
 };
 struct SharedScratch {
-  ScratchBuf logits, idx, p, xtab, htab, h, xn, xpart, hpart, ecount, eoff, perm, y;
-  unsigned* counters = nullptr;   // router last-block counter, zero between launches
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, ecount, eoff, perm, y;
+  unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
 };
 SharedScratch g_scratch;
 std::mutex g_layer_mu;
@@ -493,28 +289,27 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   bool synced = false;
   moe_status st;
   const size_t np = (size_t)T * L->topk;
-  const size_t nbx = (size_t)(L->E + kRouterExperts - 1) / kRouterExperts;
   if ((st = grow(S.logits, (size_t)T * L->E * 4, &synced)) || (st = grow(S.idx, np * 4, &synced)) ||
       (st = grow(S.p, np * 4, &synced)) ||
       (st = grow(S.xtab, (size_t)T * act_table_bytes(L->D), &synced)) ||
       (st = grow(S.htab, np * act_table_bytes(L->dff), &synced)) ||
       (st = grow(S.h, np * L->dff * 4, &synced)) || (st = grow(S.xn, (size_t)T * L->D * 4, &synced)) ||
-      (st = grow(S.xpart, (size_t)T * nbx * 8, &synced)) ||
       (st = grow(S.hpart, np * (size_t)((L->dff + 7) / 8) * 8, &synced)))
     return st;
   if (grouped_ok(L) &&
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
        (st = grow(S.perm, np * 4, &synced)) || (st = grow(S.y, np * L->D * 4, &synced))))
     return st;
-  if (!S.counters) {
-    if ((st = dev_alloc(&S.counters, 1))) return st;
-    if ((st = check_hip(hipMemsetAsync(S.counters, 0, 4, stream()), "counter init"))) return st;
-  }
   L->logits = (float*)S.logits.p; L->idx = (int*)S.idx.p; L->p = (float*)S.p.p;
   L->xtab = (uint8_t*)S.xtab.p; L->htab = (uint8_t*)S.htab.p; L->h = (float*)S.h.p;
-  L->xn = (float*)S.xn.p; L->xpart = (uint32_t*)S.xpart.p; L->hpart = (uint32_t*)S.hpart.p;
+  L->xn = (float*)S.xn.p; L->hpart = (uint32_t*)S.hpart.p;
   L->ecount = (int*)S.ecount.p; L->eoff = (int*)S.eoff.p; L->perm = (int*)S.perm.p;
-  L->y = (float*)S.y.p; L->counters = S.counters;
+  if (!S.sel_counter) {
+    if ((st = dev_alloc(&S.sel_counter, 1))) return st;
+    if ((st = check_hip(hipMemsetAsync(S.sel_counter, 0, 4, stream()), "counter init"))) return st;
+  }
+  L->y = (float*)S.y.p;
+  L->sel_counter = S.sel_counter;
   L->capT = T;
   return MOE_OK;
 }
@@ -563,7 +358,7 @@ void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, floa
   DownArgs a{L->dq, L->ds, L->rbd, T, L->D, L->dff, L->topk, L->idx, L->p, L->htab,
              act_table_bytes(L->dff), L->h, L->hpart, nchunks, resid, out, (int)rpb};
   dim3 grid((unsigned)((L->D + rpb - 1) / rpb), (unsigned)T);
-  hipLaunchKernelGGL((down_combine_kernel<Q4, G>), grid, dim3(kRouterThreads),
+  hipLaunchKernelGGL((down_combine_kernel<Q4, G>), grid, dim3(kCombineThreads),
                      (size_t)L->topk * rpb * 4, s, a);
 }
 
@@ -594,38 +389,50 @@ int grouped_min_tokens(const LayerDev* L) {
   return L->grouped_min_T > 0 ? L->grouped_min_T : dflt;
 }
 
-moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T, float* out,
-                         int32_t* idx_out, float* p_out) {
+moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps);
+
+// The MoE block of T tokens.  norm_eps >= 0: `x` is the raw residual stream
+// and the block starts with rmsnorm(x, rms2_w) (:461), fused into the router
+// product for few tokens; norm_eps < 0: `x` is already x_norm.
+moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const float* resid,
+                              int T, float* out, int32_t* idx_out, float* p_out) {
   if (T <= 0) return MOE_OK;
   moe_status st = ensure_scratch(L, T);
   if (st) return st;
-  if (T >= grouped_min_tokens(L) && grouped_ok(L))
-    return layer_forward_grouped(L, xn, resid, T, out, idx_out, p_out);
   hipStream_t s = stream();
+  const bool grouped = T >= grouped_min_tokens(L) && grouped_ok(L);
+  const bool fuse_norm = norm_eps >= 0.0f && !grouped && dense_norm_ok(T, L->D) &&
+                         dense_select_ok(T, L->E) && aligned16(x) && aligned16(L->router_w);
+  const float* xn = x;
+  if (norm_eps >= 0.0f && !fuse_norm) {
+    if ((st = rmsnorm_dev(x, L->rms2_w, L->xn, T, L->D, norm_eps))) return st;
+    xn = L->xn;
+  }
+  if (grouped) return layer_forward_grouped(L, xn, resid, T, out, idx_out, p_out);
   const bool q4 = L->dtype == 3;
-  RouterArgs ra;
-  ra.xn = xn; ra.T = T; ra.D = L->D; ra.E = L->E; ra.topk = L->topk;
-  ra.W = L->router_w; ra.b = L->router_b; ra.logits = L->logits; ra.idx = L->idx; ra.p = L->p;
-  ra.idx_user = idx_out; ra.p_user = p_out; ra.xtab = L->xtab; ra.tab_bytes = act_table_bytes(L->D);
-  ra.xpart = L->xpart; ra.counter = L->counters;
-  const int nbx = (L->E + kRouterExperts - 1) / kRouterExperts;
-  ra.cols = ((L->D + nbx - 1) / nbx + 7) / 8 * 8;
-  const size_t row_bytes = (size_t)(L->D + kRowPad) * 4;
-  ra.tb = std::min(kRouterTokens, T);
-  ra.staged = (L->D % 16 == 0) && aligned16(xn) && aligned16(L->router_w) &&
-              (kRouterExperts + ra.tb) * row_bytes <= kMaxLds;
-  const size_t lds = ra.staged ? (kRouterExperts + (size_t)ra.tb) * row_bytes : 0;
-  dim3 rgrid((unsigned)nbx, (unsigned)((T + ra.tb - 1) / ra.tb));
-  const void* rfn = q4 ? (const void*)router_kernel<true> : (const void*)router_kernel<false>;
-  if (lds > 65536 &&
-      (st = check_hip(hipFuncSetAttribute(rfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                      "router LDS attribute")))
-    return st;
-  if (q4)
-    hipLaunchKernelGGL(router_kernel<true>, rgrid, dim3(kRouterThreads), lds, s, ra);
-  else
-    hipLaunchKernelGGL(router_kernel<false>, rgrid, dim3(kRouterThreads), lds, s, ra);
-  if ((st = check_hip(hipGetLastError(), "router launch"))) return st;
+  DenseArgs ra{xn, L->D, L->router_w, L->D, L->router_b, nullptr, 0, L->logits, L->E, T, L->E, L->D};
+  if (fuse_norm) {
+    // rmsnorm + x tables + router logits in one launch
+    ra.norm = 1; ra.norm_w = L->rms2_w; ra.eps = norm_eps;
+    ra.xn_out = L->xn; ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->hpart;
+    xn = L->xn;
+  } else {
+    // x tables for the expert GEMVs
+    QShape sh;
+    sh.dtype = L->dtype; sh.M = T; sh.N = 1; sh.K = L->D; sh.lda = L->D; sh.ldc = 1; sh.rs = L->rbg;
+    QJob one{nullptr, nullptr, xn, nullptr};
+    if ((st = check_hip(launch_act_pack(sh, nullptr, one, 1, L->xtab, s), "act pack"))) return st;
+  }
+  // router logits (+ bias), then top-k and gates (in the router launch's
+  // last block for few tokens)
+  const bool fuse_sel = dense_select_ok(T, L->E) && aligned16(L->router_w) &&
+                        (fuse_norm || aligned16(xn));
+  if (fuse_sel) {
+    ra.sel_counter = L->sel_counter; ra.sel_topk = L->topk;
+    ra.sel_idx = L->idx; ra.sel_p = L->p; ra.sel_idx_user = idx_out; ra.sel_p_user = p_out;
+  }
+  if ((st = dense_matmul(ra, s))) return st;
+  if (!fuse_sel && (st = launch_select(L, T, idx_out, p_out, s))) return st;
   int nchunks = 0;
   if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s); });
   else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s); });
@@ -635,10 +442,15 @@ moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T
   return check_hip(hipGetLastError(), "down launch");
 }
 
+moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T, float* out,
+                         int32_t* idx_out, float* p_out) {
+  return layer_forward_impl(L, xn, -1.0f, resid, T, out, idx_out, p_out);
+}
+
 moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps) {
   if (T <= 0) return MOE_OK;
-  const int fast = (D % 16 == 0) && aligned16(x) && (size_t)(D + kRowPad) * 4 <= kMaxLds;
-  const size_t lds = fast ? (size_t)(D + kRowPad) * 4 : 0;
+  const int fast = (D % 4 == 0) && aligned16(x) && (size_t)D * 4 <= kMaxLds;
+  const size_t lds = fast ? (size_t)D * 4 : 0;
   if (lds > 65536) {
     moe_status st = check_hip(hipFuncSetAttribute((const void*)rmsnorm_kernel,
                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -777,10 +589,9 @@ moe_status moe_block_forward(moe_layer* layer, const float* x, int T, float* out
   if (T < 0) return set_error(MOE_ERR_ARG, "block_forward: T < 0");
   LayerDev* L = &layer->L;
   if (T == 0) return MOE_OK;
+  if (!(eps >= 0.0f)) return set_error(MOE_ERR_ARG, "block_forward: eps %g < 0", (double)eps);
   std::lock_guard<std::mutex> lk(g_layer_mu);
-  if ((st = ensure_scratch(L, T))) return st;
-  if ((st = rmsnorm_dev(x, L->rms2_w, L->xn, T, L->D, eps))) return st;
-  return layer_forward(L, L->xn, x, T, out, nullptr, nullptr);
+  return layer_forward_impl(L, x, eps, x, T, out, nullptr, nullptr);
 }
 
 moe_status moe_rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps) {
