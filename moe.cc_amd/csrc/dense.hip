@@ -67,7 +67,7 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 
 // ---------------------------------------------------------------- products
 
-// Few tokens (M <= 64 / RW): a block owns RW output rows; wave 0 is the
+// Few tokens (M <= MM = 64 / RW): a block owns RW output rows; wave 0 is the
 // consumer, waves 1..NP are producers.  The weight rows and the M token rows
 // stream in chunks of KC columns with coalesced 16-byte loads; producer p
 // owns chunks p, p + NP, ... and keeps its next chunk in registers, so each
@@ -92,7 +92,8 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 // (fused selection) writes the tables' headers.
 template <int RW, bool NORM, int PACK, int NP>
 __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) {
-  constexpr int KC = 4096 / RW;
+  constexpr int KC = RW >= 16 ? 4096 / RW : 256;
+  constexpr int MM = 64 / RW;                // token rows one block can chain
   constexpr int V4 = KC / 4;                 // float4 per row chunk (<= 64)
   constexpr int LD = KC + 4;                 // padded LDS row (floats)
   constexpr int RPL = 64 / V4;               // rows one load instruction covers
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   constexpr int NT = 64 * (NP + 1);
   extern __shared__ float4 pl4[];
   float* pl = reinterpret_cast<float*>(pl4);
-  __shared__ float inv_s[4];
+  __shared__ float inv_s[MM];
   __shared__ int pack_scratch[2];
   const int M = a.M, N = a.N, K = a.K;
   const int nc = (K + KC - 1) / KC;
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   const int bufsz = M * RW * LD;
   float* xs = pl + NB * bufsz;               // NORM: [M][K] token rows
   const int c4 = lane % V4, r0 = lane / V4;
-  float4 rw[NW], rx[4];
+  float4 rw[NW], rx[MM];
   const float* wsrc[NW];
 #pragma unroll
   for (int v = 0; v < NW; ++v)
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
     const int k = c * KC + 4 * c4;
     const bool in = k < K;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < MM; ++m)
       if (m < M) {
         if constexpr (NORM)
           rx[m] = in ? *reinterpret_cast<const float4*>(xs + (size_t)m * K + k) : zero4();
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   auto produce = [&](int c) {
     float* P = pl + (c % NB) * bufsz;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < MM; ++m) {
       if (m >= M) break;
 #pragma unroll
       for (int v = 0; v < NW; ++v) {
@@ -239,8 +240,8 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       // the last block to finish selects the experts of every token (and
       // writes the activation tables' headers from the slices' partials)
       __shared__ int last;
-      __shared__ int sidx[kMaxTopK];
-      __shared__ float sval[kMaxTopK], sexp[kMaxTopK];
+      __shared__ int sidx[NP + 1][kMaxTopK];
+      __shared__ float sval[NP + 1][kMaxTopK], sexp[NP + 1][kMaxTopK];
       __threadfence();
       __syncthreads();
       if (threadIdx.x == 0) {
@@ -265,13 +266,14 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
             hh[1] = sum;
           }
         }
-        float* sv = pl;   // the product buffers are free now
-        for (int m = 0; m < M; ++m) {
+        // one wave per token; keys in the product buffers (free now)
+        uint64_t* keys = reinterpret_cast<uint64_t*>(pl) + (size_t)wave * 1024;
+        for (int m = wave; m < M; m += NP + 1) {
           const size_t o = (size_t)m * a.sel_topk;
-          select_token_block(a.C + (size_t)m * a.ldc, N, a.sel_topk, sv, sidx, sval, sexp,
-                             a.sel_idx + o, a.sel_p + o,
-                             a.sel_idx_user ? a.sel_idx_user + o : nullptr,
-                             a.sel_p_user ? a.sel_p_user + o : nullptr);
+          select_token_any(a.C + (size_t)m * a.ldc, N, a.sel_topk, keys, sidx[wave], sval[wave],
+                           sexp[wave], a.sel_idx + o, a.sel_p + o,
+                           a.sel_idx_user ? a.sel_idx_user + o : nullptr,
+                           a.sel_p_user ? a.sel_p_user + o : nullptr);
         }
       }
     }
@@ -785,7 +787,8 @@ moe_status set_lds(F* fn, size_t bytes, const char* what) {
 }
 
 size_t gemv_lds(int RW, int NP, int M, int K, bool norm) {
-  return ((size_t)(NP + 1) * M * RW * (4096 / RW + 4) + (norm ? (size_t)M * K : 0)) * 4;
+  const int KC = RW >= 16 ? 4096 / RW : 256;
+  return ((size_t)(NP + 1) * M * RW * (KC + 4) + (norm ? (size_t)M * K : 0)) * 4;
 }
 
 template <int RW, bool NORM, int PACK, int NP>
@@ -817,6 +820,8 @@ bool dense_norm_ok(int M, int K) {
          gemv_lds(16, M == 1 ? kNpOne : 1, M, K, true) <= 150 * 1024;
 }
 
+// The last block selects with one wave per token, keys (8 bytes per
+// logit, up to 1024) in the product buffers.
 bool dense_select_ok(int M, int N) { return M >= 1 && M <= 4 && N <= 1024; }
 
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
@@ -857,6 +862,8 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     return launch_gemv<16, false, 0, kNpOne>(a, s);
   } else if (a.M <= 4) {
     return launch_gemv<16, false, 0, 1>(a, s);
+  } else if (a.M <= 16) {
+    return launch_gemv<4, false, 0, 1>(a, s);
   } else if (a.M >= 256) {
     return launch_tile<4, 4, 32>(a, s);
   } else {

@@ -181,18 +181,18 @@ struct SelectArgs {
   float* p_user;
 };
 
-template <int C>
 __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs a) {
   __shared__ int sidx[kSelectWaves][kMaxTopK];
   __shared__ float sval[kSelectWaves][kMaxTopK];
   __shared__ float sexp[kSelectWaves][kMaxTopK];
+  __shared__ ulonglong2 keys2[kSelectWaves][512];   // E <= 1024 keys per wave
   const int wave = threadIdx.x / kWave;
   const int t = blockIdx.x * kSelectWaves + wave;
   if (t >= a.T) return;
   const size_t q = (size_t)t * a.topk;
-  select_token<C>(a.logits + (size_t)t * a.E, a.E, a.topk, sidx[wave], sval[wave], sexp[wave],
-                  a.idx + q, a.p + q, a.idx_user ? a.idx_user + q : nullptr,
-                  a.p_user ? a.p_user + q : nullptr);
+  select_token_any(a.logits + (size_t)t * a.E, a.E, a.topk, reinterpret_cast<uint64_t*>(keys2[wave]),
+                   sidx[wave], sval[wave], sexp[wave], a.idx + q, a.p + q,
+                   a.idx_user ? a.idx_user + q : nullptr, a.p_user ? a.p_user + q : nullptr);
 }
 
 // ---------------------------------------------------------------- group
@@ -806,10 +806,7 @@ moe_status mma_lds_attributes() {
 moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s) {
   SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out};
   dim3 sg((unsigned)((T + kSelectWaves - 1) / kSelectWaves));
-  if (L->E <= 64) hipLaunchKernelGGL(select_kernel<1>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else if (L->E <= 128) hipLaunchKernelGGL(select_kernel<2>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else if (L->E <= 256) hipLaunchKernelGGL(select_kernel<4>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
-  else hipLaunchKernelGGL(select_kernel<16>, sg, dim3(kSelectWaves * kWave), 0, s, sa);
+  hipLaunchKernelGGL(select_kernel, sg, dim3(kSelectWaves * kWave), 0, s, sa);
   return check_hip(hipGetLastError(), "select launch");
 }
 

@@ -52,67 +52,74 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
 
 // ---- routing: top-k by the insertion rule, softmax over the selection ----
 
-// (v, i) beats (w, j): valid and larger, or equal with the lower index.
-__device__ __forceinline__ bool beats(float v, int i, float w, int j) {
-  if (i < 0) return false;
-  if (j < 0) return true;
-  return v > w || (v == w && i < j);
-}
-
-template <int CTRL>
-__device__ __forceinline__ void argmax_step_dpp(float& bv, int& bi) {
-  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bv), CTRL, 0xF, 0xF, true));
-  const int oi = __builtin_amdgcn_update_dpp(-1, bi, CTRL, 0xF, 0xF, false);
-  if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-}
-
-// Wave-wide arg-max of (value, index) pairs under `beats`; every lane ends
-// with the winner.  DPP within rows of 16, then two cross-row exchanges.
-__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
-  argmax_step_dpp<0xB1>(bv, bi);    // quad_perm [1,0,3,2]
-  argmax_step_dpp<0x4E>(bv, bi);    // quad_perm [2,3,0,1]
-  argmax_step_dpp<0x141>(bv, bi);   // row_half_mirror
-  argmax_step_dpp<0x140>(bv, bi);   // row_mirror
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    const float ov = __shfl_xor(bv, off, kWave);
-    const int oi = __shfl_xor(bi, off, kWave);
-    if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+// 64-bit ordering key of logit v at index i: a larger key comes first in
+// the top-k order of test_model_trace.c:275-288 (larger value first, the
+// lower index first among equal values).  High word: the value's bits
+// mapped to an order-preserving unsigned integer (-0 folded to +0), or 0
+// when v is NaN or -inf, which the insertion rule never selects; low word:
+// 0xFFFFFFFF - i.
+__device__ __forceinline__ uint64_t topk_key(float v, int i) {
+  uint32_t k = 0;
+  if (v > -__builtin_inff()) {
+    const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
+    k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   }
+  return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
 }
 
-// One wave selects the experts of one token and their gates:
-//   top-k by repeated arg-max (the largest remaining logit, lowest index
-//   among equals) = the insertion rule of test_model_trace.c:275-288; NaN
-//   and -inf never selected, slots left over keep index -1;
-//   p_i = expf(v_i - max) / (sum + 1e-9f), sum in slot order (:482-487).
-// C = candidates per lane (E <= 64*C).  sidx/sval/sexp: this wave's LDS
-// slots (kMaxTopK each).  Outputs are per-token rows of K entries; the user
-// copies may be null.
+// One wave selects the experts of one token: every lane ranks its
+// candidates e = lane + 64c (c < C, E <= 64*C) among the token's E logits,
+// rank = number of keys above the candidate's (topk_key), and a live
+// candidate (not NaN, not -inf) with rank < K takes slot `rank` -- the
+// result of the insertion rule of test_model_trace.c:275-288 computed
+// without a serial pass; slots left over keep index -1.  Then
+// p_i = expf(v_i - max) / (sum + 1e-9f), sum in slot order (:482-487).
+// keys: this wave's LDS scratch of E uint64 (16-byte aligned);
+// sidx/sval/sexp: its LDS slots (kMaxTopK each).  Outputs are rows of K
+// entries; the user copies may be null.
 template <int C>
-__device__ void select_token(const float* __restrict__ logit_row, int E, int K, int* sidx,
-                             float* sval, float* sexp, int* idx, float* p, int* idx_user,
-                             float* p_user) {
+__device__ void select_token(const float* __restrict__ logit_row, int E, int K, uint64_t* keys,
+                             int* sidx, float* sval, float* sexp, int* idx, float* p,
+                             int* idx_user, float* p_user) {
   const int lane = threadIdx.x % kWave;
   float v[C];
-  bool live[C];
+  uint64_t kc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int e = lane + kWave * c;
     v[c] = e < E ? logit_row[e] : -__builtin_inff();
-    live[c] = e < E && v[c] > -__builtin_inff();   // false for NaN and -inf
+    kc[c] = topk_key(v[c], e);
+    if (e < E) keys[e] = kc[c];
   }
-  for (int r = 0; r < K; ++r) {
-    float bv = -__builtin_inff();
-    int bi = -1;
+  if (lane < K) { sidx[lane] = -1; sval[lane] = -__builtin_inff(); }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  int rank[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c)
-      if (live[c] && beats(v[c], lane + kWave * c, bv, bi)) { bv = v[c]; bi = lane + kWave * c; }
-    wave_argmax(bv, bi);
+  for (int c = 0; c < C; ++c) rank[c] = 0;
+  const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(keys);
+  int j = 0;
+  for (; j + 8 <= E; j += 8) {
+    ulonglong2 w[4];
 #pragma unroll
-    for (int c = 0; c < C; ++c)
-      if (bi == lane + kWave * c) live[c] = false;
-    if (lane == 0) { sidx[r] = bi; sval[r] = bi >= 0 ? bv : -__builtin_inff(); }
+    for (int u = 0; u < 4; ++u) w[u] = k2[j / 2 + u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < C; ++c) rank[c] += (int)(w[u].x > kc[c]) + (int)(w[u].y > kc[c]);
+  }
+  for (; j < E; ++j) {
+    const uint64_t w = keys[j];
+#pragma unroll
+    for (int c = 0; c < C; ++c) rank[c] += (int)(w > kc[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int e = lane + kWave * c;
+    if (e < E && v[c] > -__builtin_inff() && rank[c] < K) {
+      sidx[rank[c]] = e;
+      sval[rank[c]] = v[c];
+    }
   }
   __threadfence_block();
   __builtin_amdgcn_wave_barrier();
@@ -137,72 +144,15 @@ __device__ void select_token(const float* __restrict__ logit_row, int E, int K, 
   __builtin_amdgcn_wave_barrier();
 }
 
-// Block-wide selection for one token (any block size, E <= 1024): every
-// thread ranks its candidates among all E logits, rank = number of live
-// logits that beat it (larger, or equal with a lower index; NaN and -inf
-// are never live), and a live candidate with rank < K takes slot `rank`.
-// This is the result of the insertion rule of test_model_trace.c:275-288
-// (ties keep the lower index first, NaN / -inf never enter, leftover slots
-// keep index -1), computed without a serial pass.  Then wave 0 forms the
-// softmax over the slots (:482-487) as select_token does.  sv: LDS scratch
-// of E floats, 16-byte aligned; all threads of the block must call this.
-__device__ __forceinline__ void select_token_block(const float* __restrict__ logit_row, int E,
-                                                  int K, float* sv, int* sidx, float* sval,
-                                                  float* sexp, int* idx, float* p,
-                                                  int* idx_user, float* p_user) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  for (int e = tid; e < E; e += nt) sv[e] = logit_row[e];
-  if (tid < K) { sidx[tid] = -1; sval[tid] = -__builtin_inff(); }
-  __syncthreads();
-  for (int i = tid; i < E; i += nt) {
-    const float vi = sv[i];
-    if (!(vi > -__builtin_inff())) continue;
-    // w beats vi iff w > vi, or w == vi at a lower index; NaN and -inf
-    // never beat a live vi, so no liveness test is needed for w
-    int rank = 0;
-    int j = 0;
-    const float4* sv4 = reinterpret_cast<const float4*>(sv);
-    for (; j + 32 <= E; j += 32) {
-      float4 w[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) w[u] = sv4[j / 4 + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int jj = j + 4 * u;
-        rank += (int)((w[u].x > vi) | ((w[u].x == vi) & (jj < i)));
-        rank += (int)((w[u].y > vi) | ((w[u].y == vi) & (jj + 1 < i)));
-        rank += (int)((w[u].z > vi) | ((w[u].z == vi) & (jj + 2 < i)));
-        rank += (int)((w[u].w > vi) | ((w[u].w == vi) & (jj + 3 < i)));
-      }
-    }
-    for (; j < E; ++j) {
-      const float w = sv[j];
-      rank += (int)((w > vi) | ((w == vi) & (j < i)));
-    }
-    if (rank < K) { sidx[rank] = i; sval[rank] = vi; }
-  }
-  __syncthreads();
-  if (tid < kWave) {
-    const int lane = tid;
-    if (lane < K) {
-      float mx = sval[0];
-      for (int i = 1; i < K; ++i) if (sval[i] > mx) mx = sval[i];
-      sexp[lane] = expf_glibc(sval[lane] - mx);
-    }
-    __threadfence_block();
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    for (int i = 0; i < K; ++i) sum = sum + sexp[i];
-    const float inv = 1.0f / (sum + 1e-9f);
-    if (lane < K) {
-      const float pv = sexp[lane] * inv;
-      idx[lane] = sidx[lane];
-      p[lane] = pv;
-      if (idx_user) idx_user[lane] = sidx[lane];
-      if (p_user) p_user[lane] = pv;
-    }
-  }
-  __syncthreads();
+// select_token with the candidates-per-lane count chosen for E (<= 1024).
+__device__ __forceinline__ void select_token_any(const float* logit_row, int E, int K,
+                                                 uint64_t* keys, int* sidx, float* sval,
+                                                 float* sexp, int* idx, float* p, int* idx_user,
+                                                 float* p_user) {
+  if (E <= 64) select_token<1>(logit_row, E, K, keys, sidx, sval, sexp, idx, p, idx_user, p_user);
+  else if (E <= 128) select_token<2>(logit_row, E, K, keys, sidx, sval, sexp, idx, p, idx_user, p_user);
+  else if (E <= 256) select_token<4>(logit_row, E, K, keys, sidx, sval, sexp, idx, p, idx_user, p_user);
+  else select_token<16>(logit_row, E, K, keys, sidx, sval, sexp, idx, p, idx_user, p_user);
 }
 
 }  // namespace moe
