@@ -275,8 +275,9 @@ moe_status moe_model_reset(moe_model* m);
 int moe_model_position(const moe_model* m);
 /* T new tokens at the current position (ids on the device if ids_on_device,
  * else host ids checked against [0, vocab)); K/V appended to the cache.
- * The last row's logits go to logits_dev [vocab] and its greedy choice (first
- * index of the largest logit) to next_dev [1] (device int32); either may be
+ * The last row's logits go to logits_dev [vocab] and the next token the
+ * reference would pick (first index of the largest softmax_rows probability,
+ * test_model_trace.c:735-746) to next_dev [1] (device int32); either may be
  * NULL.  Bit-identical to the reference's last-row logits for the whole
  * sequence so far. */
 moe_status moe_model_forward(moe_model* m, const int32_t* ids, int T, int ids_on_device,
@@ -295,6 +296,20 @@ moe_status moe_model_forward_full(moe_model* m, const int32_t* ids, int T, int a
  * decode steps.  Synchronous. */
 moe_status moe_model_generate(moe_model* m, const int32_t* prompt, int n_prompt, int n_new,
                               int32_t* out_ids, float* ms_prompt, float* ms_decode);
+
+/* The reference's next-token choice (test_model_trace.c:735-746): softmax_rows
+ * of the n logits, then the first index of the largest probability.  Equal
+ * probabilities keep the lower index, also for logits that differ but round
+ * to the same probability; a NaN or +inf logit, or all -inf, gives 0.
+ * Device pointers; next: one int32. */
+moe_status moe_greedy_dev(const float* logits, int n, int32_t* next);
+/* The head and the choice in one pass, as the decode loop runs them
+ * (test_model_trace.c:571, :735-746): logits [N] = W [N x K] . x [K] with the
+ * sequential fp32 chains of moe_matmul_f32_dev, then next = moe_greedy_dev's
+ * answer, the product's blocks handing their maxima to the choice.  Device
+ * pointers; logits may not be NULL. */
+moe_status moe_head_greedy_dev(const float* x, const float* W, int N, int K, float* logits,
+                               int32_t* next);
 
 /* Name of the kernel variant the GEMV entry points use for a shape. */
 const char* moe_gemv_variant(int dtype, int M, int N, int K);

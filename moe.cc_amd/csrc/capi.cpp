@@ -300,6 +300,45 @@ moe_status moe_matmul_f32_dev(const float* A, const float* W, float* C, int M, i
   return dense_matmul(a, g_stream);
 }
 
+moe_status moe_greedy_dev(const float* logits, int n, int32_t* next) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (!logits || !next) return set_error(MOE_ERR_ARG, "greedy: null pointer");
+  return greedy_vec(logits, n, nullptr, 0, next, nullptr, nullptr, g_stream);
+}
+
+namespace {
+float* g_head_part = nullptr;   // block maxima of moe_head_greedy_dev (grown, never freed)
+size_t g_head_part_n = 0;
+}  // namespace
+
+moe_status moe_head_greedy_dev(const float* x, const float* W, int N, int K, float* logits,
+                               int32_t* next) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (!x || !W || !logits || !next) return set_error(MOE_ERR_ARG, "head_greedy: null pointer");
+  if (N <= 0 || K <= 0) return set_error(MOE_ERR_ARG, "head_greedy: N = %d, K = %d", N, K);
+  DenseArgs a{x, K, W, K, nullptr, nullptr, 0, logits, N, 1, N, K};
+  if (!dense_amax_ok(a)) {
+    if ((st = dense_matmul(a, g_stream))) return st;
+    return greedy_vec(logits, N, nullptr, 0, next, nullptr, nullptr, g_stream);
+  }
+  const size_t need = (size_t)N / 16 + 1;
+  if (need > g_head_part_n) {
+    if (g_head_part) {
+      if ((st = check_hip(hipStreamSynchronize(g_stream), "head_greedy sync"))) return st;
+      (void)hipFree(g_head_part);
+      g_head_part = nullptr;
+      g_head_part_n = 0;
+    }
+    if ((st = check_hip(hipMalloc(&g_head_part, need * 4), "head_greedy scratch"))) return st;
+    g_head_part_n = need;
+  }
+  a.amax_part = g_head_part;
+  if ((st = dense_matmul(a, g_stream))) return st;
+  return greedy_vec(logits, N, g_head_part, dense_amax_rows(N), next, nullptr, nullptr, g_stream);
+}
+
 moe_status moe_matmul_adaptive_dev(const float* A, const float* W_fp32, const QuantizedWeight* W_q,
                                    float* C, int M, int N, int K) {
   if (!W_q) return moe_matmul_f32_dev(A, W_fp32, C, M, N, K);

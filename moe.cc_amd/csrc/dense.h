@@ -47,8 +47,14 @@ struct DenseArgs {
   float* sel_p = nullptr;
   int32_t* sel_idx_user = nullptr;
   float* sel_p_user = nullptr;
+  // Optional, one token (dense_amax_ok): each block of dense_amax_rows(N)
+  // consecutive outputs also writes its largest value (NaN if it has one)
+  // to amax_part[block], for greedy_vec.
+  float* amax_part = nullptr;
 };
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s);
+bool dense_amax_ok(const DenseArgs& a);
+int dense_amax_rows(int N);
 // Whether dense_matmul can fuse the rmsnorm for M rows of K columns.
 bool dense_norm_ok(int M, int K);
 // Whether dense_matmul can fuse the expert selection (M tokens, N experts).
@@ -89,11 +95,13 @@ struct AttnArgs {
 };
 moe_status attention_rows(const AttnArgs& a, hipStream_t s);
 
-// Greedy choice over n logits: the first index of the largest value
-// (test_model_trace.c:742-746); written to *out and, if out_hist, to
-// out_hist[*hist_pos] with *hist_pos incremented (device counters).
-moe_status argmax_vec(const float* v, int n, int32_t* out, int32_t* out_hist, int32_t* hist_pos,
-                      hipStream_t s);
+// The reference's next token over n logits (test_model_trace.c:735-746):
+// the first index of the largest softmax_rows probability.  part / rows:
+// the head product's block maxima (DenseArgs::amax_part) or null.  Written
+// to *out and, if out_hist, to out_hist[*hist_pos] with *hist_pos
+// incremented (device counters).
+moe_status greedy_vec(const float* v, int n, const float* part, int rows, int32_t* out,
+                      int32_t* out_hist, int32_t* hist_pos, hipStream_t s);
 
 // softmax_rows (test_model_trace.c:260-272) of one row of n values in place.
 moe_status softmax_vec(float* v, int n, hipStream_t s);

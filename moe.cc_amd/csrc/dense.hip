@@ -12,6 +12,7 @@
 // a chunk ahead, so that the chain, not the memory, sets the pace (a
 // dependent v_add_f32 every ~8 clocks).  Order-free steps (max, expf, the
 // products of the softmax) run across lanes.
+#include <climits>
 #include <math.h>
 
 #include <mutex>
@@ -56,6 +57,11 @@ __device__ __forceinline__ float chain_dot(float acc, const float* x, const floa
     acc = acc + p3;
   }
   return acc;
+}
+
+// max(a, b), NaN when either is NaN
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);
 }
 
 __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n, float acc) {
@@ -233,7 +239,17 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       if (live) acc = chain_sum(acc, pl + (c % NB) * bufsz + lane * LD, V4);
     }
     const int n = n0 + r;
-    if (live && n < N) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
+    float c = -__builtin_inff();
+    if (live && n < N) {
+      c = dense_epilogue(a, m, n, acc);
+      a.C[(size_t)m * a.ldc + n] = c;
+    }
+    if (a.amax_part) {   // M == 1: the block's largest output, NaN if any is NaN
+      float v = c;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off, kWave));
+      if (lane == 0) a.amax_part[blockIdx.x] = v;
+    }
   }
   if constexpr (RW == 16) {
     if (a.sel_counter) {
@@ -675,45 +691,72 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
   for (int i = threadIdx.x; i < D; i += 256) dst[i] = src[i];
 }
 
-// (v, i) beats (w, j): v is not NaN and (larger, or equal with a lower index)
-__device__ __forceinline__ bool am_beats(float v, int i, float w, int j) {
-  if (i < 0 || v != v) return false;
-  if (j < 0) return true;
-  return v > w || (v == w && i < j);
-}
+constexpr int kGreedyThreads = 1024;
 
-constexpr int kArgThreads = 1024;
-
-__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ v, int n,
-                                                             int32_t* out, int32_t* hist,
-                                                             int32_t* hist_pos) {
-  __shared__ float bv_s[kArgThreads / kWave];
-  __shared__ int bi_s[kArgThreads / kWave];
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  float bv = 0.0f;
-  int bi = -1;
-  for (int i = tid; i < n; i += kArgThreads) {
-    const float x = v[i];
-    if (am_beats(x, i, bv, bi)) { bv = x; bi = i; }
-  }
+// The smallest v over the block (all threads get it); red: one int per wave.
+__device__ int block_min(int v, int* red) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, kWave);
-    const int oi = __shfl_xor(bi, off, kWave);
-    if (am_beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    const int o = __shfl_xor(v, off, kWave);
+    v = o < v ? o : v;
   }
-  if (lane == 0) { bv_s[wave] = bv; bi_s[wave] = bi; }
   __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < (int)blockDim.x / kWave; ++w) v = red[w] < v ? red[w] : v;
+  return v;
+}
+
+// The reference's next token (test_model_trace.c:735-746): softmax_rows of
+// the logits, then the first index of the largest probability.  With m the
+// largest logit: a NaN or +inf logit, or m = -inf, turns every probability
+// into NaN and the scan stays at 0.  Otherwise e_i = expf(v_i - m) <= 1
+// with e = 1 at the maximum, the probabilities are e_i * inv with a normal
+// inv = 1 / (sum + 1e-9) (sum >= 1), and any e_i <= 1 - 2^-24 gives a
+// product that rounds below inv (the exact (1 - 2^-24) inv is at least
+// half an ulp of inv under it, and exactly representable when it is only
+// that), so the answer is the first i with expf(v_i - m) == 1.
+// part (optional): the largest value of every block of `rows` consecutive
+// logits (NaN if the block holds one), written by the head's product; only
+// the first block whose maximum qualifies is then scanned.
+__global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(const float* __restrict__ v, int n,
+                                                               const float* __restrict__ part,
+                                                               int rows, int32_t* out,
+                                                               int32_t* hist, int32_t* hist_pos) {
+  __shared__ float fred[kGreedyThreads / kWave];
+  __shared__ int ired[kGreedyThreads / kWave];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const float* src = part ? part : v;
+  const int ns = part ? (n + rows - 1) / rows : n;
+  float mx = -__builtin_inff();
+  for (int i = tid; i < ns; i += kGreedyThreads) mx = nan_max(mx, src[i]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = nan_max(mx, __shfl_xor(mx, off, kWave));
+  if (lane == 0) fred[wave] = mx;
+  __syncthreads();
+  float m = fred[0];
+  for (int w = 1; w < kGreedyThreads / kWave; ++w) m = nan_max(m, fred[w]);
+  int ans = 0;
+  if (m == m && m != __builtin_inff() && m != -__builtin_inff()) {
+    int first = INT_MAX;
+    for (int i = tid; i < ns; i += kGreedyThreads)
+      if (expf_glibc(src[i] - m) == 1.0f) { first = i; break; }
+    first = block_min(first, ired);
+    if (part && first != INT_MAX) {
+      const int lo = first * rows, hi = min(n, lo + rows);
+      first = INT_MAX;
+      for (int i = lo + tid; i < hi; i += kGreedyThreads)
+        if (expf_glibc(v[i] - m) == 1.0f) { first = i; break; }
+      first = block_min(first, ired);
+    }
+    ans = first == INT_MAX ? 0 : first;
+  }
   if (tid == 0) {
-    for (int w = 1; w < kArgThreads / kWave; ++w)
-      if (am_beats(bv_s[w], bi_s[w], bv, bi)) { bv = bv_s[w]; bi = bi_s[w]; }
-    // the scan starts from index 0: a NaN there is never replaced
-    const float v0 = v[0];
-    const int r = (v0 != v0 || bi < 0) ? 0 : bi;
-    out[0] = r;
+    out[0] = ans;
     if (hist) {
       const int p = *hist_pos;
-      hist[p] = r;
+      hist[p] = ans;
       *hist_pos = p + 1;
     }
   }
@@ -824,8 +867,21 @@ bool dense_norm_ok(int M, int K) {
 // logit, up to 1024) in the product buffers.
 bool dense_select_ok(int M, int N) { return M >= 1 && M <= 4 && N <= 1024; }
 
+bool dense_amax_ok(const DenseArgs& a) {
+  return a.M == 1 && a.K > 0 && a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) &&
+         al16(a.W) && !a.norm && !a.sel_counter;
+}
+
+int dense_amax_rows(int N) { return N >= 65536 ? 64 : 16; }
+
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return MOE_OK;
+  if (a.amax_part) {
+    if (!dense_amax_ok(a))
+      return set_error(MOE_ERR_ARG, "dense matmul: block maxima need one aligned row");
+    return dense_amax_rows(a.N) == 64 ? launch_gemv<64, false, 0, 1>(a, s)
+                                      : launch_gemv<16, false, 0, kNpOne>(a, s);
+  }
   if (a.sel_counter && (!dense_select_ok(a.M, a.N) || a.sel_topk < 1 || a.sel_topk > kMaxTopK ||
                         a.ldc != a.N))
     return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs M <= 4, N <= 1024");
@@ -913,10 +969,13 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   return check_hip(hipGetLastError(), "softmax/pv launch");
 }
 
-moe_status argmax_vec(const float* v, int n, int32_t* out, int32_t* out_hist, int32_t* hist_pos,
-                      hipStream_t s) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgThreads), 0, s, v, n, out, out_hist, hist_pos);
-  return check_hip(hipGetLastError(), "argmax launch");
+moe_status greedy_vec(const float* v, int n, const float* part, int rows, int32_t* out,
+                      int32_t* out_hist, int32_t* hist_pos, hipStream_t s) {
+  if (n <= 0) return set_error(MOE_ERR_ARG, "greedy: %d logits", n);
+  if (part && rows <= 0) return set_error(MOE_ERR_ARG, "greedy: %d rows per partial", rows);
+  hipLaunchKernelGGL(greedy_kernel, dim3(1), dim3(kGreedyThreads), 0, s, v, n, part, rows, out,
+                     out_hist, hist_pos);
+  return check_hip(hipGetLastError(), "greedy launch");
 }
 
 moe_status softmax_vec(float* v, int n, hipStream_t s) {

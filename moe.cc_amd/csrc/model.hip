@@ -66,6 +66,7 @@ struct moe_model {
   Buf x, xa, xn, qkv, H, S, ids;
   float* xf = nullptr;
   float* logits = nullptr;
+  float* head_part = nullptr;   // block maxima of the head's product
   int32_t* next = nullptr;      // greedy choice of the last forward
   int32_t* hist_pos = nullptr;  // generation counter
   Buf hist;
@@ -121,7 +122,7 @@ void free_model(moe_model* m) {
   m->lm_head = nullptr;
   dfree(m->tok_emb); dfree(m->final_norm); dfree(m->kc); dfree(m->vc);
   dfree(m->rope_cos); dfree(m->rope_sin); dfree(m->xf); dfree(m->logits);
-  dfree(m->next); dfree(m->hist_pos);
+  dfree(m->head_part); dfree(m->next); dfree(m->hist_pos);
   for (Buf* b : {&m->x, &m->xa, &m->xn, &m->qkv, &m->H, &m->S, &m->ids, &m->hist})
     if (b->p) (void)hipFree(b->p);
   delete m;
@@ -158,6 +159,7 @@ moe_status init_model(moe_model* m, const QwenConfig* cfg, int max_seq) {
       (st = dalloc(&m->rope_sin, (size_t)max_seq * d2, "rope")) ||
       (st = dalloc(&m->xf, (size_t)cfg->d_model, "model")) ||
       (st = dalloc(&m->logits, (size_t)cfg->vocab_size, "logits")) ||
+      (st = dalloc(&m->head_part, (size_t)cfg->vocab_size / 16 + 1, "logits")) ||
       (st = dalloc(&m->next, 1, "model")) || (st = dalloc(&m->hist_pos, 1, "model")))
     return st;
   // test_model_trace.c:310-336: inv_i = powf(theta, (-2 i) / hd), angle =
@@ -242,8 +244,12 @@ moe_status forward_dev(moe_model* m, const int32_t* ids_d, int T, float* logits_
   if ((st = moe_rmsnorm_dev(x + (size_t)(T - 1) * D, m->final_norm, m->xf, 1, D, eps))) return st;
   float* lg = logits_out ? logits_out : m->logits;
   DenseArgs ha{m->xf, D, m->lm_head, D, nullptr, nullptr, 0, lg, c.vocab_size, 1, c.vocab_size, D};
+  // the head's blocks leave their maxima for the next-token choice (:735-746)
+  const bool part = dense_amax_ok(ha);
+  if (part) ha.amax_part = m->head_part;
   if ((st = dense_matmul(ha, s))) return st;
-  if ((st = argmax_vec(lg, c.vocab_size, next_out ? next_out : m->next,
+  if ((st = greedy_vec(lg, c.vocab_size, part ? m->head_part : nullptr,
+                       part ? dense_amax_rows(c.vocab_size) : 0, next_out ? next_out : m->next,
                        record ? (int32_t*)m->hist.p : nullptr, m->hist_pos, s)))
     return st;
   m->pos += T;

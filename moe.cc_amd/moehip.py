@@ -73,6 +73,8 @@ _SIGS = {
     "moe_matmul_q8_dev": (_I, [_P, _P, _P, _P, _I, _I, _I]),
     "moe_matmul_q4_dev": (_I, [_P, _P, _P, _P, _I, _I, _I]),
     "moe_matmul_f32_dev": (_I, [_P, _P, _P, _I, _I, _I]),
+    "moe_greedy_dev": (_I, [_P, _I, _P]),
+    "moe_head_greedy_dev": (_I, [_P, _P, _I, _I, _P, _P]),
     "moe_matmul_adaptive_dev": (_I, [_P, _P, ctypes.POINTER(QuantizedWeight), _P, _I, _I, _I]),
     "moe_matmul_q_batched_dev": (_I, [_I, _P, _I, _I, _I, _I]),
     "moe_gemv_variant": (ctypes.c_char_p, [_I, _I, _I, _I]),

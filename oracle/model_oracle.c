@@ -202,12 +202,21 @@ void orc_model_forward_kv(const orc_config* cfg, const orc_weights* w, const int
   free(x);
 }
 
-/* Greedy choice: the first index of the largest logit (v > best, scanning
- * upward, the comparison test_model_trace.c:744-745 uses). */
-int orc_argmax(const float* v, int n) {
+/* The reference's choice of the next token (test_model_trace.c:735-746):
+ * softmax_rows over the logits (:736), then the first index whose
+ * probability beats every earlier one (start at index 0, replace on a
+ * strict '>').  Equal probabilities keep the lower index, also where the
+ * logits differ but round to the same probability; a NaN or +inf logit
+ * (or all -inf) turns every probability into NaN, so the answer is 0. */
+int orc_greedy(const float* v, int n) {
+  float* p = (float*)malloc(sizeof(float) * (size_t)n);
+  memcpy(p, v, sizeof(float) * (size_t)n);
+  orc_softmax_rows(p, 1, n);
   int best = 0;
+  float mx = p[0];
   for (int i = 1; i < n; ++i)
-    if (v[i] > v[best]) best = i;
+    if (p[i] > mx) { mx = p[i]; best = i; }
+  free(p);
   return best;
 }
 

@@ -106,8 +106,9 @@ void orc_model_forward_kv(const orc_config* cfg, const orc_weights* w, const int
 void orc_rope_tables(int hd, float theta, int n_pos, float* cos_out, float* sin_out);
 /* test_model_trace.c:260-272, rows of cols values in place */
 void orc_softmax_rows(float* mat, int rows, int cols);
-/* first index of the maximum (test_model_trace.c:742-746) */
-int orc_argmax(const float* v, int n);
+/* next-token choice: first index of the largest softmax_rows probability
+ * (test_model_trace.c:735-746) */
+int orc_greedy(const float* v, int n);
 
 /* export.py:23-27 rowwise Q8: s = max(amax,1e-8)/127, q = round-half-even(w/s) */
 void orc_quant_q8_rows(const float* W, int N, int K, int8_t* q, float* s);

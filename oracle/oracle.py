@@ -53,7 +53,7 @@ _ORC_SIGS = {
     "orc_layer_rows": (None, [_P, _P, _P, _I, _I, _P, _P, _I]),
     "orc_model_forward_kv": (None, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P]),
     "orc_rope_tables": (None, [_I, ctypes.c_float, _I, _P, _P]),
-    "orc_argmax": (_I, [_P, _I]),
+    "orc_greedy": (_I, [_P, _I]),
     "orc_softmax_rows": (None, [_P, _I, _I]),
 }
 
@@ -371,22 +371,24 @@ class TinyModel:
         return (out, x) if return_x else out
 
     def generate(self, prompt, steps, max_seq):
-        """Greedy decode: prefill the prompt, then `steps` tokens (argmax)."""
+        """Greedy decode: prefill the prompt, then `steps` tokens (greedy)."""
         cache = self.new_cache(max_seq)
         logits = self.forward_kv(prompt, 0, cache)
         out = []
         pos = len(prompt)
         for _ in range(steps):
-            nxt = argmax(logits)
+            nxt = greedy(logits)
             out.append(nxt)
             logits = self.forward_kv([nxt], pos, cache)
             pos += 1
         return np.array(out, np.int32), logits
 
 
-def argmax(v) -> int:
+def greedy(v) -> int:
+    """The reference's next-token choice over a logit row
+    (test_model_trace.c:735-746): argmax of softmax_rows, first index."""
     v = np.ascontiguousarray(v, dtype=np.float32)
-    return int(orc().orc_argmax(_c(v), v.size))
+    return int(orc().orc_greedy(_c(v), v.size))
 
 
 def softmax_rows(m):

@@ -232,7 +232,7 @@ def model_fixtures():
             qw3w.write(path, qw3w.model_entries(m))
             seq = [int(v) for v in (O.uniform_u32(n_prompt, 500 + len(tag)) % m.V)]
             prompt = list(seq)
-            logits_sha, picks, argmaxes = [], [], []
+            logits_sha, picks, choices = [], [], []
             for _ in range(steps + 1):
                 ids = np.array(seq, np.int32)
                 lg = np.empty(m.V, np.float32)
@@ -240,11 +240,11 @@ def model_fixtures():
                                                  lg.ctypes.data, m.V) == m.V
                 logits_sha.append(sha(lg))
                 picks.append([float(v) for v in lg[:8]])
-                nxt = int(O.argmax(lg))
-                argmaxes.append(nxt)
+                nxt = int(O.greedy(lg))
+                choices.append(nxt)
                 seq.append(nxt)
             out["cases"].append({"tag": tag, "model": kw, "prompt": prompt,
-                                 "greedy": argmaxes, "logits_sha": logits_sha,
+                                 "greedy": choices, "logits_sha": logits_sha,
                                  "logits_first8": picks})
     with open(os.path.join(OUT_DIR, "ref_model.json"), "w") as f:
         json.dump(out, f, indent=1)

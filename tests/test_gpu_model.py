@@ -63,6 +63,57 @@ def test_f32_special_values(moehip):
     np.testing.assert_array_equal(bits(f32_dev(moehip, A, W)), bits(O.matmul_f32(A, W)))
 
 
+def _planted_logits(n, seed, plant):
+    """N(0, 0.05) logits (all below 0.3) with `plant` = {index: value}
+    written over them."""
+    v = O.normal(n, seed, 0.0, 0.05).astype(np.float32)
+    for i, x in plant.items():
+        v[i] = x
+    return v
+
+
+A03 = np.float32(0.3)
+B03 = np.nextafter(A03, np.float32(0.0))          # one ulp under: same probability
+GREEDY_CASES = [  # (n, plant)
+    (151936, {140000: A03, 70001: B03}),           # tie across blocks: the lower index
+    (151936, {9: A03, 5: B03, 151935: B03}),       # tie inside one block
+    (151936, {3: A03, 100000: np.float32(np.nan)}),  # NaN anywhere -> 0
+    (151936, {77: np.float32(np.inf)}),            # +inf -> 0
+    (151936, {}),                                  # plain maximum
+    (1000, {999: A03, 500: B03}),
+    (1000, {17: np.float32(-np.inf)}),
+    (1, {}),
+]
+
+
+@pytest.mark.parametrize("n,plant", GREEDY_CASES)
+def test_greedy_dev_and_fused_head(moehip, n, plant):
+    """The next-token choice against the oracle's literal softmax + scan
+    (test_model_trace.c:735-746): the full-scan kernel on given logits, and
+    the head product with its block maxima.  With x = e_0 the product's
+    logits are W[:, 0] exactly (the other columns add signed zeros), so the
+    planted values reach the choice unchanged."""
+    print("greedy case", n, sorted(plant), flush=True)
+    v = _planted_logits(n, 60 + n, plant)
+    want = O.greedy(v)
+    dv = moehip.DeviceBuffer.from_array(v)
+    dn = moehip.DeviceBuffer(4)
+    moehip.check(moehip.lib().moe_greedy_dev(dv.ptr, n, dn.ptr), "greedy")
+    assert int(dn.download((1,), np.int32)[0]) == want
+    K = 64
+    W = O.normal(n * K, 61 + n, 0.0, 0.05).reshape(n, K)
+    W[:, 0] = v
+    x = np.zeros(K, np.float32)
+    x[0] = 1.0
+    dx, dW = moehip.DeviceBuffer.from_array(x), moehip.DeviceBuffer.from_array(W)
+    dl = moehip.DeviceBuffer(n * 4)
+    moehip.check(moehip.lib().moe_head_greedy_dev(dx.ptr, dW.ptr, n, K, dl.ptr, dn.ptr), "head")
+    lg = dl.download((n,), np.float32)
+    np.testing.assert_array_equal(bits(lg), bits(O.matmul_f32(x[None, :], W)[0]))
+    np.testing.assert_array_equal(bits(lg), bits(v))
+    assert int(dn.download((1,), np.int32)[0]) == want
+
+
 def _golden_cases():
     with open(GOLD) as f:
         return json.load(f)["cases"]
@@ -118,7 +169,7 @@ def test_model_prefill_chunks_and_decode(moehip, name):
         want = tm.forward_kv(ids[lo:hi], lo, cache)
         got, nxt = m.forward(ids[lo:hi])
         np.testing.assert_array_equal(bits(got), bits(want), err_msg=f"chunk {lo}:{hi}")
-        assert nxt == O.argmax(want)
+        assert nxt == O.greedy(want)
     seq = ids.tolist()
     for step in range(6):
         seq.append(nxt)

@@ -76,7 +76,7 @@ def test_kv_decode_matches_full_recompute(written, name):
     for step in range(6):
         np.testing.assert_array_equal(bits(got), bits(ref_logits(path, seq, m.V)),
                                       err_msg=f"step {step}")
-        nxt = O.argmax(got)
+        nxt = O.greedy(got)
         seq.append(nxt)
         got = m.forward_kv([nxt], len(seq) - 1, cache)
 
@@ -136,11 +136,76 @@ def test_rope_tables_closed_form():
     assert not np.all(np.abs(c - np.cos(ang2)) <= tol)
 
 
-def test_argmax_first_of_ties():
-    v = np.array([0.5, 2.0, -1.0, 2.0, np.nan, 1.0], np.float32)
-    assert O.argmax(v) == 1
-    assert O.argmax(np.array([np.nan, 5.0], np.float32)) == 0
-    assert O.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+def _ref_probs(v):
+    p = np.array(v, np.float32, copy=True)
+    O.ref_trace().ref_softmax_rows(p.ctypes.data, 1, p.size)
+    return p
+
+
+def _near_ties(rng, n):
+    """Logit rows whose top values sit within a few ulps of each other, so
+    that several of them round to the same probability."""
+    v = rng.normal(0.0, 1.0, n).astype(np.float32)
+    top = np.float32(rng.uniform(0.25, 4.0))
+    for j in rng.choice(n, 4, replace=False):
+        v[j] = top
+        for _ in range(int(rng.integers(0, 6))):
+            v[j] = np.nextafter(v[j], np.float32(-np.inf) if rng.random() < 0.5 else np.float32(np.inf))
+    return v
+
+
+@needs_ref
+def test_greedy_is_argmax_of_reference_softmax():
+    """O.greedy against the compiled reference's softmax_rows (:736) plus the
+    first-index scan of :740-746 (numpy's argmax returns the first maximum)."""
+    rng = np.random.default_rng(5)
+    for trial in range(300):
+        n = int(rng.integers(2, 3000))
+        v = _near_ties(rng, n) if trial % 2 else rng.normal(0, 3, n).astype(np.float32)
+        p = _ref_probs(v)
+        assert O.greedy(v) == int(np.argmax(p)), trial
+
+
+@needs_ref
+def test_greedy_known_answers():
+    """Logits one ulp apart whose probabilities are equal keep the lower
+    index (the logits' argmax would take the other); NaN or +inf anywhere,
+    or all -inf, make every probability NaN, and the scan stays at 0."""
+    a = np.float32(0.3)
+    v = np.array([-1.0, a, np.nextafter(a, np.float32(1.0)), 0.1], np.float32)
+    p = _ref_probs(v)
+    assert p[1] == p[2] and int(np.argmax(v)) == 2
+    assert O.greedy(v) == 1
+    for bad in ([1.0, np.nan, 5.0], [1.0, np.inf, 2.0], [-np.inf, -np.inf], [np.nan, 3.0]):
+        bad = np.array(bad, np.float32)
+        assert np.all(np.isnan(_ref_probs(bad)))
+        assert O.greedy(bad) == 0
+    assert O.greedy(np.array([-np.inf, 2.0, 3.0, -np.inf], np.float32)) == 2
+    assert O.greedy(np.array([0.5, 2.0, -1.0, 2.0, 1.0], np.float32)) == 1
+
+
+def test_greedy_equals_unit_exponential_rule():
+    """The rule the device uses: with m = max (finite), the answer is the
+    first i with expf(v_i - m) == 1 (the row maximum has probability
+    1 * inv exactly and any e_i < 1 rounds below it), else 0 when a NaN or
+    +inf logit is present or every logit is -inf."""
+    rng = np.random.default_rng(9)
+
+    def rule(v):
+        if np.isnan(v).any() or np.isposinf(v).any() or np.isneginf(v).all():
+            return 0
+        m = v.max()
+        e = np.empty_like(v)
+        d = (v - m).astype(np.float32)
+        O.orc().orc_expf_array(O._c(d), O._c(e), d.size)
+        return int(np.flatnonzero(e == np.float32(1.0))[0])
+
+    for trial in range(400):
+        n = int(rng.integers(1, 2000))
+        v = _near_ties(rng, n) if (trial % 2 and n >= 4) else rng.normal(0, 1, n).astype(np.float32)
+        if trial % 7 == 0:
+            v[rng.integers(0, n)] = -np.inf
+        assert O.greedy(v) == rule(v), trial
 
 
 def test_qw3w_round_trip(tmp_path):
@@ -191,7 +256,7 @@ def test_model_golden(case):
                                                        case["greedy"])):
         np.testing.assert_array_equal(lg[:8], np.array(first8, np.float32), err_msg=f"step {step}")
         assert hashlib.sha256(lg.tobytes()).hexdigest() == want_sha, f"step {step}"
-        assert O.argmax(lg) == nxt
+        assert O.greedy(lg) == nxt
         lg = m.forward_kv([nxt], pos, cache)
         pos += 1
 
