@@ -112,7 +112,9 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+// tab: the 32 table entries (kExp2Tab or a copy, e.g. in LDS, which a
+// kernel that evaluates many expf per lane reads with less latency).
+__device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   constexpr double kShift = 0x1.8p+52;
   constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -131,7 +133,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd = kd - kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki % 32];
+  uint64_t t = tab[ki % 32];
   t += ki << 47;
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(kC0, r, kC1);
@@ -141,6 +143,8 @@ __device__ __forceinline__ float expf_glibc(float x) {
   y = y * s;
   return (float)y;
 }
+
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
 
 // acc = ((acc + p0) + p1) + ... over 4*n4 values of an LDS row (16-byte
 // aligned): the sequential fp32 sum of the reference, as pure dependent adds
@@ -173,10 +177,11 @@ __device__ __forceinline__ float chain_sum(float acc, const float* p, int n4) {
 }
 
 // test_model_trace.c:233 then :500: h = (g / (1 + expf(-g))) * u
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  const float den = 1.0f + expf_glibc(-g);
+__device__ __forceinline__ float silu_mul_t(float g, float u, const uint64_t* tab) {
+  const float den = 1.0f + expf_glibc_t(-g, tab);
   const float sg = g / den;
   return sg * u;
 }
+__device__ __forceinline__ float silu_mul(float g, float u) { return silu_mul_t(g, u, kExp2Tab); }
 
 }  // namespace moe

@@ -40,6 +40,8 @@
 //       activation table hold the same columns in the same order).
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <unordered_set>
 
 #include "moe_device.h"
 #include "moe_internal.h"
@@ -462,6 +464,10 @@ struct GateUpGArgs {
   uint8_t* htab; size_t htab_bytes;
   uint32_t* hpart;   // [pair][nseg][2]
   int nseg;
+  // weight-stationary kernel: flag[e] = 1 for experts left to this kernel;
+  // this kernel: when set, only those experts
+  int* flag = nullptr;
+  const int* only_flagged = nullptr;
 };
 
 // Pairs base .. base + n - 1 (n <= 16*NT) of a pass over expert e's pairs
@@ -590,7 +596,7 @@ __global__ __launch_bounds__(kMmaThreads) void gate_up_grouped_kernel(GateUpGArg
   uint8_t* bbuf = reinterpret_cast<uint8_t*>(lds_b);
   const int e = blockIdx.y;
   const int n_all = a.ecount[e];
-  if (n_all == 0) return;
+  if (n_all == 0 || (a.only_flagged && !a.only_flagged[e])) return;
   const int first_all = a.eoff[e];
   const int lane = threadIdx.x % kWave;
   for (int p0 = 0; p0 < n_all; p0 += kPairsPerPass) {
@@ -624,10 +630,16 @@ __global__ __launch_bounds__(kMmaThreads) void gate_up_grouped_kernel(GateUpGArg
     else if (nl == 2) gate_up_nt<Q4, 2>(a, e, pass_pair, slot_tab, pass_xsum, n, bbuf, red_nl, red_sum);
     else gate_up_nt<Q4, 4>(a, e, pass_pair, slot_tab, pass_xsum, n, bbuf, red_nl, red_sum);
     if (threadIdx.x < n) {
+      // h segments are 64 rows: this block's 128 rows fill segment 2 bx,
+      // segment 2 bx + 1 gets the neutral header
       const int q = pass_pair[threadIdx.x];
-      uint32_t* pp = a.hpart + ((size_t)q * a.nseg + blockIdx.x) * 2;
+      uint32_t* pp = a.hpart + ((size_t)q * a.nseg + 2 * blockIdx.x) * 2;
       pp[0] = (uint32_t)red_nl[threadIdx.x];
       pp[1] = red_sum[threadIdx.x];
+      if (2 * (int)blockIdx.x + 1 < a.nseg) {
+        pp[2] = 1u;
+        pp[3] = 0u;
+      }
     }
     __syncthreads();
   }
@@ -642,6 +654,8 @@ struct DownGArgs {
   const uint8_t* htab; size_t htab_bytes;
   const uint32_t* hpart; int nseg;
   float* y;            // [pair][D]
+  int* flag = nullptr;               // as in GateUpGArgs
+  const int* only_flagged = nullptr;
 };
 
 template <bool Q4, int NL, int NT>
@@ -701,7 +715,7 @@ __global__ __launch_bounds__(kMmaThreads) void down_grouped_kernel(DownGArgs a) 
   uint8_t* bbuf = reinterpret_cast<uint8_t*>(lds_b);
   const int e = blockIdx.y;
   const int n_all = a.ecount[e];
-  if (n_all == 0) return;
+  if (n_all == 0 || (a.only_flagged && !a.only_flagged[e])) return;
   const int first_all = a.eoff[e];
   const int lane = threadIdx.x % kWave;
   for (int p0 = 0; p0 < n_all; p0 += kPairsPerPass) {
@@ -735,6 +749,394 @@ __global__ __launch_bounds__(kMmaThreads) void down_grouped_kernel(DownGArgs a) 
     else down_nt<Q4, 4>(a, e, pass_pair, slot_tab, n, hsum, bbuf);
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------- weight-stationary
+
+// The kernels above stream an expert's rows once per pass of up to 64 pairs;
+// these keep them in registers instead: each wave owns 16 * RT rows of one
+// expert (NM matrices, all K = KS * COLS columns, 8 VGPRs per row tile,
+// matrix and step) for the block's whole life, and the expert's pairs
+// stream past them through LDS, 16 at a time, double-buffered (the table
+// loads of the next pass are in registers while the MFMAs of this one run).
+// Every weight byte is read from HBM once per launch.  They take experts
+// whose tokens all fit one limb (|x| < 1.0079 for Q8, < 18.3 for Q4, the
+// common case) and flag the others (flag[e] = 1), which the streaming
+// kernels then process in a second launch.
+constexpr int kWsWaves = kMmaWaves;
+constexpr int kWsThreads = kWsWaves * kWave;
+// Pairs per pass: NT tiles of 16 (each unpacked weight operand feeds NT MFMAs).
+template <bool Q4, int KS, int NT>
+struct WsShape {
+  static constexpr int COLS = Step<Q4>::COLS, SL = Step<Q4>::SL, UPS = Step<Q4>::UPS;
+  static constexpr int K = KS * COLS;
+  static constexpr int SLOTS = 16 * NT;                     // pairs per pass
+  static constexpr int SLOT = K + 16;                       // slot stride (bytes)
+  static constexpr int UPL = K / 16;                        // 16-byte units per slot
+  static constexpr int U = (SLOTS * UPL + kWsThreads - 1) / kWsThreads;   // per thread
+  static constexpr int BUF = SLOTS * SLOT;                  // bytes per staging buffer
+  static_assert(2 * BUF <= kMmaLds, "two passes must fit the staging area");
+};
+
+// Stores of one pass's table units (loaded into registers) into a staging buffer.
+template <bool Q4, int KS, int NT, int U>
+__device__ __forceinline__ void ws_commit(const u32x4 (&r)[U], uint8_t* buf, int nlive) {
+  using SH = WsShape<Q4, KS, NT>;
+  const int total = nlive * SH::UPL;
+#pragma unroll
+  for (int i = 0; i < SH::U; ++i) {
+    const int u = (int)threadIdx.x + kWsThreads * i;
+    if (u < total)
+      *reinterpret_cast<u32x4*>(buf + (u / SH::UPL) * SH::SLOT + (u % SH::UPL) * 16) = r[i];
+  }
+}
+
+// acc[m][rt][tt] += W_m[rows of row tile rt] x slots 16 tt .. 16 tt + 15,
+// over all K columns, from staging buffer buf.
+// PIPE: slice k + 1's B reads and A unpacks are issued before slice k's
+// MFMAs, so the LDS latency and the VALU work overlap them (costs registers).
+template <bool Q4, int NM, int RT, int KS, int NT, bool PIPE>
+__device__ __forceinline__ void ws_mma(const WFrag (&w)[NM][RT][KS], const uint8_t* buf,
+                                       v4i (&acc)[NM][RT][NT]) {
+  using SH = WsShape<Q4, KS, NT>;
+  constexpr int NS = KS * SH::SL;   // slices
+  const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+  const uint8_t* B = buf + j * SH::SLOT + g * SH::SL * 16;
+  if constexpr (PIPE) {
+    v4i bv[NT], av[NM][RT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) bv[tt] = *reinterpret_cast<const v4i*>(B + tt * 16 * SH::SLOT);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) av[m][rt] = a_slice<Q4>(w[m][rt][0], 0);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      v4i bc[NT], ac[NM][RT];
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) bc[tt] = bv[tt];
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) ac[m][rt] = av[m][rt];
+      if (k + 1 < NS) {
+        const int st1 = (k + 1) / SH::SL, s1 = (k + 1) % SH::SL;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+          bv[tt] = *reinterpret_cast<const v4i*>(B + tt * 16 * SH::SLOT + (st1 * SH::UPS + s1) * 16);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) av[m][rt] = a_slice<Q4>(w[m][rt][st1], s1);
+      }
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt) acc[m][rt][tt] = mfma16(ac[m][rt], bc[tt], acc[m][rt][tt]);
+      // bounds the live registers to two slices
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const int st = k / SH::SL, s = k % SH::SL;
+    v4i bc[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+      bc[tt] = *reinterpret_cast<const v4i*>(B + tt * 16 * SH::SLOT + (st * SH::UPS + s) * 16);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const v4i av = a_slice<Q4>(w[m][rt][st], s);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) acc[m][rt][tt] = mfma16(av, bc[tt], acc[m][rt][tt]);
+      }
+    // bounds the live registers to two slices
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The weights become opaque to the compiler at every pass, so that it keeps
+// them packed instead of hoisting unpacked copies out of the pass loop.
+template <int NM, int RT, int KS>
+__device__ __forceinline__ void ws_opaque(WFrag (&w)[NM][RT][KS]) {
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int st = 0; st < KS; ++st)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(w[m][rt][st].w[h]));
+}
+
+// Pairs of the block's expert, prefetched into LDS at block start (up to
+// kWsChunk at a time): pair id and the activation sum of its table; the
+// epilogues' limb counts and sums of h (gate/up).
+constexpr int kWsChunk = 1024;
+struct WsPairs {
+  int pair[kWsChunk];
+  uint32_t asum[kWsChunk];
+  int red_nl[kWsChunk];
+  unsigned red_sum[kWsChunk];
+  int multi;
+};
+
+// The pass loop over pairs [0, n) of the chunk in sp (tables at tab_of(q)):
+// epi(acc, i0, nlive) consumes the dots of pairs i0 .. i0 + nlive - 1.  One
+// barrier per pass: the next pass's tables are loaded into registers before
+// this pass's MFMAs and stored into the other buffer after them.
+template <bool Q4, int NM, int RT, int KS, int NT, bool PIPE, class TabOf, class Epi>
+__device__ __forceinline__ void ws_passes(WFrag (&w)[NM][RT][KS], int n, const WsPairs& sp,
+                                          uint8_t* lds, TabOf&& tab_of, Epi&& epi) {
+  using SH = WsShape<Q4, KS, NT>;
+  const int npass = (n + SH::SLOTS - 1) / SH::SLOTS;
+  auto nlive_of = [&](int P) { return min(SH::SLOTS, n - P * SH::SLOTS); };
+  auto issue = [&](u32x4 (&r)[SH::U], int P) {
+    const int total = nlive_of(P) * SH::UPL;
+#pragma unroll
+    for (int i = 0; i < SH::U; ++i) {
+      const int u = (int)threadIdx.x + kWsThreads * i;
+      if (u < total)
+        r[i] = b_unit_load<Q4>(tab_of(sp.pair[P * SH::SLOTS + u / SH::UPL]), SH::K, 0, u % SH::UPL);
+    }
+  };
+  u32x4 r[SH::U];
+  issue(r, 0);
+  ws_commit<Q4, KS, NT>(r, lds, nlive_of(0));
+  __syncthreads();
+  for (int P = 0; P < npass; ++P) {
+    const int cur = P & 1, nxt = cur ^ 1;
+    ws_opaque(w);
+    if (P + 1 < npass) issue(r, P + 1);
+    v4i acc[NM][RT][NT];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) acc[m][rt][tt] = v4i{0, 0, 0, 0};
+    ws_mma<Q4, NM, RT, KS, NT, PIPE>(w, lds + cur * SH::BUF, acc);
+    if (P + 1 < npass) ws_commit<Q4, KS, NT>(r, lds + nxt * SH::BUF, nlive_of(P + 1));
+    epi(acc, P * SH::SLOTS, nlive_of(P));
+    __syncthreads();
+  }
+}
+
+// This lane's weight fragments: rows row0 + 16 rt + (lane % 16) of the NM
+// matrices (rows past nrows read row nrows - 1; their results are dropped).
+template <int NM, int RT, int KS>
+__device__ __forceinline__ void ws_load_weights(WFrag (&w)[NM][RT][KS], const uint8_t* const* mat,
+                                                long long rb, int row0, int nrows) {
+  const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = min(row0 + 16 * rt + j, nrows - 1);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int st = 0; st < KS; ++st) w[m][rt][st] = load_wfrag(mat[m] + (size_t)row * rb, st, g);
+  }
+}
+
+// Prefetch of pairs [c0, c0 + n) of the expert (perm positions first + i):
+// info(q) returns {limb count, activation sum} of pair q's table.  Returns
+// whether any needs more than one limb (block-wide).
+template <class Info>
+__device__ __forceinline__ bool ws_prefetch(WsPairs& sp, const int* perm, int first, int c0, int n,
+                                            Info&& info) {
+  if (threadIdx.x == 0) sp.multi = 0;
+  __syncthreads();
+  int multi = 0;
+  for (int i = threadIdx.x; i < n; i += kWsThreads) {
+    const int q = perm[first + c0 + i];
+    const int2 v = info(q);
+    sp.pair[i] = q;
+    sp.asum[i] = (uint32_t)v.y;
+    sp.red_nl[i] = 1;
+    sp.red_sum[i] = 0;
+    multi |= v.x > 1;
+  }
+  if (multi) atomicOr(&sp.multi, 1);
+  __syncthreads();
+  return sp.multi != 0;
+}
+
+constexpr int kWsDownNT = 1;                      // pair tiles per pass (down)
+
+// gate/up + SwiGLU for the rows 128 * blockIdx.x .. of expert blockIdx.y:
+// wave w owns rows 16 w .. 16 w + 15 of the block, both matrices, all K.
+template <bool Q4, int KS>
+__global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
+  constexpr int NT = 1;
+  extern __shared__ u32x4 lds_b[];
+  __shared__ WsPairs sp;
+  __shared__ uint64_t exp_tab[32];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(lds_b);
+  const int e = blockIdx.y;
+  const int n_all = a.ecount[e];
+  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;   // records the flag
+  if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  if (n_all == 0) {
+    if (rec) a.flag[e] = 0;
+    return;
+  }
+  const int first = a.eoff[e];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, g = lane / 16, j = lane % 16;
+  WFrag w[2][1][KS];
+  const uint8_t* mats[2] = {a.gq + (size_t)e * a.dff * a.rb, a.uq + (size_t)e * a.dff * a.rb};
+  ws_load_weights<2, 1, KS>(w, mats, a.rb, blockIdx.x * kMmaRows + wave * 16, a.dff);
+  const int rowq = blockIdx.x * kMmaRows + wave * 16 + 4 * g;   // this lane's 4 result rows
+  const bool live_rows = rowq < a.dff;
+  float sg[4], su[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = min(rowq + r, a.dff - 1);
+    sg[r] = a.gs[(size_t)e * a.dff + row];
+    su[r] = a.us[(size_t)e * a.dff + row];
+  }
+  const float div = Q4 ? 7.0f : 127.0f;
+  auto tab_of = [&](int q) { return a.xtab + (size_t)(q / a.topk) * a.xtab_bytes; };
+  for (int c0 = 0; c0 < n_all; c0 += kWsChunk) {
+    const int n = min(kWsChunk, n_all - c0);
+    const bool multi = ws_prefetch(sp, a.perm, first, c0, n, [&](int q) {
+      const uint8_t* tb = tab_of(q);
+      return make_int2(act_nl(tb), (int)act_asum(tb));
+    });
+    if (multi) {   // every block of the expert sees the same pairs
+      if (rec) a.flag[e] = 1;
+      return;
+    }
+    auto epi = [&](const v4i (&acc)[2][1][NT], int i0, int nlive) {
+      if (j >= nlive || !live_rows) return;
+      const int i = i0 + j;
+      const int q = sp.pair[i];
+      const uint32_t xs = sp.asum[i];
+      uint8_t* tabq = a.htab + (size_t)q * a.htab_bytes;
+      int nl = 1;
+      uint32_t hs = 0;
+      uint32_t bytes[4][4];   // [limb][r]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t dg = (uint32_t)acc[0][0][0][r], du = (uint32_t)acc[1][0][0][r];
+        if (Q4) { dg -= 8u * xs; du -= 8u * xs; }
+        const float gv = qdot_epilogue(dg, div, sg[r]);
+        const float uv = qdot_epilogue(du, div, su[r]);
+        const int32_t hv = f2i_trunc_x86(silu_mul_t(gv, uv, exp_tab) * div);
+        const int nn = limbs_needed(hv);
+        nl = nn > nl ? nn : nl;
+        hs += (uint32_t)hv;
+        uint32_t b[4];
+        split_limbs(hv, b);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) bytes[l][r] = b[l];
+      }
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        uint8_t* plane = reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.dff, l)));
+        if constexpr (!Q4) {
+          *reinterpret_cast<uint32_t*>(plane + rowq) =
+              pack4(bytes[l][0], bytes[l][1], bytes[l][2], bytes[l][3]);
+        } else {
+          *reinterpret_cast<uint16_t*>(plane + rowq / 2) = (uint16_t)(bytes[l][0] | (bytes[l][2] << 8));
+          *reinterpret_cast<uint16_t*>(plane + a.dff / 2 + rowq / 2) =
+              (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
+        }
+      }
+      atomicMax(&sp.red_nl[i], nl);
+      atomicAdd(&sp.red_sum[i], hs);
+    };
+    ws_passes<Q4, 2, 1, KS, NT, true>(w, n, sp, lds, tab_of, epi);
+    // this block's two 64-row segments of each pair's h header (the first
+    // holds the block's sums, the second the neutral header)
+    for (int i = threadIdx.x; i < n; i += kWsThreads) {
+      uint32_t* pp = a.hpart + ((size_t)sp.pair[i] * a.nseg + 2 * blockIdx.x) * 2;
+      pp[0] = (uint32_t)sp.red_nl[i];
+      pp[1] = sp.red_sum[i];
+      if (2 * (int)blockIdx.x + 1 < a.nseg) {
+        pp[2] = 1u;
+        pp[3] = 0u;
+      }
+    }
+    __syncthreads();
+  }
+  if (rec) a.flag[e] = 0;
+}
+
+constexpr int kWsDownRT = 2;                      // row tiles per wave (down)
+constexpr int kWsDownRows = kWsWaves * kWsDownRT * 16;
+
+// down for the rows kWsDownRows * blockIdx.x .. of expert blockIdx.y: y per pair.
+template <bool Q4, int KS>
+__global__ __launch_bounds__(kWsThreads) void down_ws_kernel(DownGArgs a) {
+  constexpr int RT = kWsDownRT;
+  extern __shared__ u32x4 lds_b[];
+  __shared__ WsPairs sp;
+  uint8_t* lds = reinterpret_cast<uint8_t*>(lds_b);
+  const int e = blockIdx.y;
+  const int n_all = a.ecount[e];
+  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;
+  if (n_all == 0) {
+    if (rec) a.flag[e] = 0;
+    return;
+  }
+  const int first = a.eoff[e];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, g = lane / 16, j = lane % 16;
+  WFrag w[1][RT][KS];
+  const uint8_t* mats[1] = {a.dq + (size_t)e * a.D * a.rb};
+  const int row0 = blockIdx.x * kWsDownRows + wave * RT * 16;
+  ws_load_weights<1, RT, KS>(w, mats, a.rb, row0, a.D);
+  float sd[RT][4];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sd[rt][r] = a.ds[(size_t)e * a.D + min(row0 + rt * 16 + 4 * g + r, a.D - 1)];
+  const float div = Q4 ? 7.0f : 127.0f;
+  auto tab_of = [&](int q) { return a.htab + (size_t)q * a.htab_bytes; };
+  for (int c0 = 0; c0 < n_all; c0 += kWsChunk) {
+    const int n = min(kWsChunk, n_all - c0);
+    const bool multi = ws_prefetch(sp, a.perm, first, c0, n, [&](int q) {
+      int nl = 1;
+      uint32_t hs = 0;
+      for (int s = 0; s < a.nseg; ++s) {
+        const uint32_t* pp = a.hpart + ((size_t)q * a.nseg + s) * 2;
+        nl = (int)pp[0] > nl ? (int)pp[0] : nl;
+        hs += pp[1];
+      }
+      return make_int2(nl, (int)hs);
+    });
+    if (multi) {
+      if (rec) a.flag[e] = 1;
+      return;
+    }
+    auto epi = [&](const v4i (&acc)[1][RT][kWsDownNT], int i0, int nlive) {
+#pragma unroll
+     for (int tt = 0; tt < kWsDownNT; ++tt) {
+      if (tt * 16 + j >= nlive) break;
+      const int q = sp.pair[i0 + tt * 16 + j];
+      const uint32_t hs = sp.asum[i0 + tt * 16 + j];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int row = row0 + rt * 16 + 4 * g;
+        if (row >= a.D) continue;
+        float yv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          uint32_t d = (uint32_t)acc[0][rt][tt][r];
+          if (Q4) d -= 8u * hs;
+          yv[r] = qdot_epilogue(d, div, sd[rt][r]);
+        }
+        *reinterpret_cast<float4*>(a.y + (size_t)q * a.D + row) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+      }
+     }
+    };
+    ws_passes<Q4, 1, RT, KS, kWsDownNT, false>(w, n, sp, lds, tab_of, epi);
+  }
+  if (rec) a.flag[e] = 0;
 }
 
 // ---------------------------------------------------------------- combine
@@ -786,19 +1188,54 @@ moe_status launch_router_tile(const RouterTileArgs& a, hipStream_t s) {
   return check_hip(hipGetLastError(), "router tile launch");
 }
 
-// Dynamic LDS above 64 KB needs the per-kernel attribute (set once).
-moe_status mma_lds_attributes() {
-  static bool done = false;
-  if (done) return MOE_OK;
-  const void* fns[4] = {(const void*)gate_up_grouped_kernel<true>, (const void*)down_grouped_kernel<true>,
-                        (const void*)gate_up_grouped_kernel<false>, (const void*)down_grouped_kernel<false>};
-  for (int i = 0; i < 4; ++i) {
-    moe_status st = check_hip(hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  kMmaLds), "grouped LDS attribute");
-    if (st) return st;
+// Dynamic LDS above 64 KB needs the per-kernel attribute (set once per kernel).
+std::mutex g_attr_mu;
+std::unordered_set<const void*> g_attr_set;
+
+moe_status grouped_lds_attribute(const void* fn) {
+  std::lock_guard<std::mutex> lk(g_attr_mu);
+  if (g_attr_set.count(fn)) return MOE_OK;
+  moe_status st = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMmaLds),
+                            "grouped LDS attribute");
+  if (st == MOE_OK) g_attr_set.insert(fn);
+  return st;
+}
+
+using GroupedFn = const void*;
+
+// Weight-stationary kernels exist for 1..8 steps of K (Q4: 256 columns a
+// step, Q8: 128); longer rows use the streaming kernels.
+template <bool Q4, bool GU>
+GroupedFn ws_fn(int ks) {
+  switch (ks) {
+#define WS_CASE(n) \
+  case n: return GU ? (GroupedFn)gate_up_ws_kernel<Q4, n> : (GroupedFn)down_ws_kernel<Q4, n>;
+    WS_CASE(1) WS_CASE(2) WS_CASE(3) WS_CASE(4) WS_CASE(5) WS_CASE(6) WS_CASE(7) WS_CASE(8)
+#undef WS_CASE
+    default: return nullptr;
   }
-  done = true;
-  return MOE_OK;
+}
+
+GroupedFn pick_ws(bool q4, bool gate_up, int ks) {
+  if (q4) return gate_up ? ws_fn<true, true>(ks) : ws_fn<true, false>(ks);
+  return gate_up ? ws_fn<false, true>(ks) : ws_fn<false, false>(ks);
+}
+
+template <class Args>
+moe_status launch_grouped(GroupedFn fn, dim3 grid, const Args& args, size_t lds, hipStream_t s) {
+  moe_status st = grouped_lds_attribute(fn);
+  if (st) return st;
+  hipLaunchKernelGGL(((void (*)(Args))fn), grid, dim3(kMmaThreads), lds, s, args);
+  return check_hip(hipGetLastError(), "grouped launch");
+}
+
+// Dynamic LDS of a weight-stationary kernel: two staging buffers.
+size_t ws_lds(int nt, int K) { return 2 * (size_t)16 * nt * (K + 16); }
+
+// MOEHIP_GROUPED_WS=0 selects the streaming kernels everywhere.
+bool ws_enabled() {
+  static const bool v = !(getenv("MOEHIP_GROUPED_WS") && atoi(getenv("MOEHIP_GROUPED_WS")) == 0);
+  return v;
 }
 
 }  // namespace
@@ -842,26 +1279,40 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
                      L->ecount, L->eoff, L->perm);
   if ((st = check_hip(hipGetLastError(), "group launch"))) return st;
   // 5. gate/up + SwiGLU
-  const int nseg = (L->dff + kMmaRows - 1) / kMmaRows;
+  const int nseg = 2 * ((L->dff + kMmaRows - 1) / kMmaRows);   // h header segments of 64 rows
   GateUpGArgs ga{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk,
                  L->ecount, L->eoff, L->perm, L->xtab, act_table_bytes(L->D),
                  L->htab, act_table_bytes(L->dff), L->hpart, nseg};
-  dim3 gg((unsigned)nseg, (unsigned)L->E);
-  if ((st = mma_lds_attributes())) return st;
-  if (q4)
-    hipLaunchKernelGGL(gate_up_grouped_kernel<true>, gg, dim3(kMmaThreads), kMmaLds, s, ga);
-  else
-    hipLaunchKernelGGL(gate_up_grouped_kernel<false>, gg, dim3(kMmaThreads), kMmaLds, s, ga);
-  if ((st = check_hip(hipGetLastError(), "grouped gate/up launch"))) return st;
+  dim3 gg((unsigned)((L->dff + kMmaRows - 1) / kMmaRows), (unsigned)L->E);
+  // weight-stationary kernels where the rows fit registers; experts with
+  // multi-limb activations (flagged by them) go to the streaming kernels
+  const int cols = q4 ? 256 : 128;
+  const bool ws = ws_enabled();
+  const GroupedFn gu_stream =
+      q4 ? (GroupedFn)gate_up_grouped_kernel<true> : (GroupedFn)gate_up_grouped_kernel<false>;
+  const GroupedFn gu_ws = ws ? pick_ws(q4, true, L->D / cols) : nullptr;
+  if (gu_ws) {
+    ga.flag = L->wsflag;
+    if ((st = launch_grouped(gu_ws, gg, ga, ws_lds(1, L->D), s))) return st;
+    ga.flag = nullptr;
+    ga.only_flagged = L->wsflag;
+  }
+  if ((st = launch_grouped(gu_stream, gg, ga, kMmaLds, s))) return st;
   // 6. down
   DownGArgs da{L->dq, L->ds, L->rbd, L->D, L->dff, L->ecount, L->eoff, L->perm,
                L->htab, act_table_bytes(L->dff), L->hpart, nseg, L->y};
+  const GroupedFn dn_stream =
+      q4 ? (GroupedFn)down_grouped_kernel<true> : (GroupedFn)down_grouped_kernel<false>;
+  const GroupedFn dn_ws = ws ? pick_ws(q4, false, L->dff / cols) : nullptr;
+  if (dn_ws) {
+    da.flag = L->wsflag + L->E;
+    dim3 dgw((unsigned)((L->D + kWsDownRows - 1) / kWsDownRows), (unsigned)L->E);
+    if ((st = launch_grouped(dn_ws, dgw, da, ws_lds(kWsDownNT, L->dff), s))) return st;
+    da.flag = nullptr;
+    da.only_flagged = L->wsflag + L->E;
+  }
   dim3 dg((unsigned)((L->D + kMmaRows - 1) / kMmaRows), (unsigned)L->E);
-  if (q4)
-    hipLaunchKernelGGL(down_grouped_kernel<true>, dg, dim3(kMmaThreads), kMmaLds, s, da);
-  else
-    hipLaunchKernelGGL(down_grouped_kernel<false>, dg, dim3(kMmaThreads), kMmaLds, s, da);
-  if ((st = check_hip(hipGetLastError(), "grouped down launch"))) return st;
+  if ((st = launch_grouped(dn_stream, dg, da, kMmaLds, s))) return st;
   // 7. ordered combine + residual
   dim3 cg((unsigned)((L->D / 4 + 255) / 256), (unsigned)T);
   hipLaunchKernelGGL(combine_kernel, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D,

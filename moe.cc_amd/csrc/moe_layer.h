@@ -37,6 +37,7 @@ struct LayerDev {
   int* ecount = nullptr;     // [E]
   int* eoff = nullptr;       // [E]
   int* perm = nullptr;       // [T*topk]
+  int* wsflag = nullptr;     // [2][E] experts left to the streaming gate/up, down kernels
   float* y = nullptr;        // [T*topk][D]
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };
