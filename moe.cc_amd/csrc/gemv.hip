@@ -67,13 +67,16 @@ struct GemvEpiMaker {
     float* C;
     int M, ldc, m0;
     float div;
+    using Pre = float;
+    __device__ Pre pre(int row) const { return S[row]; }
     template <class Tot>
-    __device__ void operator()(int row, const Tot& tot) const {
-      const float sc = S[row];
+    __device__ void operator()(int row, const Tot& tot, float sc) const {
 #pragma unroll
       for (int t = 0; t < MTI; ++t)
         if (m0 + t < M) C[(size_t)(m0 + t) * ldc + row] = qdot_epilogue(tot[0][t], div, sc);
     }
+    template <class Tot>
+    __device__ void operator()(int row, const Tot& tot) const { (*this)(row, tot, S[row]); }
   };
   template <int MTI>
   __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{S, C, M, ldc, mbase + t0, div}; }

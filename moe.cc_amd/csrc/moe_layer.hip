@@ -56,12 +56,16 @@ struct GateUpEpi {
   float* hb;
   int r0;
   float div;
+  using Pre = float2;
+  __device__ Pre pre(int row) const { return make_float2(gs[row], us[row]); }
   template <class Tot>
-  __device__ void operator()(int row, const Tot& tot) const {
-    const float g = qdot_epilogue(tot[0][0], div, gs[row]);
-    const float u = qdot_epilogue(tot[1][0], div, us[row]);
+  __device__ void operator()(int row, const Tot& tot, float2 sc) const {
+    const float g = qdot_epilogue(tot[0][0], div, sc.x);
+    const float u = qdot_epilogue(tot[1][0], div, sc.y);
     hb[row - r0] = silu_mul(g, u);
   }
+  template <class Tot>
+  __device__ void operator()(int row, const Tot& tot) const { (*this)(row, tot, pre(row)); }
 };
 struct GateUpEpiMaker {
   GateUpEpi e;
@@ -135,10 +139,14 @@ struct DownEpi {
   float* yb;
   int r0;
   float div;
+  using Pre = float;
+  __device__ Pre pre(int row) const { return ds[row]; }
   template <class Tot>
-  __device__ void operator()(int row, const Tot& tot) const {
-    yb[row - r0] = qdot_epilogue(tot[0][0], div, ds[row]);
+  __device__ void operator()(int row, const Tot& tot, float sc) const {
+    yb[row - r0] = qdot_epilogue(tot[0][0], div, sc);
   }
+  template <class Tot>
+  __device__ void operator()(int row, const Tot& tot) const { (*this)(row, tot, ds[row]); }
 };
 struct DownEpiMaker {
   DownEpi e;

@@ -240,6 +240,9 @@ constexpr int pf_for() { return (Q4 && NL > 1) ? 1 : 2; }
 
 // The rows are shared by a team of nwv waves; this wave is number wv.
 // asum_in (optional, per token slot) replaces the tables' header sums.
+// The epilogue's per-row data (its scales) is fetched with the row's
+// weights: epi.pre(row) at load time, epi(row, tot, pre) at the end, so the
+// scale load's latency hides behind the weight stream.
 template <bool Q4, class G, int NL, int MTI, int NM, class Epi>
 __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long rs, int K,
                                             const uint8_t* const* tab, int r0, int r1,
@@ -250,8 +253,10 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
   const int lane = threadIdx.x % kWave, wave = wv;
   const int g = lane / G::LPR, r = lane % G::LPR;
   const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
-  auto load = [&](int gi, uint32_t (&w)[NM][G::DW]) {
+  using Pre = typename Epi::Pre;
+  auto load = [&](int gi, uint32_t (&w)[NM][G::DW], Pre& pd) {
     const int row = r0 + gi * G::WR + g;
+    pd = epi.pre(row < r1 ? row : r0);
 #pragma unroll
     for (int mat = 0; mat < NM; ++mat) {
       if (row < r1) {
@@ -262,7 +267,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
       }
     }
   };
-  auto finish = [&](int gi, const uint32_t (&w)[NM][G::DW]) {
+  auto finish = [&](int gi, const uint32_t (&w)[NM][G::DW], const Pre& pd) {
     const int row = r0 + gi * G::WR + g;
     uint32_t tot[NM][MTI];
 #pragma unroll
@@ -272,16 +277,17 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
         const uint32_t v = group_sum_dpp<G::LPR>(lane_dot<Q4, G, NL>(w[mat], ar[t]));
         tot[mat][t] = Q4 ? v - 8u * asum[t] : v;
       }
-    if (r == 0 && row < r1) epi(row, tot);
+    if (r == 0 && row < r1) epi(row, tot, pd);
   };
 
   // PF row groups of loads in flight: group gi is reduced while the loads of
   // the next PF-1 groups of this wave are outstanding
   constexpr int PF = pf_for<Q4, NL>();
   uint32_t wr[PF][NM][G::DW];
+  Pre pre[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i)
-    if (wave + i * nwv < ngroups) load(wave + i * nwv, wr[i]);  // weights first
+    if (wave + i * nwv < ngroups) load(wave + i * nwv, wr[i], pre[i]);  // weights first
 #pragma unroll
   for (int t = 0; t < MTI; ++t) {
     load_act_regs<Q4, G, NL>(tab[t], K, ar[t]);
@@ -293,9 +299,9 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
     for (int i = 0; i < PF; ++i) {
       const int gi = wave + (base + i) * nwv;
       if (gi >= ngroups) { done = true; break; }
-      finish(gi, wr[i]);
+      finish(gi, wr[i], pre[i]);
       const int gn = gi + PF * nwv;
-      if (gn < ngroups) load(gn, wr[i]);
+      if (gn < ngroups) load(gn, wr[i], pre[i]);
     }
     if (done) break;
   }
@@ -303,11 +309,13 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
 
 // Token slots per weight pass so that activation registers stay within a
 // budget (96 dwords for one matrix, 64 for two); 0 = does not fit.
-// Activations needing 4 limbs (|x| > 257 for Q8, > 4662 for Q4) take the
-// exact fp32 fallback, which keeps the tiled kernels' register budget small.
+// Activations needing 4 limbs (|x| > 257 for Q8), or more than one for Q4
+// (|x| > 18.3, rare after RMSNorm), take the exact fp32 fallback, which keeps
+// the tiled kernels' registers (and so their occupancy) at the one-limb
+// budget for Q4 and the two-limb one for Q8 (|x| > 1.008 is common there).
 template <bool Q4, class G, int NL, int NM>
 constexpr int mti_for() {
-  if (NL > 2) return 0;
+  if (NL > 2 || (Q4 && NL > 1)) return 0;
   constexpr int per = NL * G::DW * (Q4 ? 2 : 1);
   constexpr int n = (NM == 1 ? 64 : 48) / per;
   return n >= 4 ? 4 : (n >= 2 ? 2 : (n >= 1 ? 1 : 0));

@@ -138,12 +138,17 @@ def test_variant_selection(moehip):
 
 
 @pytest.mark.parametrize("dtype,N,K,M,scale", [(2, 768, 2048, 1, 1.0), (3, 2048, 768, 3, 1.0),
-                                               (3, 768, 2048, 5, 40.0), (2, 512, 1024, 2, 400.0)])
+                                               (3, 768, 2048, 5, 40.0), (2, 512, 1024, 2, 400.0),
+                                               # one token: the flat stream over all jobs' rows
+                                               (3, 2048, 768, 1, 1.0), (3, 768, 2048, 1, 1.0),
+                                               (3, 100, 768, 1, 40.0), (2, 77, 2048, 1, 400.0),
+                                               (3, 13, 4096, 1, 3000.0)])
 def test_prepacked_matches_oracle(moehip, dtype, N, K, M, scale):
     """Pack once, run several products from the same tables.  scale 40 / 400
-    pushes Q4 / Q8 activations into the 2- and 4-byte limb ranges."""
+    pushes Q4 / Q8 activations into the 2- and 4-byte limb ranges (3000:
+    4-limb Q4, the exact fallback)."""
     L = moehip.lib()
-    nj = 3
+    nj = 3 if M > 1 else 7
     A = O.normal(M * K, 900 + M, 0.0, scale).reshape(M, K)
     dA = moehip.DeviceBuffer.from_array(A)
     tb = L.moe_act_table_bytes(K)
