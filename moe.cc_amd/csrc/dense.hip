@@ -90,9 +90,10 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 // LDS: NP + 1 buffers of M*RW rows of KC + 4 floats, then (NORM) the rows.
 //
 // NORM: the token rows are staged whole in LDS and rmsnorm'ed first
-// (test_model_trace.c:241-255): squares x*x by all threads, one pure add
-// chain per token in the consumer lanes, msq / K, 1 / sqrtf(msq + eps), then
-// x = (x * inv) * w; the producers' first weight chunks load meanwhile.
+// (test_model_trace.c:241-255): squares x*x by all threads, their
+// sequential sum by the whole block (block_seq_sum), msq / K,
+// 1 / sqrtf(msq + eps), then x = (x * inv) * w; the producers' first weight
+// chunks load meanwhile.
 // Each block also writes a column slice of the normalized rows and
 // (PACK = 2 / 3) packs the slice into the activation tables; the last block
 // (fused selection) writes the tables' headers.
@@ -110,6 +111,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   float* pl = reinterpret_cast<float*>(pl4);
   __shared__ float inv_s[MM];
   __shared__ int pack_scratch[2];
+  __shared__ SeqSumScratch seq;
   const int M = a.M, N = a.N, K = a.K;
   const int nc = (K + KC - 1) / KC;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -164,10 +166,9 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       reinterpret_cast<float4*>(pl)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
     }
     __syncthreads();
-    if (wave == 0 && lane < M) {
-      const float msq = chain_sum(0.0f, pl + (size_t)lane * K, k4);
-      const float mean = msq / (float)K;
-      inv_s[lane] = 1.0f / sqrtf(mean + a.eps);
+    for (int m = 0; m < M; ++m) {
+      const float msq = block_seq_sum<NT>(pl + (size_t)m * K, K, seq);
+      if (threadIdx.x == 0) inv_s[m] = 1.0f / sqrtf(msq / (float)K + a.eps);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < M * K; i += NT) {
@@ -495,19 +496,24 @@ __global__ __launch_bounds__(64) void heads_kernel(HeadArgs a) {
 // ---------------------------------------------------------------- attention
 
 // Scores of query row t, head h against cache positions tk0 .. tk0 + 63
-// (<= pos0 + t): the 64 K rows are staged in LDS, lane i runs the chain
-// dot = (((0 + q0 k0) + q1 k1) + ...) over hd and stores dot * scale.
-// fuse_heads (T == 1, position P = pos0): q is normed and rotated here; the
-// block holding position P computes K's row P the same way (the cache does
-// not have it yet) and, for the first query head of each KV group, writes
-// K and V row P into the caches.  All global loads are issued first.
+// (<= pos0 + t): lane i runs the chain dot = (((0 + q0 k0) + q1 k1) + ...)
+// over hd for position tk0 + i and stores dot * scale.  REG (hd <= 128):
+// each lane loads its K row straight into registers (one round trip);
+// otherwise the 64 K rows are staged in LDS.  fuse_heads (T == 1, position
+// P = pos0): q is normed and rotated here; the block holding position P
+// computes K's row P the same way (the cache does not have it yet) and, for
+// the first query head of each KV group, writes K and V row P into the
+// caches.  All global loads are issued first.
+constexpr int kRegHd = 128;
+
+template <bool REG>
 __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   extern __shared__ float lds[];
   const int hd = a.hd, LD = hd + 4, d2 = hd / 2;
   const int hdp = (hd + 3) & ~3;
   float* q = lds;                       // [hd] the query (rotated)
-  float* kt = q + hdp;                  // [64][LD] K rows
-  float* qraw = kt + 64 * LD;           // [hd]
+  float* kt = q + hdp;                  // REG: [hd] K row P; else [64][LD] K rows
+  float* qraw = kt + (REG ? hdp : 64 * LD);   // [hd]
   float* kraw = qraw + hdp;             // [hd]
   float* wq = kraw + hdp;               // [hd]
   float* wk = wq + hdp;                 // [hd]
@@ -548,24 +554,33 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
       for (int d = lane; d < hd; d += 64) vd[d] = vraw[d];
     }
   }
-  // 16 loads in flight per lane, then their stores
-  for (int base = 0; base < total; base += 64 * 16) {
-    float4 r[16];
+  float4 kr[REG ? kRegHd / 4 : 1];
+  if constexpr (REG) {
+    // this lane's K row (position tk0 + lane) into registers
+    // (columns past hd: the row's last float4 again; their products are not summed)
+    const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)(lane < cached ? lane : 0) * hd);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int i = base + lane + 64 * u;
-      r[u] = i < total ? *reinterpret_cast<const float4*>(kbase + (size_t)(i / h4) * hd + 4 * (i % h4))
-                       : zero4();
-    }
+    for (int i = 0; i < kRegHd / 4; ++i) kr[i] = src[i < h4 ? i : h4 - 1];
+  } else {
+    // 16 loads in flight per lane, then their stores
+    for (int base = 0; base < total; base += 64 * 16) {
+      float4 r[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int i = base + lane + 64 * u;
-      if (i < total) *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + lane + 64 * u;
+        r[u] = i < total ? *reinterpret_cast<const float4*>(kbase + (size_t)(i / h4) * hd + 4 * (i % h4))
+                         : zero4();
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + lane + 64 * u;
+        if (i < total) *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
+      }
     }
   }
   if (a.fuse_heads) {
     __syncthreads();
-    float* knew = kt + (P - tk0) * LD;
+    float* knew = REG ? kt : kt + (P - tk0) * LD;
     heads_prep(qraw, own_new ? kraw : nullptr, a.q_norm ? wq : nullptr, a.k_norm ? wk : nullptr,
                a.eps, hd, cs, sn, sq, inv_s, q, knew);
     if (own_new && h % group == 0) {
@@ -578,7 +593,27 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   }
   __syncthreads();
   if (lane < rows) {
-    const float dot = chain_dot(0.0f, q, kt + lane * LD, h4);
+    float dot;
+    if constexpr (REG) {
+      const bool fresh = own_new && lane == P - tk0;   // row P: computed above, in LDS
+      const float4* kn4 = reinterpret_cast<const float4*>(kt);
+      const float4* q4 = reinterpret_cast<const float4*>(q);
+      dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRegHd / 4; ++i) {
+        if (i < h4) {
+          const float4 kv = fresh ? kn4[i] : kr[i];
+          const float4 qv = q4[i];
+          const float p0 = qv.x * kv.x, p1 = qv.y * kv.y, p2 = qv.z * kv.z, p3 = qv.w * kv.w;
+          dot = dot + p0;
+          dot = dot + p1;
+          dot = dot + p2;
+          dot = dot + p3;
+        }
+      }
+    } else {
+      dot = chain_dot(0.0f, q, kt + lane * LD, h4);
+    }
     a.S[((size_t)t * a.nq + h) * a.max_seq + tk0 + lane] = dot * a.scale;
   }
 }
@@ -948,11 +983,16 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   if (a.fuse_heads && a.T != 1) return set_error(MOE_ERR_ARG, "attention: fused heads need T == 1");
   const int nmax = a.pos0 + a.T;   // positions of the last row
   const size_t hdp = (size_t)((a.hd + 3) & ~3);
-  const size_t lds_s = (9 * hdp + 64 * (size_t)(a.hd + 4)) * 4;
-  moe_status st = set_lds(attn_scores_kernel, lds_s, "scores LDS attribute");
-  if (st) return st;
-  hipLaunchKernelGGL(attn_scores_kernel, dim3((unsigned)((nmax + 63) / 64), (unsigned)a.nq, (unsigned)a.T),
-                     dim3(64), lds_s, s, a);
+  const dim3 sgrid((unsigned)((nmax + 63) / 64), (unsigned)a.nq, (unsigned)a.T);
+  moe_status st;
+  if (a.hd <= kRegHd) {
+    const size_t lds_s = 10 * hdp * 4;
+    hipLaunchKernelGGL(attn_scores_kernel<true>, sgrid, dim3(64), lds_s, s, a);
+  } else {
+    const size_t lds_s = (9 * hdp + 64 * (size_t)(a.hd + 4)) * 4;
+    if ((st = set_lds(attn_scores_kernel<false>, lds_s, "scores LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_scores_kernel<false>, sgrid, dim3(64), lds_s, s, a);
+  }
   if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
   const size_t es_f = (size_t)((a.max_seq + 3) & ~3);
   if (a.T <= 4) {

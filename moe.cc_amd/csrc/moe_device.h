@@ -176,6 +176,132 @@ __device__ __forceinline__ float chain_sum(float acc, const float* p, int n4) {
   return acc;
 }
 
+// ---------------------------------------------------------------------------
+// The sequential fp32 sum s = (((0 + p0) + p1) + ... + p_{n-1}), each add
+// rounded, computed by a whole block in about n/8 dependent adds.
+//
+// The n values are split into kSeqSegs segments.  Segment j starts from the
+// unknown partial sum s_j; its estimate e_j (the exact sum of p_0 .. p_{k-1}
+// in double, rounded to fp32) is within a few ulps of s_j (the rounding
+// errors of k adds grow like sqrt(k) ulps), so the segment's chain is run
+// from the kSeqCands consecutive fp32 values centred on e_j: NT / kSeqSegs
+// threads per segment, kSeqCands / that many independent chains each (which
+// fill the add latency instead of lengthening it).  Then one wave walks the
+// segments in order: s_0 = +0, and s_{j+1} is the chain output of the
+// candidate whose bits equal s_j's.  A chain that starts from the same bits
+// adds the same values in the same order, so that output is s_{j+1}
+// exactly.  When no candidate matches (a far estimate, or NaN / inf among
+// the values) the wave runs the segment's chain itself.  The result is
+// bit-identical to the sequential loop in every case; only the latency
+// depends on the values.
+// ---------------------------------------------------------------------------
+constexpr int kSeqSegs = 8;
+constexpr int kSeqCands = 64;
+
+struct SeqSumScratch {
+  double part[kSeqSegs];
+  float cand[kSeqSegs][kSeqCands];
+  float out[kSeqSegs][kSeqCands];
+  float result;
+};
+
+// Order-preserving integer image of a float's bits (-0 just below +0).
+__device__ __forceinline__ int32_t seq_key(float f) {
+  const int32_t b = __float_as_int(f);
+  return b >= 0 ? b : b ^ 0x7FFFFFFF;
+}
+__device__ __forceinline__ float seq_unkey(int32_t k) {
+  return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF);
+}
+
+// Every thread of the block (NT threads: 32 to 512, a power of two) must
+// call this; p (LDS) holds the n values; returns s to every thread.
+template <int NT>
+__device__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
+  constexpr int S = kSeqSegs, C = NT / S, CPT = kSeqCands / C;
+  static_assert(C >= 4 && C <= 64 && (C & (C - 1)) == 0 && CPT >= 1 && C * CPT == kSeqCands,
+                "threads per segment");
+  const int tid = threadIdx.x, j = tid / C, i = tid % C;
+  const int L = ((n + S - 1) / S + 3) & ~3;   // segments start on float4 boundaries
+  const int k0 = min(n, j * L), k1 = min(n, k0 + L);
+  // 1. segment sums in double (the C threads of a segment are adjacent lanes)
+  double d = 0.0;
+  for (int k = k0 + i; k < k1; k += C) d += (double)p[k];
+#pragma unroll
+  for (int off = C / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+  if (i == 0) sc.part[j] = d;
+  __syncthreads();
+  // 2.-3. the start estimate of segment j and this thread's candidates
+  float c[CPT];
+  if (j > 0) {
+    double est = 0.0;
+    for (int q = 0; q < j; ++q) est += sc.part[q];
+    const int32_t base = seq_key((float)est) - kSeqCands / 2 + i * CPT;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) c[u] = seq_unkey(base + u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) c[u] = 0.0f;   // segment 0 starts at +0
+  }
+  // 4. the segment's chains from the candidates (independent, interleaved)
+  float acc[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) acc[u] = c[u];
+  {
+    // 16 float4 read ahead of their 64 x CPT adds (p is 16-byte aligned)
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    int k = k0;
+    for (; k + 64 <= k1; k += 64) {
+      float4 v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = p4[k / 4 + r];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+          acc[u] = acc[u] + v[r].x;
+          acc[u] = acc[u] + v[r].y;
+          acc[u] = acc[u] + v[r].z;
+          acc[u] = acc[u] + v[r].w;
+        }
+    }
+    for (; k < k1; ++k) {
+      const float v = p[k];
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) acc[u] = acc[u] + v;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    sc.cand[j][i * CPT + u] = c[u];
+    sc.out[j][i * CPT + u] = acc[u];
+  }
+  __syncthreads();
+  // 5. stitch the segments in order (wave 0, lane l <-> candidate l)
+  if (tid < 64) {
+    const int lane = tid;
+    float t = 0.0f;
+    for (int q = 0; q < S; ++q) {
+      const bool hit = __float_as_uint(sc.cand[q][lane]) == __float_as_uint(t);
+      const unsigned long long m = __ballot(hit);
+      if (m) {
+        t = sc.out[q][__ffsll((long long)m) - 1];
+      } else {
+        const int q0 = min(n, q * L), q1 = min(n, q0 + L);
+        int k = q0;
+        if (q1 - q0 >= 4) {
+          t = chain_sum(t, p + q0, (q1 - q0) / 4);
+          k = q0 + (q1 - q0) / 4 * 4;
+        }
+        for (; k < q1; ++k) t = t + p[k];
+      }
+    }
+    if (lane == 0) sc.result = t;
+  }
+  __syncthreads();
+  return sc.result;
+}
+
 // test_model_trace.c:233 then :500: h = (g / (1 + expf(-g))) * u
 __device__ __forceinline__ float silu_mul_t(float g, float u, const uint64_t* tab) {
   const float den = 1.0f + expf_glibc_t(-g, tab);

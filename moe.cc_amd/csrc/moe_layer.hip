@@ -209,14 +209,15 @@ __global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs 
 }
 
 // rmsnorm (test_model_trace.c:241-255): one block per token; the squares
-// x_i * x_i are formed by all threads into LDS and thread 0 sums them in
-// order with pure dependent adds (msq / D, 1 / sqrtf(msq + eps)).
+// x_i * x_i are formed by all threads into LDS and summed in order by
+// block_seq_sum (msq / D, 1 / sqrtf(msq + eps)).
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       float* __restrict__ y, int D, float eps,
                                                       int fast) {
   extern __shared__ float4 sq4[];
   __shared__ float inv_s;
+  __shared__ SeqSumScratch seq;
   const int t = blockIdx.x;
   const float* xt = x + (size_t)t * D;
   if (fast) {
@@ -225,8 +226,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       sq4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
     }
     __syncthreads();
+    const float acc = block_seq_sum<256>(reinterpret_cast<const float*>(sq4), D, seq);
     if (threadIdx.x == 0) {
-      const float acc = chain_sum(0.0f, reinterpret_cast<const float*>(sq4), D / 4);
       const float msq = acc / (float)D;
       inv_s = 1.0f / sqrtf(msq + eps);
     }

@@ -143,6 +143,43 @@ def test_rmsnorm_dev(moehip):
         np.testing.assert_array_equal(bits(dy.download((T, D), np.float32)), bits(O.rmsnorm(x, w)))
 
 
+def _seq_sum_rows():
+    """Rows whose sequential sum of squares defeats the segment estimates of
+    block_seq_sum in different ways (every path of its stitching runs)."""
+    rng = np.random.default_rng(77)
+    D = 2048
+    rows = [rng.normal(0, 1, D),                                  # the common case
+            rng.normal(0, 1, D) * 10.0 ** rng.integers(-18, 18, D),   # huge dynamic range
+            np.where(np.arange(D) % 97 == 0, 3e18, 1e-3),          # a few huge squares: far estimates
+            rng.normal(0, 1, D), rng.normal(0, 1, D), rng.normal(0, 1e19, D)]   # overflow to inf
+    rows[3][1000] = np.nan
+    rows[4][5] = np.inf
+    return np.array(rows, np.float32)
+
+
+def test_rmsnorm_parallel_sum_paths(moehip):
+    """The block-parallel sequential sum of squares (candidate segments with a
+    sequential fallback) against the oracle's loop, bit for bit, through both
+    users: the RMSNorm kernel and the norm fused into the router product."""
+    x = _seq_sum_rows()
+    T, D = x.shape
+    for w in (None, O.normal(D, 78, 1.0, 0.1)):
+        dx, dy = moehip.DeviceBuffer.from_array(x), moehip.DeviceBuffer(x.nbytes)
+        dw = moehip.DeviceBuffer.from_array(w) if w is not None else None
+        moehip.check(moehip.lib().moe_rmsnorm_dev(dx.ptr, dw.ptr if dw else None, dy.ptr, T, D, 1e-6))
+        np.testing.assert_array_equal(bits(dy.download((T, D), np.float32)), bits(O.rmsnorm(x, w)))
+    # fused into the router (one token and four tokens at a time)
+    dtype, E, dff = 3, 16, 256
+    ex = random_experts(dtype, E, D, dff, 79)
+    rw = O.normal(E * D, 80, 0.0, 0.02).reshape(E, D)
+    rms2 = O.normal(D, 81, 1.0, 0.1)
+    layer = make_layer(moehip, dtype, ex, rw, None, rms2)
+    finite = x[np.isfinite(x).all(axis=1)][:3]
+    for rows in (finite[:1], finite[:3]):
+        want = O.moe_block(O.rmsnorm(rows, rms2), rows, rw, None, ex)[0]
+        np.testing.assert_array_equal(bits(layer.block_forward(rows)), bits(want))
+
+
 def test_repeated_forward_and_growing_T(moehip):
     """Scratch reuse: T grows and shrinks between calls; results stay exact."""
     dtype, E, D, dff = 3, 64, 1024, 512
