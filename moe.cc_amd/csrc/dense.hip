@@ -297,6 +297,132 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   }
 }
 
+// One token, few rows (the router): one block per output row.  The token
+// row is staged in LDS (normalized first when NORM, the sum of squares by
+// block_seq_sum), the products x[k] * W[n][k] are formed into LDS and summed
+// in order by block_seq_sum, so a row costs about K / 8 dependent adds
+// instead of K.  With PACK each block packs its column slice of the
+// normalized row into the activation tables (row_finish_kernel writes the
+// header and, with a fused selection, picks the experts).
+constexpr int kRowThreads = 256;
+constexpr int kRowMaxK = 8192;
+
+template <bool NORM, int PACK>
+__global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
+  extern __shared__ float4 rl4[];
+  const int K = a.K, k4 = K / 4, n = blockIdx.x;
+  float* xs = reinterpret_cast<float*>(rl4);   // [K] the token row
+  float* pv = xs + K;                          // [K] squares, then products, then keys
+  float* nw = pv + K;                          // [K] NORM: the norm weights
+  float4* xs4 = rl4;
+  float4* pv4 = rl4 + k4;
+  __shared__ SeqSumScratch seq;
+  __shared__ int pack_scratch[2];
+  __shared__ float inv_s;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  constexpr int WV = kRowMaxK / 4 / kRowThreads;
+  // the weight row into registers first, then the token row into LDS
+  const float4* wr = reinterpret_cast<const float4*>(a.W + (size_t)n * a.ldw);
+  float4 w[WV];
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = tid + kRowThreads * u;
+    w[u] = i < k4 ? wr[i] : zero4();
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(a.A);
+  const float4* nw4g = reinterpret_cast<const float4*>(a.norm_w);
+  for (int i = tid; i < k4; i += kRowThreads) {
+    const float4 v = x4[i];
+    xs4[i] = v;
+    if (NORM) {
+      pv4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+      reinterpret_cast<float4*>(nw)[i] = a.norm_w ? nw4g[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+  }
+  __syncthreads();
+  if constexpr (NORM) {
+    const float msq = block_seq_sum<kRowThreads>(pv, K, seq);
+    if (tid == 0) inv_s = 1.0f / sqrtf(msq / (float)K + a.eps);
+    __syncthreads();
+    for (int i = tid; i < K; i += kRowThreads) {
+      const float v = xs[i] * inv_s;
+      xs[i] = v * nw[i];   // a missing weight is 1 (the reference multiplies by 1.0f)
+    }
+    __syncthreads();
+    // this block's column slice [c0, c1) (a multiple of 8 columns)
+    const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
+    const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
+    if (a.xn_out)
+      for (int i = c0 + tid; i < c1; i += kRowThreads) a.xn_out[i] = xs[i];
+    if constexpr (PACK != 0) {
+      if (tid == 0) { pack_scratch[0] = 1; pack_scratch[1] = 0; }
+      __syncthreads();
+      int nl;
+      uint32_t sum;
+      pack_act_cols<PACK == 3>(xs, K, c0, c1, a.pack_tabs, tid, kRowThreads, nl, sum);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const int on = __shfl_xor(nl, off, kWave);
+        nl = on > nl ? on : nl;
+        sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+      }
+      if (lane == 0) {
+        atomicMax(&pack_scratch[0], nl);
+        atomicAdd(reinterpret_cast<unsigned*>(&pack_scratch[1]), sum);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t* pp = a.pack_part + (size_t)blockIdx.x * 2;
+        pp[0] = (uint32_t)pack_scratch[0];
+        pp[1] = (uint32_t)pack_scratch[1];
+      }
+    }
+  }
+  // products x[k] * W[n][k], then their sum in column order
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = tid + kRowThreads * u;
+    if (i < k4) {
+      const float4 x = xs4[i];
+      pv4[i] = make_float4(x.x * w[u].x, x.y * w[u].y, x.z * w[u].z, x.w * w[u].w);
+    }
+  }
+  __syncthreads();
+  const float acc = block_seq_sum<kRowThreads>(pv, K, seq);
+  if (tid == 0) a.C[n] = dense_epilogue(a, 0, n, acc);
+}
+
+// After dense_row_kernel (a kernel boundary instead of a fence in each of
+// its blocks): the activation table's header from the slices' partials and
+// the token's expert selection.  One wave.
+__global__ __launch_bounds__(kWave) void row_finish_kernel(DenseArgs a) {
+  __shared__ uint64_t keys[1024];
+  __shared__ int sidx[kMaxTopK];
+  __shared__ float sval[kMaxTopK], sexp[kMaxTopK];
+  const int lane = threadIdx.x;
+  if (a.pack_dtype) {
+    uint32_t nl = 1, sum = 0;
+    for (int b = lane; b < a.N; b += kWave) {
+      const uint32_t* pp = a.pack_part + (size_t)b * 2;
+      nl = pp[0] > nl ? pp[0] : nl;
+      sum += pp[1];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t on = (uint32_t)__shfl_xor((int)nl, off, kWave);
+      nl = on > nl ? on : nl;
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    }
+    if (lane == 0) {
+      uint32_t* hh = reinterpret_cast<uint32_t*>(a.pack_tabs);
+      hh[0] = nl;
+      hh[1] = sum;
+    }
+  }
+  select_token_any(a.C, a.N, a.sel_topk, keys, sidx, sval, sexp, a.sel_idx, a.sel_p, a.sel_idx_user,
+                   a.sel_p_user);
+}
+
 // Many tokens: a block computes a tile of 16*CT tokens x 16*CE rows; thread
 // (ti, ei) owns tokens t0 + ti + 16i and rows n0 + ei + 16j, CT*CE chains.
 // Token and weight rows stream through two LDS chunk buffers of KC columns.
@@ -909,6 +1035,23 @@ bool dense_amax_ok(const DenseArgs& a) {
 
 int dense_amax_rows(int N) { return N >= 65536 ? 64 : 16; }
 
+// One token against few rows: the row kernel.
+bool dense_row_ok(const DenseArgs& a, bool vec) {
+  return a.M == 1 && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
+}
+
+template <bool NORM, int PACK>
+moe_status launch_row(const DenseArgs& a, hipStream_t s) {
+  const size_t lds = (size_t)(NORM ? 3 : 2) * a.K * 4;
+  moe_status st = set_lds(dense_row_kernel<NORM, PACK>, lds, "row kernel LDS attribute");
+  if (st) return st;
+  hipLaunchKernelGGL((dense_row_kernel<NORM, PACK>), dim3((unsigned)a.N), dim3(kRowThreads), lds, s, a);
+  if ((st = check_hip(hipGetLastError(), "dense row launch"))) return st;
+  if (!a.sel_counter) return MOE_OK;
+  hipLaunchKernelGGL(row_finish_kernel, dim3(1), dim3(kWave), 0, s, a);
+  return check_hip(hipGetLastError(), "row finish launch");
+}
+
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return MOE_OK;
   if (a.amax_part) {
@@ -927,6 +1070,11 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
       return set_error(MOE_ERR_ARG, "dense matmul: fused rmsnorm needs M <= 4 aligned rows");
     if (a.pack_dtype && (!a.sel_counter || !a.pack_part || !a.pack_tabs))
       return set_error(MOE_ERR_ARG, "dense matmul: packing needs the fused selection");
+    if (dense_row_ok(a, vec)) {
+      if (a.pack_dtype == 2) return launch_row<true, 2>(a, s);
+      if (a.pack_dtype == 3) return launch_row<true, 3>(a, s);
+      return launch_row<true, 0>(a, s);
+    }
     if (a.M == 1) {
       if (a.pack_dtype == 2) return launch_gemv<16, true, 2, kNpOne>(a, s);
       if (a.pack_dtype == 3) return launch_gemv<16, true, 3, kNpOne>(a, s);
@@ -941,6 +1089,7 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(dense_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), "dense generic launch");
   }
+  if (dense_row_ok(a, vec)) return launch_row<false, 0>(a, s);
   if (a.sel_counter) {
     if (!vec) return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs aligned rows");
     return a.M == 1 ? launch_gemv<16, false, 0, kNpOne>(a, s) : launch_gemv<16, false, 0, 1>(a, s);

@@ -277,15 +277,23 @@ __device__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
     sc.out[j][i * CPT + u] = acc[u];
   }
   __syncthreads();
-  // 5. stitch the segments in order (wave 0, lane l <-> candidate l)
+  // 5. stitch the segments in order (wave 0, lane l <-> candidate l; all
+  // candidates and outputs read up front)
   if (tid < 64) {
     const int lane = tid;
-    float t = 0.0f;
+    uint32_t cb[S];
+    float ob[S];
+#pragma unroll
     for (int q = 0; q < S; ++q) {
-      const bool hit = __float_as_uint(sc.cand[q][lane]) == __float_as_uint(t);
-      const unsigned long long m = __ballot(hit);
+      cb[q] = __float_as_uint(sc.cand[q][lane]);
+      ob[q] = sc.out[q][lane];
+    }
+    float t = 0.0f;
+#pragma unroll
+    for (int q = 0; q < S; ++q) {
+      const unsigned long long m = __ballot(cb[q] == __float_as_uint(t));
       if (m) {
-        t = sc.out[q][__ffsll((long long)m) - 1];
+        t = __shfl(ob[q], __ffsll((long long)m) - 1, 64);
       } else {
         const int q0 = min(n, q * L), q1 = min(n, q0 + L);
         int k = q0;
