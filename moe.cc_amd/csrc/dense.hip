@@ -721,20 +721,29 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   if (lane < rows) {
     float dot;
     if constexpr (REG) {
-      const bool fresh = own_new && lane == P - tk0;   // row P: computed above, in LDS
-      const float4* kn4 = reinterpret_cast<const float4*>(kt);
+      if (own_new && lane == P - tk0) {   // row P: computed above, in LDS
+        const float4* kn4 = reinterpret_cast<const float4*>(kt);
+#pragma unroll
+        for (int i = 0; i < kRegHd / 4; ++i) kr[i] = kn4[i < h4 ? i : h4 - 1];
+      }
       const float4* q4 = reinterpret_cast<const float4*>(q);
       dot = 0.0f;
+      // the query (an LDS broadcast) is read 8 float4 ahead of its adds
 #pragma unroll
-      for (int i = 0; i < kRegHd / 4; ++i) {
-        if (i < h4) {
-          const float4 kv = fresh ? kn4[i] : kr[i];
-          const float4 qv = q4[i];
-          const float p0 = qv.x * kv.x, p1 = qv.y * kv.y, p2 = qv.z * kv.z, p3 = qv.w * kv.w;
-          dot = dot + p0;
-          dot = dot + p1;
-          dot = dot + p2;
-          dot = dot + p3;
+      for (int ib = 0; ib < kRegHd / 4; ib += 8) {
+        float4 qv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qv[u] = q4[ib + u < h4 ? ib + u : h4 - 1];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (ib + u < h4) {
+            const float p0 = qv[u].x * kr[ib + u].x, p1 = qv[u].y * kr[ib + u].y;
+            const float p2 = qv[u].z * kr[ib + u].z, p3 = qv[u].w * kr[ib + u].w;
+            dot = dot + p0;
+            dot = dot + p1;
+            dot = dot + p2;
+            dot = dot + p3;
+          }
         }
       }
     } else {
