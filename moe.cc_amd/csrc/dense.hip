@@ -159,6 +159,16 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   if (prod >= 0 && prod < nc) loadW(prod);
   if constexpr (NORM) {
     const int k4 = K / 4;
+    // the norm weights this thread applies, loaded while the squares are summed
+    constexpr int NWR = 2;
+    const bool nw_regs = k4 <= NWR * NT;
+    float4 nwr[NWR];
+#pragma unroll
+    for (int u = 0; u < NWR; ++u) {
+      const int j = (int)threadIdx.x + u * NT;
+      nwr[u] = (nw_regs && a.norm_w && j < k4) ? reinterpret_cast<const float4*>(a.norm_w)[j]
+                                              : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
     for (int i = threadIdx.x; i < M * k4; i += NT) {
       const int m = i / k4, j = i % k4;
       const float4 v = *reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda + 4 * j);
@@ -171,9 +181,25 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       if (threadIdx.x == 0) inv_s[m] = 1.0f / sqrtf(msq / (float)K + a.eps);
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < M * K; i += NT) {
-      const float v = xs[i] * inv_s[i / K];
-      xs[i] = a.norm_w ? v * a.norm_w[i % K] : v * 1.0f;
+    if (nw_regs) {
+      // (a missing weight is 1: the reference multiplies by 1.0f)
+#pragma unroll
+      for (int u = 0; u < NWR; ++u) {
+        const int j = (int)threadIdx.x + u * NT;
+        if (j < k4)
+          for (int m = 0; m < M; ++m) {
+            float4* xp = reinterpret_cast<float4*>(xs + (size_t)m * K) + j;
+            const float4 x = *xp, w = nwr[u];
+            const float iv = inv_s[m];
+            const float v0 = x.x * iv, v1 = x.y * iv, v2 = x.z * iv, v3 = x.w * iv;
+            *xp = make_float4(v0 * w.x, v1 * w.y, v2 * w.z, v3 * w.w);
+          }
+      }
+    } else {
+      for (int i = threadIdx.x; i < M * K; i += NT) {
+        const float v = xs[i] * inv_s[i / K];
+        xs[i] = a.norm_w ? v * a.norm_w[i % K] : v * 1.0f;
+      }
     }
     __syncthreads();
     // this block's column slice [c0, c1) (a multiple of 8 columns)
