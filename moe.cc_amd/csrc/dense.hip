@@ -1051,8 +1051,11 @@ moe_status launch_tile(const DenseArgs& a, hipStream_t s) {
 }  // namespace
 
 // Producer waves of the few-token GEMV: three for one token (the LDS of four
-// product buffers fits), one otherwise.
+// product buffers fits), one otherwise; the wide one-token products (the
+// vocabulary head) keep MOEHIP_HEAD_NP... three as well: their rows stream
+// from HBM and more producers keep more bytes in flight.
 constexpr int kNpOne = 3;
+constexpr int kNpWide = 3;
 
 bool dense_norm_ok(int M, int K) {
   return M >= 1 && M <= 4 && K % 4 == 0 && K <= 8192 &&
@@ -1092,7 +1095,7 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (a.amax_part) {
     if (!dense_amax_ok(a))
       return set_error(MOE_ERR_ARG, "dense matmul: block maxima need one aligned row");
-    return dense_amax_rows(a.N) == 64 ? launch_gemv<64, false, 0, 1>(a, s)
+    return dense_amax_rows(a.N) == 64 ? launch_gemv<64, false, 0, kNpWide>(a, s)
                                       : launch_gemv<16, false, 0, kNpOne>(a, s);
   }
   if (a.sel_counter && (!dense_select_ok(a.M, a.N) || a.sel_topk < 1 || a.sel_topk > kMaxTopK ||
@@ -1130,7 +1133,7 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     return a.M == 1 ? launch_gemv<16, false, 0, kNpOne>(a, s) : launch_gemv<16, false, 0, 1>(a, s);
   }
   if (a.M == 1 && a.N >= 65536) {
-    return launch_gemv<64, false, 0, 1>(a, s);
+    return launch_gemv<64, false, 0, kNpWide>(a, s);
   } else if (a.M <= 2 && a.N >= 32768) {
     return launch_gemv<32, false, 0, 1>(a, s);
   } else if (a.M == 1) {
