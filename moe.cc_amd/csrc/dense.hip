@@ -156,31 +156,56 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       }
     }
   };
-  if (prod >= 0 && prod < nc) loadW(prod);
   if constexpr (NORM) {
     const int k4 = K / 4;
-    // the norm weights this thread applies, loaded while the squares are summed
-    constexpr int NWR = 2;
+    // The token rows first, alone: issued with the weight chunks of every
+    // block they would return behind that burst.  Producer 0 requests chunk
+    // 0 once the rows are in (after the staging barrier), so that it arrives
+    // while the squares are summed; the other producers' first chunks, needed
+    // a chunk-time later, wait until the norm is done.
+    constexpr int XR = 2, NWR = 2;
+    const bool x_regs = M * k4 <= XR * NT;
     const bool nw_regs = k4 <= NWR * NT;
-    float4 nwr[NWR];
+    float4 xr[XR], nwr[NWR];
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+      const int i = (int)threadIdx.x + u * NT;
+      xr[u] = (x_regs && i < M * k4)
+                  ? *reinterpret_cast<const float4*>(a.A + (size_t)(i / k4) * a.lda + 4 * (i % k4))
+                  : zero4();
+    }
 #pragma unroll
     for (int u = 0; u < NWR; ++u) {
       const int j = (int)threadIdx.x + u * NT;
       nwr[u] = (nw_regs && a.norm_w && j < k4) ? reinterpret_cast<const float4*>(a.norm_w)[j]
                                               : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    for (int i = threadIdx.x; i < M * k4; i += NT) {
-      const int m = i / k4, j = i % k4;
-      const float4 v = *reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda + 4 * j);
-      reinterpret_cast<float4*>(xs)[i] = v;
-      reinterpret_cast<float4*>(pl)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    if (x_regs) {
+#pragma unroll
+      for (int u = 0; u < XR; ++u) {
+        const int i = (int)threadIdx.x + u * NT;
+        if (i < M * k4) {
+          const float4 v = xr[u];
+          reinterpret_cast<float4*>(xs)[i] = v;
+          reinterpret_cast<float4*>(pl)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+        }
+      }
+    } else {
+      for (int i = threadIdx.x; i < M * k4; i += NT) {
+        const int m = i / k4, j = i % k4;
+        const float4 v = *reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda + 4 * j);
+        reinterpret_cast<float4*>(xs)[i] = v;
+        reinterpret_cast<float4*>(pl)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+      }
     }
     __syncthreads();
+    if (prod == 0 && nc > 0) loadW(0);
     for (int m = 0; m < M; ++m) {
       const float msq = block_seq_sum<NT>(pl + (size_t)m * K, K, seq);
       if (threadIdx.x == 0) inv_s[m] = 1.0f / sqrtf(msq / (float)K + a.eps);
     }
     __syncthreads();
+    if (prod > 0 && prod < nc) loadW(prod);
     if (nw_regs) {
       // (a missing weight is 1: the reference multiplies by 1.0f)
 #pragma unroll
@@ -236,6 +261,9 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
         }
       }
     }
+  }
+  if constexpr (!NORM) {
+    if (prod >= 0 && prod < nc) loadW(prod);
   }
   if (prod >= 0) {
     if (prod < nc) loadX(prod);
@@ -330,7 +358,10 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
 // instead of K.  With PACK each block packs its column slice of the
 // normalized row into the activation tables (row_finish_kernel writes the
 // header and, with a fused selection, picks the experts).
-constexpr int kRowThreads = 256;
+// 512 threads: two waves per SIMD.  A wave issues a VALU instruction about
+// every 8 clocks whether or not it depends on the previous one, so the
+// candidate chains of block_seq_sum fill a SIMD only with two waves on it.
+constexpr int kRowThreads = 512;
 constexpr int kRowMaxK = 8192;
 
 template <bool NORM, int PACK>
@@ -339,7 +370,6 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   const int K = a.K, k4 = K / 4, n = blockIdx.x;
   float* xs = reinterpret_cast<float*>(rl4);   // [K] the token row
   float* pv = xs + K;                          // [K] squares, then products, then keys
-  float* nw = pv + K;                          // [K] NORM: the norm weights
   float4* xs4 = rl4;
   float4* pv4 = rl4 + k4;
   __shared__ SeqSumScratch seq;
@@ -347,7 +377,18 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   __shared__ float inv_s;
   const int tid = threadIdx.x, lane = tid % kWave;
   constexpr int WV = kRowMaxK / 4 / kRowThreads;
-  // the weight row into registers first, then the token row into LDS
+  // the token row (and norm weights) into registers first, then the weight
+  // row (a wave's loads complete in order: the LDS staging waits only for
+  // the token row)
+  const float4* x4 = reinterpret_cast<const float4*>(a.A);
+  const float4* nw4g = reinterpret_cast<const float4*>(a.norm_w);
+  float4 xv[WV], nv[WV];
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = tid + kRowThreads * u;
+    xv[u] = i < k4 ? x4[i] : zero4();
+    nv[u] = (NORM && a.norm_w && i < k4) ? nw4g[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+  }
   const float4* wr = reinterpret_cast<const float4*>(a.W + (size_t)n * a.ldw);
   float4 w[WV];
 #pragma unroll
@@ -355,14 +396,13 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
     const int i = tid + kRowThreads * u;
     w[u] = i < k4 ? wr[i] : zero4();
   }
-  const float4* x4 = reinterpret_cast<const float4*>(a.A);
-  const float4* nw4g = reinterpret_cast<const float4*>(a.norm_w);
-  for (int i = tid; i < k4; i += kRowThreads) {
-    const float4 v = x4[i];
-    xs4[i] = v;
-    if (NORM) {
-      pv4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-      reinterpret_cast<float4*>(nw)[i] = a.norm_w ? nw4g[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = tid + kRowThreads * u;
+    if (i < k4) {
+      const float4 v = xv[u];
+      xs4[i] = v;
+      if (NORM) pv4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
     }
   }
   __syncthreads();
@@ -370,9 +410,16 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
     const float msq = block_seq_sum<kRowThreads>(pv, K, seq);
     if (tid == 0) inv_s = 1.0f / sqrtf(msq / (float)K + a.eps);
     __syncthreads();
-    for (int i = tid; i < K; i += kRowThreads) {
-      const float v = xs[i] * inv_s;
-      xs[i] = v * nw[i];   // a missing weight is 1 (the reference multiplies by 1.0f)
+    // (a missing weight is 1: the reference multiplies by 1.0f)
+    const float iv = inv_s;
+#pragma unroll
+    for (int u = 0; u < WV; ++u) {
+      const int i = tid + kRowThreads * u;
+      if (i < k4) {
+        const float4 x = xv[u], g = nv[u];
+        const float v0 = x.x * iv, v1 = x.y * iv, v2 = x.z * iv, v3 = x.w * iv;
+        xs4[i] = make_float4(v0 * g.x, v1 * g.y, v2 * g.z, v3 * g.w);
+      }
     }
     __syncthreads();
     // this block's column slice [c0, c1) (a multiple of 8 columns)
@@ -1080,7 +1127,7 @@ bool dense_row_ok(const DenseArgs& a, bool vec) {
 
 template <bool NORM, int PACK>
 moe_status launch_row(const DenseArgs& a, hipStream_t s) {
-  const size_t lds = (size_t)(NORM ? 3 : 2) * a.K * 4;
+  const size_t lds = (size_t)2 * a.K * 4;
   moe_status st = set_lds(dense_row_kernel<NORM, PACK>, lds, "row kernel LDS attribute");
   if (st) return st;
   hipLaunchKernelGGL((dense_row_kernel<NORM, PACK>), dim3((unsigned)a.N), dim3(kRowThreads), lds, s, a);

@@ -214,28 +214,59 @@ __device__ __forceinline__ float seq_unkey(int32_t k) {
   return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF);
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, true);
+  return __hiloint2double(hi, lo);
+}
+
+// Sum over groups of W consecutive lanes (W = 4 .. 64, a power of two);
+// every lane of a group gets its group's total.
+template <int W>
+__device__ __forceinline__ double group_sum_f64(double v) {
+  v += dpp_f64<0xB1>(v);                 // quad_perm [1,0,3,2]
+  v += dpp_f64<0x4E>(v);                 // quad_perm [2,3,0,1]
+  if (W >= 8) v += dpp_f64<0x141>(v);    // row_half_mirror
+  if (W >= 16) v += dpp_f64<0x140>(v);   // row_mirror
+  if (W >= 32) v += __shfl_xor(v, 16, 64);
+  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Every thread of the block (NT threads: 32 to 512, a power of two) must
 // call this; p (LDS) holds the n values; returns s to every thread.
 template <int NT>
-__device__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
+__device__ __forceinline__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
   constexpr int S = kSeqSegs, C = NT / S, CPT = kSeqCands / C;
   static_assert(C >= 4 && C <= 64 && (C & (C - 1)) == 0 && CPT >= 1 && C * CPT == kSeqCands,
                 "threads per segment");
   const int tid = threadIdx.x, j = tid / C, i = tid % C;
   const int L = ((n + S - 1) / S + 3) & ~3;   // segments start on float4 boundaries
   const int k0 = min(n, j * L), k1 = min(n, k0 + L);
-  // 1. segment sums in double (the C threads of a segment are adjacent lanes)
+  const float4* p4 = reinterpret_cast<const float4*>(p);   // p is 16-byte aligned
+  // 1. segment sums in double (the C threads of a segment are adjacent
+  // lanes; any order: this is an estimate)
   double d = 0.0;
-  for (int k = k0 + i; k < k1; k += C) d += (double)p[k];
-#pragma unroll
-  for (int off = C / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+  {
+    const int f1 = k0 / 4 + (k1 - k0) / 4;   // whole float4 of the segment
+#pragma unroll 2
+    for (int f = k0 / 4 + i; f < f1; f += C) {
+      const float4 v = p4[f];
+      d += ((double)v.x + (double)v.y) + ((double)v.z + (double)v.w);
+    }
+    if (4 * f1 + i < k1) d += (double)p[4 * f1 + i];
+  }
+  d = group_sum_f64<C>(d);
   if (i == 0) sc.part[j] = d;
   __syncthreads();
   // 2.-3. the start estimate of segment j and this thread's candidates
   float c[CPT];
   if (j > 0) {
     double est = 0.0;
-    for (int q = 0; q < j; ++q) est += sc.part[q];
+#pragma unroll
+    for (int q = 0; q < S - 1; ++q)
+      if (q < j) est += sc.part[q];
     const int32_t base = seq_key((float)est) - kSeqCands / 2 + i * CPT;
 #pragma unroll
     for (int u = 0; u < CPT; ++u) c[u] = seq_unkey(base + u);
@@ -248,22 +279,24 @@ __device__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
 #pragma unroll
   for (int u = 0; u < CPT; ++u) acc[u] = c[u];
   {
-    // 16 float4 read ahead of their 64 x CPT adds (p is 16-byte aligned)
-    const float4* p4 = reinterpret_cast<const float4*>(p);
+    // 16 float4 read ahead of their 64 x CPT adds; the chains take turns
+    // value by value
     int k = k0;
     for (; k + 64 <= k1; k += 64) {
       float4 v[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) v[r] = p4[k / 4 + r];
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
+      for (int r = 0; r < 16; ++r) {
 #pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-          acc[u] = acc[u] + v[r].x;
-          acc[u] = acc[u] + v[r].y;
-          acc[u] = acc[u] + v[r].z;
-          acc[u] = acc[u] + v[r].w;
-        }
+        for (int u = 0; u < CPT; ++u) acc[u] = acc[u] + v[r].x;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) acc[u] = acc[u] + v[r].y;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) acc[u] = acc[u] + v[r].z;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) acc[u] = acc[u] + v[r].w;
+      }
     }
     for (; k < k1; ++k) {
       const float v = p[k];
@@ -293,7 +326,7 @@ __device__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
     for (int q = 0; q < S; ++q) {
       const unsigned long long m = __ballot(cb[q] == __float_as_uint(t));
       if (m) {
-        t = __shfl(ob[q], __ffsll((long long)m) - 1, 64);
+        t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ob[q]), __ffsll((long long)m) - 1));
       } else {
         const int q0 = min(n, q * L), q1 = min(n, q0 + L);
         int k = q0;
