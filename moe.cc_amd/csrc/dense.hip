@@ -831,7 +831,9 @@ constexpr int kPvThreads = 256;
 // Softmax of the n = pos0 + t + 1 scores of (t, h) and the weighted V sum
 // for head dimensions DPB*g .. DPB*g + DPB - 1 (test_model_trace.c:408-426):
 //   m = S[0], then every larger score (a NaN S[0] stays; later NaNs never
-//   win); e_i = expf(S_i - m); sum = (((0 + e_0) + e_1) + ...) in thread 0;
+//   win); e_i = expf(S_i - m); sum = (((0 + e_0) + e_1) + ...) (the
+//   sequential sum: one chain, or block_seq_sum for the long rows of
+//   prefill);
 //   p_i = e_i * (1 / (sum + 1e-9)); out_d = (((0 + p_0 v_0d) + p_1 v_1d) + ...).
 // The weighted sum runs over chunks of CH positions: every thread forms
 // products p_i * v_id of the chunk into a transposed LDS tile [d][i] (the
@@ -851,7 +853,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   float* es = lds;                                  // [max_seq, rounded up to 4]
   float* pt = lds + ((a.max_seq + 3) & ~3);         // [DPB][LDT]
   __shared__ float red[kPvThreads / kWave];
-  __shared__ float inv_s;
+  __shared__ SeqSumScratch seq;
   const int kvh = h / (a.nq / a.nkv);
   const int d0 = DPB * blockIdx.x;
   const int dl = min(DPB, hd - d0);
@@ -904,9 +906,17 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   for (int i = tid; i < n; i += kPvThreads) es[i] = expf_glibc(es[i] - m);
   for (int i = n + tid; i < ((n + 3) & ~3); i += kPvThreads) es[i] = 0.0f;
   __syncthreads();
-  if (tid == 0) inv_s = 1.0f / (chain_sum(0.0f, es, (n + 3) / 4) + 1e-9f);
-  __syncthreads();
-  const float inv = inv_s;
+  // the sum: by the whole block for long rows (prefill), else one chain in
+  // thread 0 (block_seq_sum's fixed cost exceeds a chain of a few hundred)
+  float esum;
+  if constexpr (DPB >= 128) {
+    esum = block_seq_sum<kPvThreads>(es, n, seq);
+  } else {
+    if (tid == 0) seq.result = chain_sum(0.0f, es, (n + 3) / 4);
+    __syncthreads();
+    esum = seq.result;
+  }
+  const float inv = 1.0f / (esum + 1e-9f);
   for (int i = tid; i < n; i += kPvThreads) es[i] = es[i] * inv;
   __syncthreads();
   float out = 0.0f;

@@ -55,17 +55,25 @@ __global__ __launch_bounds__(kBlock) void act_pack_kernel(QShape sh, const QJob*
                    scratch);
 }
 
-// Epilogue of the plain GEMV: C[m, row] = ((float)dot / div) * S[row].
+// Epilogue of the plain GEMV: y = ((float)dot / div) * S[row], staged in
+// the block's LDS buffer Y[t][row - r0] (t = token slot of the block) and
+// written to C by the whole block at the end (gemv_write_outputs): one
+// coalesced, nontemporal burst per block instead of a 4-byte store per row
+// group in the middle of the weight stream (measured ~1.5% faster; the
+// output writes, ~1% of the bytes, still cost ~8% of the streaming rate on
+// the box, wherever in the launch they are placed).
+constexpr int kYRows = 512;   // rows per block, at most
+
 struct GemvEpiMaker {
   const float* S;
-  float* C;
-  int M, ldc, mbase;
+  float* Y;
+  int ldy, M, mbase, r0;
   float div;
   template <int MTI>
   struct Epi {
     const float* S;
-    float* C;
-    int M, ldc, m0;
+    float* Y;
+    int ldy, M, m0, tb, r0;   // token m0 + t lives in slot tb + t
     float div;
     using Pre = float;
     __device__ Pre pre(int row) const { return S[row]; }
@@ -73,14 +81,25 @@ struct GemvEpiMaker {
     __device__ void operator()(int row, const Tot& tot, float sc) const {
 #pragma unroll
       for (int t = 0; t < MTI; ++t)
-        if (m0 + t < M) C[(size_t)(m0 + t) * ldc + row] = qdot_epilogue(tot[0][t], div, sc);
+        if (m0 + t < M) Y[(tb + t) * ldy + (row - r0)] = qdot_epilogue(tot[0][t], div, sc);
     }
     template <class Tot>
     __device__ void operator()(int row, const Tot& tot) const { (*this)(row, tot, S[row]); }
   };
   template <int MTI>
-  __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{S, C, M, ldc, mbase + t0, div}; }
+  __device__ Epi<MTI> at(int t0) const { return Epi<MTI>{S, Y, ldy, M, mbase + t0, t0, r0, div}; }
 };
+
+// The block's staged outputs to C (after every wave has finished its rows).
+__device__ __forceinline__ void gemv_write_outputs(const float* Y, int ldy, float* C, int ldc,
+                                                   int mbase, int ntok, int r0, int r1) {
+  __syncthreads();
+  const int n = r1 - r0;
+  for (int t = 0; t < ntok; ++t) {
+    float* c = C + (size_t)(mbase + t) * ldc + r0;
+    for (int i = (int)threadIdx.x; i < n; i += (int)blockDim.x) __builtin_nontemporal_store(Y[t * ldy + i], c + i);
+  }
+}
 
 template <bool Q4, class G, int MT>
 __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
@@ -102,8 +121,10 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
     xs[t] = job.A + (size_t)m * a.sh.lda;
   }
   const uint8_t* W[1] = {job.W};
-  GemvEpiMaker mk{job.S, job.C, a.sh.M, a.sh.ldc, mbase, Q4 ? 7.0f : 127.0f};
+  __shared__ float ybuf[MT * kYRows];
+  GemvEpiMaker mk{job.S, ybuf, kYRows, a.sh.M, mbase, r0, Q4 ? 7.0f : 127.0f};
   stream_tokens<Q4, G, 1, MT>(W, a.sh.rs, a.sh.K, tabs, xs, ntok, r0, r1, mk);
+  gemv_write_outputs(ybuf, kYRows, job.C, a.sh.ldc, mbase, ntok, r0, r1);
 }
 
 template <bool Q4>
@@ -116,11 +137,13 @@ __global__ __launch_bounds__(kBlock) void qgemv_generic(QShape sh, const QJob* _
   const int m0 = blockIdx.y * 16;
   const int m1 = m0 + 16 < sh.M ? m0 + 16 : sh.M;
   const uint8_t* W[1] = {job.W};
+  __shared__ float ybuf[16 * kWaves];
+  GemvEpiMaker mk{job.S, ybuf, kWaves, sh.M, m0, r0, Q4 ? 7.0f : 127.0f};
   for (int m = m0; m < m1; ++m) {
-    GemvEpiMaker mk{job.S, job.C, sh.M, sh.ldc, m, Q4 ? 7.0f : 127.0f};
-    auto epi = mk.at<1>(0);
+    auto epi = mk.at<1>(m - m0);
     generic_rows_fp32<Q4, 1>(W, sh.rs, sh.K, job.A + (size_t)m * sh.lda, r0, r1, epi);
   }
+  gemv_write_outputs(ybuf, kWaves, job.C, sh.ldc, m0, m1 - m0, r0, r1);
 }
 
 // fp32 path: one thread per output, k ascending, unfused multiply then add.
@@ -251,6 +274,7 @@ hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJo
   rpb = (rpb + unit - 1) / unit * unit;
   if (rpb < unit) rpb = unit;
   if (rpb > (long long)max_groups * unit) rpb = (long long)max_groups * unit;
+  if (rpb > kYRows) rpb = kYRows / unit * unit;   // the staging buffer's rows
   if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
   TiledArgs a;
   a.sh = sh;
