@@ -733,24 +733,30 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   const int cached = own_new ? rows - 1 : rows;        // rows read from the cache
   const int h4 = hd / 4;
   const int total = cached * h4;
+  // fuse_heads: the head rows, norm weights and cos/sin into registers first
+  // (a wave's loads complete in order: heads_prep below then waits for these
+  // alone, not for the K rows requested after them)
+  constexpr int SR = (REG ? kRegHd : kMaxHd) / 64, SC = SR / 2;
+  float rq[SR], rwq[SR], rk[SR], rwk[SR], rv[SR], rcs[SC], rsn[SC];
+  const bool write_v = own_new && h % group == 0;
   if (a.fuse_heads) {
     const float* krow = a.qkv + (size_t)t * a.ld + (size_t)(a.nq + kvh) * hd;
-    for (int d = lane; d < hd; d += 64) {
-      qraw[d] = qrow[d];
-      if (a.q_norm) wq[d] = a.q_norm[d];
-      if (own_new) {
-        kraw[d] = krow[d];
-        if (a.k_norm) wk[d] = a.k_norm[d];
-      }
+    const float* vraw = a.qkv + (size_t)t * a.ld + (size_t)(a.nq + a.nkv + kvh) * hd;
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      const int d = lane + 64 * u;
+      const bool in = d < hd;
+      rq[u] = in ? qrow[d] : 0.0f;
+      rwq[u] = in && a.q_norm ? a.q_norm[d] : 0.0f;
+      rk[u] = in && own_new ? krow[d] : 0.0f;
+      rwk[u] = in && own_new && a.k_norm ? a.k_norm[d] : 0.0f;
+      rv[u] = in && write_v ? vraw[d] : 0.0f;
     }
-    for (int i = lane; i < d2; i += 64) {
-      cs[i] = a.rope_cos[(size_t)P * d2 + i];
-      sn[i] = a.rope_sin[(size_t)P * d2 + i];
-    }
-    if (own_new && h % group == 0) {   // V row P into the cache unchanged
-      const float* vraw = a.qkv + (size_t)t * a.ld + (size_t)(a.nq + a.nkv + kvh) * hd;
-      float* vd = a.vc + ((size_t)kvh * a.max_seq + P) * hd;
-      for (int d = lane; d < hd; d += 64) vd[d] = vraw[d];
+#pragma unroll
+    for (int u = 0; u < SC; ++u) {
+      const int i = lane + 64 * u;
+      rcs[u] = i < d2 ? a.rope_cos[(size_t)P * d2 + i] : 0.0f;
+      rsn[u] = i < d2 ? a.rope_sin[(size_t)P * d2 + i] : 0.0f;
     }
   }
   float4 kr[REG ? kRegHd / 4 : 1];
@@ -778,6 +784,30 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
     }
   }
   if (a.fuse_heads) {
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      const int d = lane + 64 * u;
+      if (d < hd) {
+        qraw[d] = rq[u];
+        wq[d] = rwq[u];
+        kraw[d] = rk[u];
+        wk[d] = rwk[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < SC; ++u) {
+      const int i = lane + 64 * u;
+      if (i < d2) {
+        cs[i] = rcs[u];
+        sn[i] = rsn[u];
+      }
+    }
+    if (write_v) {   // V row P into the cache unchanged
+      float* vd = a.vc + ((size_t)kvh * a.max_seq + P) * hd;
+#pragma unroll
+      for (int u = 0; u < SR; ++u)
+        if (lane + 64 * u < hd) vd[lane + 64 * u] = rv[u];
+    }
     __syncthreads();
     float* knew = REG ? kt : kt + (P - tk0) * LD;
     heads_prep(qraw, own_new ? kraw : nullptr, a.q_norm ? wq : nullptr, a.k_norm ? wk : nullptr,
@@ -882,14 +912,38 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
       col[3 * LDT] = pk * rg[u].w;
     }
   };
-  // the first V tile loads while the softmax runs
-  load(0);
+  // the scores first (into registers when they fit), then the first V
+  // tile, which loads while the softmax runs (a thread's loads complete in
+  // order, so the max waits for the scores alone)
   const float* Srow = a.S + ((size_t)t * a.nq + h) * a.max_seq;
+  constexpr int SR = 8;
+  const bool s_regs = n <= SR * kPvThreads;
+  float sr[SR];
+  if (s_regs) {
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      const int i = tid + kPvThreads * u;
+      sr[u] = i < n ? Srow[i] : 0.0f;
+    }
+  }
+  load(0);
   float mx = -__builtin_inff();
-  for (int i = tid; i < n; i += kPvThreads) {
-    const float s = Srow[i];
-    es[i] = s;
-    if (s == s && s > mx) mx = s;
+  if (s_regs) {
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      const int i = tid + kPvThreads * u;
+      if (i < n) {
+        const float s = sr[u];
+        es[i] = s;
+        if (s == s && s > mx) mx = s;
+      }
+    }
+  } else {
+    for (int i = tid; i < n; i += kPvThreads) {
+      const float s = Srow[i];
+      es[i] = s;
+      if (s == s && s > mx) mx = s;
+    }
   }
   // order-free max over the non-NaN scores (-inf when there is none)
 #pragma unroll
