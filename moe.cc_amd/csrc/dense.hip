@@ -13,6 +13,7 @@
 // dependent v_add_f32 every ~8 clocks).  Order-free steps (max, expf, the
 // products of the softmax) run across lanes.
 #include <climits>
+#include <cstdlib>
 #include <math.h>
 
 #include <mutex>
@@ -985,6 +986,170 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   if (tid < dl) a.H[(size_t)t * a.nq * hd + (size_t)h * hd + d0 + tid] = out;
 }
 
+// ---- many query rows (prefill): kQt rows share each staged K / V tile ----
+//
+// The one-row kernels above read the whole key / value prefix once per
+// query row (T^2/2 rows of hd floats for T new rows); these read it once per
+// kQt rows.  Same chains, same order: bit-identical results.
+constexpr int kQt = 8;
+
+// Scores of query rows t0 .. t0 + kQt - 1 (t0 = kQt blockIdx.z) of head
+// blockIdx.y against keys tk0 .. tk0 + 63 (tk0 = 64 blockIdx.x): K rows and
+// queries staged in LDS with coalesced loads; wave w runs the chains of rows
+// 2w and 2w + 1 side by side, lane = key.  q must already be normed and
+// rotated (heads_kernel).  S as attn_scores_kernel, key <= pos0 + t only.
+__global__ __launch_bounds__(256) void attn_scores_qt_kernel(AttnArgs a) {
+  extern __shared__ float lds[];
+  const int hd = a.hd, h4 = hd / 4, LD = hd + 4;
+  float* kt = lds;             // [64][LD]
+  float* qs = kt + 64 * LD;    // [kQt][hd]
+  const int h = blockIdx.y, t0 = blockIdx.z * kQt, tk0 = blockIdx.x * 64;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int nt = min(kQt, a.T - t0);
+  const int Pmax = a.pos0 + t0 + nt - 1;
+  if (tk0 > Pmax) return;   // every key of the block is masked (uniform)
+  const int kvh = h / (a.nq / a.nkv);
+  const int rows = min(64, Pmax + 1 - tk0);
+  const float* kbase = a.kc + ((size_t)kvh * a.max_seq + tk0) * hd;
+  {
+    const int total = rows * h4, qtotal = nt * h4;
+    constexpr int U = 8;   // float4 loads in flight per thread
+    for (int base = 0; base < total + qtotal; base += 256 * U) {
+      float4 r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + tid + 256 * u;
+        if (i < total) {
+          r[u] = *reinterpret_cast<const float4*>(kbase + (size_t)(i / h4) * hd + 4 * (i % h4));
+        } else if (i < total + qtotal) {
+          const int j = i - total;
+          r[u] = *reinterpret_cast<const float4*>(a.qkv + (size_t)(t0 + j / h4) * a.ld + (size_t)h * hd +
+                                                  4 * (j % h4));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + tid + 256 * u;
+        if (i < total) {
+          *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
+        } else if (i < total + qtotal) {
+          const int j = i - total;
+          *reinterpret_cast<float4*>(qs + (j / h4) * hd + 4 * (j % h4)) = r[u];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int qa = 2 * wave, qb = qa + 1, key = tk0 + lane;
+  const bool va = lane < rows && qa < nt && key <= a.pos0 + t0 + qa;
+  const bool vb = lane < rows && qb < nt && key <= a.pos0 + t0 + qb;
+  if (!va && !vb) return;
+  const float4* k4 = reinterpret_cast<const float4*>(kt + lane * LD);
+  const float4* x4 = reinterpret_cast<const float4*>(qs + qa * hd);
+  const float4* y4 = reinterpret_cast<const float4*>(qs + (qb < nt ? qb : qa) * hd);
+  float da = 0.0f, db = 0.0f;
+  for (int c = 0; c < h4; ++c) {
+    const float4 k = k4[c], x = x4[c], y = y4[c];
+    const float a0 = x.x * k.x, a1 = x.y * k.y, a2 = x.z * k.z, a3 = x.w * k.w;
+    const float b0 = y.x * k.x, b1 = y.y * k.y, b2 = y.z * k.z, b3 = y.w * k.w;
+    da = da + a0;
+    db = db + b0;
+    da = da + a1;
+    db = db + b1;
+    da = da + a2;
+    db = db + b2;
+    da = da + a3;
+    db = db + b3;
+  }
+  if (va) a.S[((size_t)(t0 + qa) * a.nq + h) * a.max_seq + key] = da * a.scale;
+  if (vb) a.S[((size_t)(t0 + qb) * a.nq + h) * a.max_seq + key] = db * a.scale;
+}
+
+// Softmax and weighted V sum of query rows t0 .. t0 + kQt - 1 of head
+// blockIdx.y for dimensions d0 .. d0 + kPvDpb - 1: thread (qi, dd) =
+// (tid / kPvDpb, tid % kPvDpb).  Row qi (n = pos0 + t0 + qi + 1 scores) in
+// LDS; its max by its kPvDpb threads (order-free, a NaN first score wins as
+// in attn_softmax_pv_kernel), e = expf(s - m), the sum chain in thread dd =
+// 0, p = e * (1 / (sum + 1e-9)); then V staged kPvCh positions at a time and
+// out = (((0 + p_0 v_0) + p_1 v_1) + ...) over the row's positions in order.
+constexpr int kPvDpb = 32;
+constexpr int kPvCh = 128;
+static_assert(kQt * kPvDpb == 256, "one thread per (row, dimension)");
+
+size_t attn_pv_qt_lds(int pos0, int T) {
+  const size_t es = (size_t)((pos0 + T + 3) & ~3);
+  return ((size_t)kQt * es + (size_t)kPvCh * kPvDpb) * 4;
+}
+
+__global__ __launch_bounds__(256) void attn_pv_qt_kernel(AttnArgs a) {
+  extern __shared__ float lds[];
+  const int hd = a.hd;
+  const int h = blockIdx.y, t0 = blockIdx.z * kQt, d0 = blockIdx.x * kPvDpb;
+  const int tid = threadIdx.x, qi = tid / kPvDpb, dd = tid % kPvDpb;
+  const int ES = (a.pos0 + a.T + 3) & ~3;            // row stride of es
+  float* es = lds;                                    // [kQt][ES]
+  float* vt = es + (size_t)kQt * ES;                  // [kPvCh][kPvDpb]
+  __shared__ float inv_s[kQt];
+  const int nt = min(kQt, a.T - t0);
+  const int nmax = a.pos0 + t0 + nt;                  // positions of the last row
+  const bool row_live = qi < nt;
+  const int n = row_live ? a.pos0 + t0 + qi + 1 : 0;
+  const int kvh = h / (a.nq / a.nkv);
+  float* er = es + (size_t)qi * ES;
+  // 1. the row's scores, its max, the exponentials
+  const float* Srow = a.S + ((size_t)(t0 + qi) * a.nq + h) * a.max_seq;
+  float mx = -__builtin_inff();
+  for (int i = dd; i < n; i += kPvDpb) {
+    const float s = Srow[i];
+    er[i] = s;
+    if (s == s && s > mx) mx = s;
+  }
+#pragma unroll
+  for (int off = kPvDpb / 2; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off, kWave);
+    mx = o > mx ? o : mx;
+  }
+  __syncthreads();
+  float m = mx;
+  if (n > 0) {
+    const float s0 = er[0];
+    if (s0 != s0) m = s0;
+  }
+  for (int i = dd; i < n; i += kPvDpb) er[i] = expf_glibc(er[i] - m);
+  for (int i = n + dd; i < ((n + 3) & ~3); i += kPvDpb) er[i] = 0.0f;
+  __syncthreads();
+  if (dd == 0 && row_live) inv_s[qi] = 1.0f / (chain_sum(0.0f, er, (n + 3) / 4) + 1e-9f);
+  __syncthreads();
+  if (row_live) {
+    const float inv = inv_s[qi];
+    for (int i = dd; i < n; i += kPvDpb) er[i] = er[i] * inv;
+  }
+  // 2. the weighted V sums
+  const float* vbase = a.vc + (size_t)kvh * a.max_seq * hd + d0;
+  const int dl = min(kPvDpb, hd - d0);
+  float out = 0.0f;
+  for (int c0 = 0; c0 < nmax; c0 += kPvCh) {
+    __syncthreads();   // the previous chunk's readers are done (and p is complete)
+    constexpr int PER = kPvCh * kPvDpb / 4 / 256;   // float4 per thread
+    float4 r[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = tid + 256 * u;                  // float4 index in the tile
+      const int pos = c0 + i / (kPvDpb / 4), c = 4 * (i % (kPvDpb / 4));
+      r[u] = (pos < nmax && c < dl) ? *reinterpret_cast<const float4*>(vbase + (size_t)pos * hd + c) : zero4();
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) reinterpret_cast<float4*>(vt)[tid + 256 * u] = r[u];
+    __syncthreads();
+    const int np = min(kPvCh, n - c0);
+    for (int j = 0; j < np; ++j) {
+      const float pv = er[c0 + j] * vt[j * kPvDpb + dd];
+      out = out + pv;
+    }
+  }
+  if (row_live && dd < dl) a.H[(size_t)(t0 + qi) * a.nq * hd + (size_t)h * hd + d0 + dd] = out;
+}
+
 // ---------------------------------------------------------------- misc
 
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ ids,
@@ -1279,6 +1444,21 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   if (a.T <= 0) return MOE_OK;
   if (a.hd % 4 || a.hd > kMaxHd) return set_error(MOE_ERR_ARG, "attention: head_dim %d", a.hd);
   if (a.fuse_heads && a.T != 1) return set_error(MOE_ERR_ARG, "attention: fused heads need T == 1");
+  if (a.T > 4 && !a.fuse_heads && a.nkv > 0 && a.nq % a.nkv == 0 &&
+      attn_pv_qt_lds(a.pos0, a.T) <= 160 * 1024 && !getenv("MOEHIP_ATTN_ROWWISE")) {
+    const unsigned qg = (unsigned)((a.T + kQt - 1) / kQt);
+    const size_t lds_s = ((size_t)64 * (a.hd + 4) + (size_t)kQt * a.hd) * 4;
+    moe_status st;
+    if ((st = set_lds(attn_scores_qt_kernel, lds_s, "scores LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_scores_qt_kernel, dim3((unsigned)((a.pos0 + a.T + 63) / 64), (unsigned)a.nq, qg),
+                       dim3(256), lds_s, s, a);
+    if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
+    const size_t lds_p = attn_pv_qt_lds(a.pos0, a.T);
+    if ((st = set_lds(attn_pv_qt_kernel, lds_p, "softmax/pv LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_pv_qt_kernel, dim3((unsigned)((a.hd + kPvDpb - 1) / kPvDpb), (unsigned)a.nq, qg),
+                       dim3(256), lds_p, s, a);
+    return check_hip(hipGetLastError(), "softmax/pv launch");
+  }
   const int nmax = a.pos0 + a.T;   // positions of the last row
   const size_t hdp = (size_t)((a.hd + 3) & ~3);
   const dim3 sgrid((unsigned)((nmax + 63) / 64), (unsigned)a.nq, (unsigned)a.T);
