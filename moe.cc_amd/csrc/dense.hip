@@ -986,83 +986,86 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   if (tid < dl) a.H[(size_t)t * a.nq * hd + (size_t)h * hd + d0 + tid] = out;
 }
 
-// ---- many query rows (prefill): kQt rows share each staged K / V tile ----
+// ---- many query rows (prefill): several rows share each staged K / V tile ----
 //
 // The one-row kernels above read the whole key / value prefix once per
 // query row (T^2/2 rows of hd floats for T new rows); these read it once per
-// kQt rows.  Same chains, same order: bit-identical results.
+// kSq (scores) or kQt (softmax and V sums) rows.  Same chains, same order:
+// bit-identical results.
 constexpr int kQt = 8;
 
-// Scores of query rows t0 .. t0 + kQt - 1 (t0 = kQt blockIdx.z) of head
+// Scores of query rows t0 .. t0 + kSq - 1 (t0 = kSq blockIdx.z) of head
 // blockIdx.y against keys tk0 .. tk0 + 63 (tk0 = 64 blockIdx.x): K rows and
 // queries staged in LDS with coalesced loads; wave w runs the chains of rows
-// 2w and 2w + 1 side by side, lane = key.  q must already be normed and
-// rotated (heads_kernel).  S as attn_scores_kernel, key <= pos0 + t only.
+// w, w + 4, w + 8, w + 12 side by side, lane = key.  q must already be
+// normed and rotated (heads_kernel).  S as attn_scores_kernel, key <= pos0 +
+// t only.
+constexpr int kSq = 16;                 // query rows per block
+constexpr int kSqPerWave = kSq / 4;     // chains per lane
+
 __global__ __launch_bounds__(256) void attn_scores_qt_kernel(AttnArgs a) {
   extern __shared__ float lds[];
   const int hd = a.hd, h4 = hd / 4, LD = hd + 4;
   float* kt = lds;             // [64][LD]
-  float* qs = kt + 64 * LD;    // [kQt][hd]
-  const int h = blockIdx.y, t0 = blockIdx.z * kQt, tk0 = blockIdx.x * 64;
+  float* qs = kt + 64 * LD;    // [kSq][hd]
+  const int h = blockIdx.y, t0 = blockIdx.z * kSq, tk0 = blockIdx.x * 64;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int nt = min(kQt, a.T - t0);
+  const int nt = min(kSq, a.T - t0);
   const int Pmax = a.pos0 + t0 + nt - 1;
   if (tk0 > Pmax) return;   // every key of the block is masked (uniform)
   const int kvh = h / (a.nq / a.nkv);
   const int rows = min(64, Pmax + 1 - tk0);
   const float* kbase = a.kc + ((size_t)kvh * a.max_seq + tk0) * hd;
-  {
-    const int total = rows * h4, qtotal = nt * h4;
-    constexpr int U = 8;   // float4 loads in flight per thread
-    for (int base = 0; base < total + qtotal; base += 256 * U) {
-      float4 r[U];
+  // K rows (rows past `rows` read row rows - 1; never used), then the queries
+  // (rows past nt read row nt - 1)
+  for (int base = 0; base < 64 * h4; base += 256 * 8) {
+    float4 r[8];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = base + tid + 256 * u;
-        if (i < total) {
-          r[u] = *reinterpret_cast<const float4*>(kbase + (size_t)(i / h4) * hd + 4 * (i % h4));
-        } else if (i < total + qtotal) {
-          const int j = i - total;
-          r[u] = *reinterpret_cast<const float4*>(a.qkv + (size_t)(t0 + j / h4) * a.ld + (size_t)h * hd +
-                                                  4 * (j % h4));
-        }
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + tid + 256 * u, rr = min(i / h4, rows - 1);
+      r[u] = i < 64 * h4 ? *reinterpret_cast<const float4*>(kbase + (size_t)rr * hd + 4 * (i % h4)) : zero4();
+    }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = base + tid + 256 * u;
-        if (i < total) {
-          *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
-        } else if (i < total + qtotal) {
-          const int j = i - total;
-          *reinterpret_cast<float4*>(qs + (j / h4) * hd + 4 * (j % h4)) = r[u];
-        }
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + tid + 256 * u;
+      if (i < 64 * h4) *reinterpret_cast<float4*>(kt + (i / h4) * LD + 4 * (i % h4)) = r[u];
     }
   }
-  __syncthreads();
-  const int qa = 2 * wave, qb = qa + 1, key = tk0 + lane;
-  const bool va = lane < rows && qa < nt && key <= a.pos0 + t0 + qa;
-  const bool vb = lane < rows && qb < nt && key <= a.pos0 + t0 + qb;
-  if (!va && !vb) return;
-  const float4* k4 = reinterpret_cast<const float4*>(kt + lane * LD);
-  const float4* x4 = reinterpret_cast<const float4*>(qs + qa * hd);
-  const float4* y4 = reinterpret_cast<const float4*>(qs + (qb < nt ? qb : qa) * hd);
-  float da = 0.0f, db = 0.0f;
-  for (int c = 0; c < h4; ++c) {
-    const float4 k = k4[c], x = x4[c], y = y4[c];
-    const float a0 = x.x * k.x, a1 = x.y * k.y, a2 = x.z * k.z, a3 = x.w * k.w;
-    const float b0 = y.x * k.x, b1 = y.y * k.y, b2 = y.z * k.z, b3 = y.w * k.w;
-    da = da + a0;
-    db = db + b0;
-    da = da + a1;
-    db = db + b1;
-    da = da + a2;
-    db = db + b2;
-    da = da + a3;
-    db = db + b3;
+  for (int i = tid; i < kSq * h4; i += 256) {
+    const int qr = min(i / h4, nt - 1);
+    *reinterpret_cast<float4*>(qs + (i / h4) * hd + 4 * (i % h4)) =
+        *reinterpret_cast<const float4*>(a.qkv + (size_t)(t0 + qr) * a.ld + (size_t)h * hd + 4 * (i % h4));
   }
-  if (va) a.S[((size_t)(t0 + qa) * a.nq + h) * a.max_seq + key] = da * a.scale;
-  if (vb) a.S[((size_t)(t0 + qb) * a.nq + h) * a.max_seq + key] = db * a.scale;
+  __syncthreads();
+  const int key = tk0 + lane;
+  if (lane >= rows) return;
+  const float4* k4 = reinterpret_cast<const float4*>(kt + lane * LD);
+  float dot[kSqPerWave];
+#pragma unroll
+  for (int u = 0; u < kSqPerWave; ++u) dot[u] = 0.0f;
+  for (int c = 0; c < h4; ++c) {
+    const float4 k = k4[c];
+    float4 x[kSqPerWave];
+#pragma unroll
+    for (int u = 0; u < kSqPerWave; ++u) x[u] = reinterpret_cast<const float4*>(qs + (wave + 4 * u) * hd)[c];
+    float p[kSqPerWave][4];
+#pragma unroll
+    for (int u = 0; u < kSqPerWave; ++u) {
+      p[u][0] = x[u].x * k.x;
+      p[u][1] = x[u].y * k.y;
+      p[u][2] = x[u].z * k.z;
+      p[u][3] = x[u].w * k.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int u = 0; u < kSqPerWave; ++u) dot[u] = dot[u] + p[u][e];
+  }
+#pragma unroll
+  for (int u = 0; u < kSqPerWave; ++u) {
+    const int q = wave + 4 * u;
+    if (q < nt && key <= a.pos0 + t0 + q) a.S[((size_t)(t0 + q) * a.nq + h) * a.max_seq + key] = dot[u] * a.scale;
+  }
 }
 
 // Softmax and weighted V sum of query rows t0 .. t0 + kQt - 1 of head
@@ -1142,7 +1145,26 @@ __global__ __launch_bounds__(256) void attn_pv_qt_kernel(AttnArgs a) {
     for (int u = 0; u < PER; ++u) reinterpret_cast<float4*>(vt)[tid + 256 * u] = r[u];
     __syncthreads();
     const int np = min(kPvCh, n - c0);
-    for (int j = 0; j < np; ++j) {
+    int j = 0;
+    // 16 positions' operands read ahead of their chain steps
+    for (; j + 16 <= np; j += 16) {
+      float4 pe[4];
+      float vv[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pe[u] = *reinterpret_cast<const float4*>(er + c0 + j + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) vv[u] = vt[(j + u) * kPvDpb + dd];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float p0 = pe[u].x * vv[4 * u], p1 = pe[u].y * vv[4 * u + 1];
+        const float p2 = pe[u].z * vv[4 * u + 2], p3 = pe[u].w * vv[4 * u + 3];
+        out = out + p0;
+        out = out + p1;
+        out = out + p2;
+        out = out + p3;
+      }
+    }
+    for (; j < np; ++j) {
       const float pv = er[c0 + j] * vt[j * kPvDpb + dd];
       out = out + pv;
     }
@@ -1447,10 +1469,11 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   if (a.T > 4 && !a.fuse_heads && a.nkv > 0 && a.nq % a.nkv == 0 &&
       attn_pv_qt_lds(a.pos0, a.T) <= 160 * 1024 && !getenv("MOEHIP_ATTN_ROWWISE")) {
     const unsigned qg = (unsigned)((a.T + kQt - 1) / kQt);
-    const size_t lds_s = ((size_t)64 * (a.hd + 4) + (size_t)kQt * a.hd) * 4;
+    const size_t lds_s = ((size_t)64 * (a.hd + 4) + (size_t)kSq * a.hd) * 4;
     moe_status st;
     if ((st = set_lds(attn_scores_qt_kernel, lds_s, "scores LDS attribute"))) return st;
-    hipLaunchKernelGGL(attn_scores_qt_kernel, dim3((unsigned)((a.pos0 + a.T + 63) / 64), (unsigned)a.nq, qg),
+    hipLaunchKernelGGL(attn_scores_qt_kernel,
+                       dim3((unsigned)((a.pos0 + a.T + 63) / 64), (unsigned)a.nq, (unsigned)((a.T + kSq - 1) / kSq)),
                        dim3(256), lds_s, s, a);
     if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
     const size_t lds_p = attn_pv_qt_lds(a.pos0, a.T);
