@@ -199,16 +199,51 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs
 
 // ---------------------------------------------------------------- group
 
+// Exclusive prefix sum of v over the kGroupThreads threads of the block (a
+// shuffle scan per wave, then the wave totals); *total gets the sum.
+__device__ __forceinline__ int group_excl_scan(int v, int* wsum, int* total) {
+  constexpr int NW = kGroupThreads / kWave;
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) wsum[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int t = lane < NW ? wsum[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < NW; off <<= 1) {
+      const int y = __shfl_up(t, off, kWave);
+      if (lane >= off) t += y;
+    }
+    if (lane < NW) wsum[lane] = t;
+  }
+  __syncthreads();
+  *total = wsum[NW - 1];
+  const int base = w > 0 ? wsum[w - 1] : 0;
+  __syncthreads();   // wsum may be reused
+  return base + x - v;
+}
+
 // One block: count the pairs of each expert, exclusive prefix sum, then
 // scatter the pair ids.  The order of pairs within an expert does not
 // affect any result (every pair's outputs are computed independently).
+// Also the weight-stationary kernels' tasks, in expert order: expert e's
+// pairs in runs of at most kWsSplitPairs, {e | pairs << 16, first pair},
+// then {-1, 0} up to ntask_max; and their flags cleared.
 __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int* __restrict__ idx,
                                                               int npairs, int E,
                                                               int* __restrict__ ecount,
                                                               int* __restrict__ eoff,
-                                                              int* __restrict__ perm) {
+                                                              int* __restrict__ perm,
+                                                              int2* __restrict__ tasks,
+                                                              int ntask_max,
+                                                              int* __restrict__ wsflag) {
   __shared__ int cnt[kGroupThreads];
-  __shared__ int scan[kGroupThreads];
+  __shared__ int wsum[kGroupThreads / kWave];
   const int tid = threadIdx.x;
   cnt[tid] = 0;
   __syncthreads();
@@ -217,21 +252,27 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int* __restr
     if (e >= 0) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  // inclusive scan (Hillis-Steele) over the E <= 1024 counts
-  scan[tid] = cnt[tid];
-  __syncthreads();
-  for (int off = 1; off < kGroupThreads; off <<= 1) {
-    const int v = tid >= off ? scan[tid - off] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  const int start = scan[tid] - cnt[tid];
+  const int c = cnt[tid];   // zero past E
+  int total;
+  const int start = group_excl_scan(c, wsum, &total);
   if (tid < E) {
-    ecount[tid] = cnt[tid];
+    ecount[tid] = c;
     eoff[tid] = start;
+    if (wsflag) {
+      wsflag[tid] = 0;
+      wsflag[E + tid] = 0;
+    }
   }
-  __syncthreads();
+  if (tasks) {
+    const int nsplit = (c + kWsSplitPairs - 1) / kWsSplitPairs;
+    int ntasks;
+    const int t0 = group_excl_scan(nsplit, wsum, &ntasks);
+    for (int k = 0; k < nsplit; ++k) {
+      const int p0 = k * kWsSplitPairs, n = min(kWsSplitPairs, c - p0);
+      tasks[t0 + k] = make_int2(tid | (n << 16), start + p0);
+    }
+    for (int i = ntasks + tid; i < ntask_max; i += kGroupThreads) tasks[i] = make_int2(-1, 0);
+  }
   cnt[tid] = start;   // cursor
   __syncthreads();
   for (int q = tid; q < npairs; q += kGroupThreads) {
@@ -464,10 +505,11 @@ struct GateUpGArgs {
   uint8_t* htab; size_t htab_bytes;
   uint32_t* hpart;   // [pair][nseg][2]
   int nseg;
-  // weight-stationary kernel: flag[e] = 1 for experts left to this kernel;
-  // this kernel: when set, only those experts
+  // weight-stationary kernel: flag[e] = 1 for experts left to this kernel
+  // (cleared by group_kernel); this kernel: when set, only those experts
   int* flag = nullptr;
   const int* only_flagged = nullptr;
+  const int2* tasks = nullptr;  // weight-stationary kernel: its task per blockIdx.y (group_kernel)
 };
 
 // Pairs base .. base + n - 1 (n <= 16*NT) of a pass over expert e's pairs
@@ -656,6 +698,7 @@ struct DownGArgs {
   float* y;            // [pair][D]
   int* flag = nullptr;               // as in GateUpGArgs
   const int* only_flagged = nullptr;
+  const int2* tasks = nullptr;
 };
 
 template <bool Q4, int NL, int NT>
@@ -977,15 +1020,10 @@ __global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
   __shared__ WsPairs sp;
   __shared__ uint64_t exp_tab[32];
   uint8_t* lds = reinterpret_cast<uint8_t*>(lds_b);
-  const int e = blockIdx.y;
-  const int n_all = a.ecount[e];
-  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;   // records the flag
+  const int2 task = a.tasks[blockIdx.y];
+  if (task.x < 0) return;
+  const int e = task.x & 0xFFFF, n_all = task.x >> 16, first = task.y;
   if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
-  if (n_all == 0) {
-    if (rec) a.flag[e] = 0;
-    return;
-  }
-  const int first = a.eoff[e];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, g = lane / 16, j = lane % 16;
   WFrag w[2][1][KS];
   const uint8_t* mats[2] = {a.gq + (size_t)e * a.dff * a.rb, a.uq + (size_t)e * a.dff * a.rb};
@@ -1007,8 +1045,8 @@ __global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
       const uint8_t* tb = tab_of(q);
       return make_int2(act_nl(tb), (int)act_asum(tb));
     });
-    if (multi) {   // every block of the expert sees the same pairs
-      if (rec) a.flag[e] = 1;
+    if (multi) {   // every block of this split sees the same pairs
+      if (threadIdx.x == 0) a.flag[e] = 1;
       return;
     }
     auto epi = [&](const v4i (&acc)[2][1][NT], int i0, int nlive) {
@@ -1064,7 +1102,6 @@ __global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
     }
     __syncthreads();
   }
-  if (rec) a.flag[e] = 0;
 }
 
 constexpr int kWsDownRT = 2;                      // row tiles per wave (down)
@@ -1077,14 +1114,9 @@ __global__ __launch_bounds__(kWsThreads) void down_ws_kernel(DownGArgs a) {
   extern __shared__ u32x4 lds_b[];
   __shared__ WsPairs sp;
   uint8_t* lds = reinterpret_cast<uint8_t*>(lds_b);
-  const int e = blockIdx.y;
-  const int n_all = a.ecount[e];
-  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;
-  if (n_all == 0) {
-    if (rec) a.flag[e] = 0;
-    return;
-  }
-  const int first = a.eoff[e];
+  const int2 task = a.tasks[blockIdx.y];
+  if (task.x < 0) return;
+  const int e = task.x & 0xFFFF, n_all = task.x >> 16, first = task.y;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, g = lane / 16, j = lane % 16;
   WFrag w[1][RT][KS];
   const uint8_t* mats[1] = {a.dq + (size_t)e * a.D * a.rb};
@@ -1110,7 +1142,7 @@ __global__ __launch_bounds__(kWsThreads) void down_ws_kernel(DownGArgs a) {
       return make_int2(nl, (int)hs);
     });
     if (multi) {
-      if (rec) a.flag[e] = 1;
+      if (threadIdx.x == 0) a.flag[e] = 1;
       return;
     }
     auto epi = [&](const v4i (&acc)[1][RT][kWsDownNT], int i0, int nlive) {
@@ -1136,7 +1168,6 @@ __global__ __launch_bounds__(kWsThreads) void down_ws_kernel(DownGArgs a) {
     };
     ws_passes<Q4, 1, RT, KS, kWsDownNT, false>(w, n, sp, lds, tab_of, epi);
   }
-  if (rec) a.flag[e] = 0;
 }
 
 // ---------------------------------------------------------------- combine
@@ -1275,8 +1306,9 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
   // 4. group pairs by expert
   const int npairs = T * L->topk;
+  const int ntask_max = npairs / kWsSplitPairs + L->E + 1;
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
-                     L->ecount, L->eoff, L->perm);
+                     L->ecount, L->eoff, L->perm, L->tasks, ntask_max, L->wsflag);
   if ((st = check_hip(hipGetLastError(), "group launch"))) return st;
   // 5. gate/up + SwiGLU
   const int nseg = 2 * ((L->dff + kMmaRows - 1) / kMmaRows);   // h header segments of 64 rows
@@ -1293,8 +1325,11 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   const GroupedFn gu_ws = ws ? pick_ws(q4, true, L->D / cols) : nullptr;
   if (gu_ws) {
     ga.flag = L->wsflag;
-    if ((st = launch_grouped(gu_ws, gg, ga, ws_lds(1, L->D), s))) return st;
+    ga.tasks = L->tasks;
+    const dim3 ggw(gg.x, (unsigned)ntask_max);
+    if ((st = launch_grouped(gu_ws, ggw, ga, ws_lds(1, L->D), s))) return st;
     ga.flag = nullptr;
+    ga.tasks = nullptr;
     ga.only_flagged = L->wsflag;
   }
   if ((st = launch_grouped(gu_stream, gg, ga, kMmaLds, s))) return st;
@@ -1306,9 +1341,11 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   const GroupedFn dn_ws = ws ? pick_ws(q4, false, L->dff / cols) : nullptr;
   if (dn_ws) {
     da.flag = L->wsflag + L->E;
-    dim3 dgw((unsigned)((L->D + kWsDownRows - 1) / kWsDownRows), (unsigned)L->E);
+    da.tasks = L->tasks;
+    dim3 dgw((unsigned)((L->D + kWsDownRows - 1) / kWsDownRows), (unsigned)ntask_max);
     if ((st = launch_grouped(dn_ws, dgw, da, ws_lds(kWsDownNT, L->dff), s))) return st;
     da.flag = nullptr;
+    da.tasks = nullptr;
     da.only_flagged = L->wsflag + L->E;
   }
   dim3 dg((unsigned)((L->D + kMmaRows - 1) / kMmaRows), (unsigned)L->E);

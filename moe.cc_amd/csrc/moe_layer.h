@@ -11,6 +11,10 @@ namespace moe {
 
 constexpr int kMaxTopK = 32;
 
+// Pairs of one expert that one block of the weight-stationary grouped
+// kernels takes at most (an expert with more is split over several blocks).
+constexpr int kWsSplitPairs = 256;
+
 struct LayerDev {
   int dtype = 2, D = 0, dff = 0, E = 0, topk = 0;
   long long rbg = 0, rbd = 0;          // row bytes of gate/up and of down
@@ -38,6 +42,9 @@ struct LayerDev {
   int* eoff = nullptr;       // [E]
   int* perm = nullptr;       // [T*topk]
   int* wsflag = nullptr;     // [2][E] experts left to the streaming gate/up, down kernels
+  int2* tasks = nullptr;     // [T*topk/kWsSplitPairs + E + 1] tasks of the weight-stationary
+                             // kernels: {expert | pairs << 16, first pair in perm}, x = -1 past
+                             // the last
   float* y = nullptr;        // [T*topk][D]
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };

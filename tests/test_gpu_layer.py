@@ -204,6 +204,11 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     (3, 17, 64, 1024, 512, False, True, 40.0),   # 2-limb Q4 activations
     (2, 9, 64, 1024, 256, True, True, 400.0),    # 4-limb Q8 activations (and h)
     (3, 70, 8, 512, 256, False, True, 3000.0),   # 4-limb Q4, > 32 pairs per expert
+    # E = top-k: every expert takes every token, > 256 pairs each, so the
+    # weight-stationary kernels split each expert over several blocks
+    (3, 300, 8, 512, 256, False, True, 1.0),
+    (3, 520, 8, 256, 256, False, True, 40.0),    # split and flagged (2-limb Q4)
+    (2, 280, 8, 512, 256, True, True, 0.3),      # split, one-limb Q8
 ]
 
 
