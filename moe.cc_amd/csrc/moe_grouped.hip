@@ -1284,6 +1284,8 @@ bool grouped_ok(const LayerDev* L) {
          is16(L->router_w);
 }
 
+constexpr int kPackOverlapTokens = 1024;
+
 moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
                                  float* out, int32_t* idx_out, float* p_out) {
   hipStream_t s = stream();
@@ -1291,12 +1293,25 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   moe_status st;
   if (!is16(xn) || !is16(out) || (resid && !is16(resid)))
     return set_error(MOE_ERR_ARG, "grouped forward: arrays must be 16-byte aligned");
-  // 1. x tables
+  // 1. x tables; for many tokens on the side stream, where they overlap the
+  // router, the selection and the grouping and are joined before gate/up
+  // (the fork and join cost ~8 us: more than the packing saves below ~1024
+  // tokens, measured)
   QShape sh;
   sh.dtype = L->dtype; sh.M = T; sh.N = 1; sh.K = L->D; sh.lda = L->D; sh.ldc = 1;
   sh.rs = L->rbg;
   QJob one{nullptr, nullptr, xn, nullptr};
-  if ((st = check_hip(launch_act_pack(sh, nullptr, one, 1, L->xtab, s), "act pack"))) return st;
+  const bool overlap = T >= kPackOverlapTokens;
+  if (overlap) {
+    hipStream_t s2 = side_stream();
+    if ((st = check_hip(hipEventRecord(fork_event(), s), "fork record")) ||
+        (st = check_hip(hipStreamWaitEvent(s2, fork_event(), 0), "fork wait")) ||
+        (st = check_hip(launch_act_pack(sh, nullptr, one, 1, L->xtab, s2), "act pack")) ||
+        (st = check_hip(hipEventRecord(join_event(), s2), "join record")))
+      return st;
+  } else if ((st = check_hip(launch_act_pack(sh, nullptr, one, 1, L->xtab, s), "act pack"))) {
+    return st;
+  }
   // 2. router logits
   RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E};
   if (T >= 512) st = launch_router_tile<2, 2, 64>(ra, s);
@@ -1310,6 +1325,7 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
                      L->ecount, L->eoff, L->perm, L->tasks, ntask_max, L->wsflag);
   if ((st = check_hip(hipGetLastError(), "group launch"))) return st;
+  if (overlap && (st = check_hip(hipStreamWaitEvent(s, join_event(), 0), "join wait"))) return st;
   // 5. gate/up + SwiGLU
   const int nseg = 2 * ((L->dff + kMmaRows - 1) / kMmaRows);   // h header segments of 64 rows
   GateUpGArgs ga{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk,
