@@ -1050,13 +1050,13 @@ __global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
       return;
     }
     auto epi = [&](const v4i (&acc)[2][1][NT], int i0, int nlive) {
-      if (j >= nlive || !live_rows) return;
-      const int i = i0 + j;
+      const int i = i0 + (j < nlive ? j : 0);
+      int nl = 1;
+      uint32_t hs = 0;
+      if (j < nlive && live_rows) {
       const int q = sp.pair[i];
       const uint32_t xs = sp.asum[i];
       uint8_t* tabq = a.htab + (size_t)q * a.htab_bytes;
-      int nl = 1;
-      uint32_t hs = 0;
       uint32_t bytes[4][4];   // [limb][r]
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1085,8 +1085,19 @@ __global__ __launch_bounds__(kWsThreads) void gate_up_ws_kernel(GateUpGArgs a) {
               (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
         }
       }
-      atomicMax(&sp.red_nl[i], nl);
-      atomicAdd(&sp.red_sum[i], hs);
+      }
+      // the pair's four row groups (lanes j, j + 16, j + 32, j + 48) combine
+      // first: one LDS atomic pair per wave and pair
+#pragma unroll
+      for (int off = 16; off < kWave; off <<= 1) {
+        const int o = __shfl_xor(nl, off, kWave);
+        nl = o > nl ? o : nl;
+        hs += (uint32_t)__shfl_xor((int)hs, off, kWave);
+      }
+      if (g == 0 && j < nlive) {
+        atomicMax(&sp.red_nl[i], nl);
+        atomicAdd(&sp.red_sum[i], hs);
+      }
     };
     ws_passes<Q4, 2, 1, KS, NT, true>(w, n, sp, lds, tab_of, epi);
     // this block's two 64-row segments of each pair's h header (the first

@@ -90,8 +90,7 @@ struct GateUpArgs {
 template <bool Q4, class G>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   extern __shared__ float hb[];   // [rows_per_block]
-  __shared__ int red_nl;
-  __shared__ unsigned red_sum;
+  __shared__ int red[2];   // limb count, activation sum
   const int q = blockIdx.y;
   const int e = a.idx[q];
   if (e < 0) return;
@@ -103,7 +102,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   const float* xs[1] = {a.xn + (size_t)t * a.D};
   GateUpEpiMaker mk{GateUpEpi{a.gs + (size_t)e * a.dff, a.us + (size_t)e * a.dff, hb, r0,
                               Q4 ? 7.0f : 127.0f}};
-  if (threadIdx.x == 0) { red_nl = 1; red_sum = 0; }
+  if (threadIdx.x == 0) { red[0] = 1; red[1] = 0; }
   if constexpr (std::is_same<G, GenericGeom>::value) {
     auto epi = mk.e;
     generic_rows_fp32<Q4, 2>(W, a.rb, a.D, xs[0], r0, r1, epi);
@@ -116,13 +115,12 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   uint32_t sum;
   pack_act_cols<Q4>(hb - r0, a.dff, r0, r1, a.htab + (size_t)q * a.htab_bytes, threadIdx.x,
                     blockDim.x, nl, sum);
-  atomicMax(&red_nl, nl);
-  atomicAdd(&red_sum, sum);
+  block_max_sum(nl, sum, red);
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + blockIdx.x) * 2;
-    pp[0] = (uint32_t)red_nl;
-    pp[1] = red_sum;
+    pp[0] = (uint32_t)red[0];
+    pp[1] = (uint32_t)red[1];
   }
 }
 

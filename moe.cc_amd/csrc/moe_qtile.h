@@ -39,8 +39,26 @@ __device__ __forceinline__ const uint32_t* act_plane(const uint8_t* tab, int K, 
   return reinterpret_cast<const uint32_t*>(tab + 16 + (size_t)l * (((size_t)K + 15) / 16) * 16);
 }
 
-// Packs one activation row into its table.  Called by a whole block (any
-// size); contains barriers.  `scratch` is 2 ints of LDS.
+// Block-wide max of nl and sum of part into scratch[0] / scratch[1] (LDS,
+// set to {1, 0} by the caller before a barrier): each wave reduces across
+// its lanes first, then one LDS atomic pair per wave (hundreds of atomics on
+// one address serialise: ~3 us for a 256-thread block, measured).  Whole
+// waves only.
+__device__ __forceinline__ void block_max_sum(int nl, uint32_t part, int* scratch) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int o = __shfl_xor(nl, off, kWave);
+    nl = o > nl ? o : nl;
+    part += (uint32_t)__shfl_xor((int)part, off, kWave);
+  }
+  if (threadIdx.x % kWave == 0) {
+    atomicMax(&scratch[0], nl);
+    atomicAdd(reinterpret_cast<unsigned*>(&scratch[1]), part);
+  }
+}
+
+// Packs one activation row into its table.  Called by a whole block (whole
+// waves); contains barriers.  `scratch` is 2 ints of LDS.
 template <bool Q4>
 __device__ void pack_act_row(const float* __restrict__ x, int K, uint8_t* __restrict__ tab,
                              int* scratch) {
@@ -76,8 +94,7 @@ __device__ void pack_act_row(const float* __restrict__ x, int K, uint8_t* __rest
       }
     }
   }
-  atomicMax(&scratch[0], nl);
-  atomicAdd(reinterpret_cast<unsigned*>(&scratch[1]), part);
+  block_max_sum(nl, part, scratch);
   __syncthreads();
   if (threadIdx.x == 0) {
     reinterpret_cast<int*>(tab)[0] = scratch[0];
