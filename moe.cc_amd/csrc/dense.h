@@ -47,6 +47,10 @@ struct DenseArgs {
   float* sel_p = nullptr;
   int32_t* sel_idx_user = nullptr;
   float* sel_p_user = nullptr;
+  // With the fused selection, only where dense_row_path(a) holds: the row
+  // kernel runs alone, and the caller's next kernel reads C and pack_part
+  // and does the selection and the tables' headers itself.
+  int sel_defer = 0;
   // Optional, one token (dense_amax_ok): each block of dense_amax_rows(N)
   // consecutive outputs also writes its largest value (NaN if it has one)
   // to amax_part[block], for greedy_vec.
@@ -59,6 +63,9 @@ int dense_amax_rows(int N);
 bool dense_norm_ok(int M, int K);
 // Whether dense_matmul can fuse the expert selection (M tokens, N experts).
 bool dense_select_ok(int M, int N);
+// Whether dense_matmul runs `a` with the one-token row kernel (one block
+// per output row; with packing, pack_part then holds N partial headers).
+bool dense_row_path(const DenseArgs& a);
 
 // x[t] = emb[ids[t]] (ids clamped to [0, V)), T rows of D floats.
 moe_status embed_rows(const int32_t* ids, int T, const float* emb, int V, int D, float* x,

@@ -1376,6 +1376,12 @@ bool dense_row_ok(const DenseArgs& a, bool vec) {
   return a.M == 1 && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
 }
 
+bool dense_row_path(const DenseArgs& a) {
+  const bool vec = a.K > 0 && a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) &&
+                   al16(a.W);
+  return a.N > 0 && dense_row_ok(a, vec) && (!a.norm || dense_norm_ok(a.M, a.K));
+}
+
 template <bool NORM, int PACK>
 moe_status launch_row(const DenseArgs& a, hipStream_t s) {
   const size_t lds = (size_t)2 * a.K * 4;
@@ -1383,7 +1389,7 @@ moe_status launch_row(const DenseArgs& a, hipStream_t s) {
   if (st) return st;
   hipLaunchKernelGGL((dense_row_kernel<NORM, PACK>), dim3((unsigned)a.N), dim3(kRowThreads), lds, s, a);
   if ((st = check_hip(hipGetLastError(), "dense row launch"))) return st;
-  if (!a.sel_counter) return MOE_OK;
+  if (!a.sel_counter || a.sel_defer) return MOE_OK;
   hipLaunchKernelGGL(row_finish_kernel, dim3(1), dim3(kWave), 0, s, a);
   return check_hip(hipGetLastError(), "row finish launch");
 }
@@ -1400,6 +1406,8 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
                         a.ldc != a.N))
     return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs M <= 4, N <= 1024");
   if (a.K <= 0) return set_error(MOE_ERR_ARG, "dense matmul: K = %d", a.K);
+  if (a.sel_defer && (!a.sel_counter || !dense_row_path(a)))
+    return set_error(MOE_ERR_ARG, "dense matmul: a deferred selection needs the row kernel");
   const bool vec = a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) && al16(a.W);
   if (a.norm) {
     if (!vec || !dense_norm_ok(a.M, a.K))

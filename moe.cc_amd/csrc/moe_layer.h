@@ -36,6 +36,8 @@ struct LayerDev {
   float* h = nullptr;        // [T*topk][dff] (decode kernels)
   float* xn = nullptr;       // [T][D] normed input (block forward)
   uint32_t* hpart = nullptr; // [T*topk][h segments][2] partial headers of the h tables
+  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables (fused
+                             // rmsnorm + router)
   // grouped kernels: pairs per expert, first pair of each expert in `perm`,
   // pair ids (t * topk + j) grouped by expert, expert outputs per pair
   int* ecount = nullptr;     // [E]
@@ -73,6 +75,35 @@ __device__ __forceinline__ uint64_t topk_key(float v, int i) {
     k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   }
   return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+// The gates of one token's K slots (sidx / sval in LDS, empty slots -1 /
+// -inf): p_i = expf(v_i - max) / (sum + 1e-9f), max over the slots in order
+// (a larger value replaces it), sum in slot order (test_model_trace.c:
+// 482-487); slot i to idx[i] / p[i] and the caller's copies (may be null).
+// One wave; sexp is its LDS scratch of K floats.
+__device__ __forceinline__ void select_gates(int K, const int* sidx, const float* sval, float* sexp,
+                                             int* idx, float* p, int* idx_user, float* p_user) {
+  const int lane = threadIdx.x % kWave;
+  if (lane < K) {
+    float mx = sval[0];
+    for (int i = 1; i < K; ++i) if (sval[i] > mx) mx = sval[i];
+    sexp[lane] = expf_glibc(sval[lane] - mx);
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  float sum = 0.0f;
+  for (int i = 0; i < K; ++i) sum = sum + sexp[i];
+  const float inv = 1.0f / (sum + 1e-9f);
+  if (lane < K) {
+    const float pv = sexp[lane] * inv;
+    idx[lane] = sidx[lane];
+    p[lane] = pv;
+    if (idx_user) idx_user[lane] = sidx[lane];
+    if (p_user) p_user[lane] = pv;
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
 }
 
 // One wave selects the experts of one token: every lane ranks its
@@ -131,25 +162,51 @@ __device__ void select_token(const float* __restrict__ logit_row, int E, int K, 
   }
   __threadfence_block();
   __builtin_amdgcn_wave_barrier();
-  if (lane < K) {
-    float mx = sval[0];
-    for (int i = 1; i < K; ++i) if (sval[i] > mx) mx = sval[i];
-    sexp[lane] = expf_glibc(sval[lane] - mx);
+  select_gates(K, sidx, sval, sexp, idx, p, idx_user, p_user);
+}
+
+// The slots of one token's selection, by a whole block of NT threads
+// (E <= NT, whole waves; contains barriers): the same rank rule as
+// select_token (rank = keys above the candidate's; a live candidate with
+// rank < K takes slot `rank`, slots left over keep -1 / -inf), the key range
+// split into NT / E' parts (E' = E rounded up to a power of two, at most 4
+// parts) whose partial ranks add.  v: this thread's logit (candidate
+// threadIdx.x, when < E; read by the caller, so that its load can be issued
+// early).  keys: LDS scratch of E uint64 (16-byte aligned); part: NT ints.
+template <int NT>
+__device__ void block_select_slots(float v, int E, int K, uint64_t* keys, int* part, int* sidx,
+                                   float* sval) {
+  const int tid = threadIdx.x;
+  if (tid < E) keys[tid] = topk_key(v, tid);
+  if (tid < K) { sidx[tid] = -1; sval[tid] = -__builtin_inff(); }
+  __syncthreads();
+  int ep = 1;
+  while (ep < E) ep *= 2;
+  const int np = NT / ep < 4 ? NT / ep : 4;
+  const int c = tid % ep, pi = tid / ep;
+  if (pi < np && c < E) {
+    const uint64_t kc = keys[c];
+    const int span = (E + np - 1) / np;
+    const int j0 = pi * span, j1 = j0 + span < E ? j0 + span : E;
+    int rank = 0;
+    int j = j0;
+    for (; j + 2 <= j1 && (j & 1) == 0; j += 2) {
+      const ulonglong2 w = reinterpret_cast<const ulonglong2*>(keys)[j / 2];
+      rank += (int)(w.x > kc) + (int)(w.y > kc);
+    }
+    for (; j < j1; ++j) rank += (int)(keys[j] > kc);
+    part[tid] = rank;
   }
-  __threadfence_block();
-  __builtin_amdgcn_wave_barrier();
-  float sum = 0.0f;
-  for (int i = 0; i < K; ++i) sum = sum + sexp[i];
-  const float inv = 1.0f / (sum + 1e-9f);
-  if (lane < K) {
-    const float pv = sexp[lane] * inv;
-    idx[lane] = sidx[lane];
-    p[lane] = pv;
-    if (idx_user) idx_user[lane] = sidx[lane];
-    if (p_user) p_user[lane] = pv;
+  __syncthreads();
+  if (tid < E) {
+    int rank = 0;
+    for (int q = 0; q < np; ++q) rank += part[tid + q * ep];
+    if (v > -__builtin_inff() && rank < K) {
+      sidx[rank] = tid;
+      sval[rank] = v;
+    }
   }
-  __threadfence_block();
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
 }
 
 // select_token with the candidates-per-lane count chosen for E (<= 1024).

@@ -80,6 +80,16 @@ struct GateUpArgs {
   float* h; uint8_t* htab; size_t htab_bytes;
   uint32_t* hpart;      // [pair][chunk][2] partial (limbs, sum) of each row chunk of h
   int nchunks, rows_per_block;
+  // SEL (one token, E <= kTileBlock): the selection is made here, from the
+  // router logits and the x table's nxpart partial headers; p and the
+  // caller's copies (may be null) get the gates
+  const float* logits = nullptr;
+  const uint32_t* xpart = nullptr;
+  int nxpart = 0, E = 0;
+  int* idx_w = nullptr;
+  float* p = nullptr;
+  int32_t* idx_user = nullptr;
+  float* p_user = nullptr;
 };
 
 // gate/up + SwiGLU for one (token, rank) pair and one row chunk:
@@ -87,12 +97,51 @@ struct GateUpArgs {
 // fp32 and, packed, into its rows of the pair's table for the down GEMV; the
 // chunk's limb count and activation sum go to hpart (no atomics).  Row chunks
 // start at multiples of 8, so a chunk owns whole packed dwords.
-template <bool Q4, class G>
+// SEL (decode, one token): every block ranks the token's E logits itself
+// (block_select_slots) and takes the expert of its slot; it also reduces the
+// router blocks' partial headers of the x table (the largest limb count, the
+// wrapping sum), so no kernel runs between the router and this one.  Block
+// (0, 0) writes the selection and gates (select_gates) and the x table's
+// header.
+template <bool Q4, class G, bool SEL>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   extern __shared__ float hb[];   // [rows_per_block]
   __shared__ int red[2];   // limb count, activation sum
   const int q = blockIdx.y;
-  const int e = a.idx[q];
+  int e;
+  int x_nl = 0;
+  uint32_t x_sum[1] = {0u};
+  if constexpr (SEL) {
+    __shared__ __align__(16) uint64_t keys[kTileBlock];
+    __shared__ int part[kTileBlock];
+    __shared__ int sidx[kMaxTopK];
+    __shared__ float sval[kMaxTopK], sexp[kMaxTopK];
+    __shared__ int xred[2];
+    const int tid = threadIdx.x;
+    // both loads first: the logits and the partial headers
+    const float v = tid < a.E ? a.logits[tid] : -__builtin_inff();
+    uint2 pp = make_uint2(1u, 0u);
+    if (tid < a.nxpart) pp = reinterpret_cast<const uint2*>(a.xpart)[tid];
+    if (tid == 0) { xred[0] = 1; xred[1] = 0; }
+    block_select_slots<kTileBlock>(v, a.E, a.topk, keys, part, sidx, sval);
+    block_max_sum((int)pp.x, pp.y, xred);
+    __syncthreads();
+    // (no partials: the table's header was written by its own pack kernel)
+    x_nl = a.nxpart > 0 ? xred[0] : 0;
+    x_sum[0] = (uint32_t)xred[1];
+    e = sidx[q];
+    if (blockIdx.x == 0 && q == 0) {
+      if (tid < kWave)
+        select_gates(a.topk, sidx, sval, sexp, a.idx_w, a.p, a.idx_user, a.p_user);
+      if (tid == 0 && a.nxpart > 0) {
+        uint32_t* hh = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(a.xtab));
+        hh[0] = (uint32_t)x_nl;
+        hh[1] = x_sum[0];
+      }
+    }
+  } else {
+    e = a.idx[q];
+  }
   if (e < 0) return;
   const int t = q / a.topk;
   const int r0 = blockIdx.x * a.rows_per_block;
@@ -107,7 +156,8 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     auto epi = mk.e;
     generic_rows_fp32<Q4, 2>(W, a.rb, a.D, xs[0], r0, r1, epi);
   } else {
-    stream_tokens<Q4, G, 2, 1>(W, a.rb, a.D, tabs, xs, 1, r0, r1, mk);
+    stream_tokens<Q4, G, 2, 1>(W, a.rb, a.D, tabs, xs, 1, r0, r1, mk, x_nl,
+                               x_nl > 0 ? x_sum : nullptr);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < r1 - r0; i += blockDim.x) a.h[(size_t)q * a.dff + r0 + i] = hb[i];
@@ -268,7 +318,7 @@ struct ScratchBuf {
   size_t bytes = 0;
 };
 struct SharedScratch {
-  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, ecount, eoff, perm, y, wsflag, tasks;
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, wsflag, tasks;
   unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
 };
 SharedScratch g_scratch;
@@ -301,7 +351,8 @@ moe_status ensure_scratch(LayerDev* L, int T) {
       (st = grow(S.xtab, (size_t)T * act_table_bytes(L->D), &synced)) ||
       (st = grow(S.htab, np * act_table_bytes(L->dff), &synced)) ||
       (st = grow(S.h, np * L->dff * 4, &synced)) || (st = grow(S.xn, (size_t)T * L->D * 4, &synced)) ||
-      (st = grow(S.hpart, np * (size_t)((L->dff + 7) / 8) * 8, &synced)))
+      (st = grow(S.hpart, np * (size_t)((L->dff + 7) / 8) * 8, &synced)) ||
+      (st = grow(S.xpart, (size_t)std::min(T, 4) * (L->E + 16) * 8, &synced)))
     return st;
   if (grouped_ok(L) &&
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
@@ -311,7 +362,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
     return st;
   L->logits = (float*)S.logits.p; L->idx = (int*)S.idx.p; L->p = (float*)S.p.p;
   L->xtab = (uint8_t*)S.xtab.p; L->htab = (uint8_t*)S.htab.p; L->h = (float*)S.h.p;
-  L->xn = (float*)S.xn.p; L->hpart = (uint32_t*)S.hpart.p;
+  L->xn = (float*)S.xn.p; L->hpart = (uint32_t*)S.hpart.p; L->xpart = (uint32_t*)S.xpart.p;
   L->ecount = (int*)S.ecount.p; L->eoff = (int*)S.eoff.p; L->perm = (int*)S.perm.p;
   L->wsflag = (int*)S.wsflag.p; L->tasks = (int2*)S.tasks.p;
   if (!S.sel_counter) {
@@ -336,7 +387,9 @@ int gateup_target_blocks() { static const int v = env_int("MOEHIP_GATEUP_BLOCKS"
 int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 512); return v; }
 
 template <bool Q4, class G>
-void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s) {
+void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s,
+                    bool sel = false, int nxpart = 0, int32_t* idx_out = nullptr,
+                    float* p_out = nullptr) {
   // rows per block: a multiple of both the wave-group unit and 8 (whole
   // packed dwords of h), sized for ~1024 blocks
   constexpr int unit0 = kTileWaves * G::WR;
@@ -353,7 +406,13 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
                L->xtab, act_table_bytes(L->D), xn, L->h, L->htab, act_table_bytes(L->dff),
                L->hpart, nc, (int)rpb};
   dim3 grid((unsigned)nc, (unsigned)npairs);
-  hipLaunchKernelGGL((gate_up_kernel<Q4, G>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+  if (sel) {
+    a.logits = L->logits; a.xpart = L->xpart; a.nxpart = nxpart; a.E = L->E;
+    a.idx_w = L->idx; a.p = L->p; a.idx_user = idx_out; a.p_user = p_out;
+    hipLaunchKernelGGL((gate_up_kernel<Q4, G, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+  } else {
+    hipLaunchKernelGGL((gate_up_kernel<Q4, G, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+  }
 }
 
 template <bool Q4, class G>
@@ -424,7 +483,7 @@ moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const
   if (fuse_norm) {
     // rmsnorm + x tables + router logits in one launch
     ra.norm = 1; ra.norm_w = L->rms2_w; ra.eps = norm_eps;
-    ra.xn_out = L->xn; ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->hpart;
+    ra.xn_out = L->xn; ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
     xn = L->xn;
   } else {
     // x tables for the expert GEMVs
@@ -441,11 +500,16 @@ moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const
     ra.sel_counter = L->sel_counter; ra.sel_topk = L->topk;
     ra.sel_idx = L->idx; ra.sel_p = L->p; ra.sel_idx_user = idx_out; ra.sel_p_user = p_out;
   }
+  // one token through the row kernel: the gate/up blocks select themselves
+  static const bool sel_kernel = getenv("MOEHIP_SELECT_KERNEL") != nullptr;
+  const bool sel_gu = fuse_sel && T == 1 && L->E <= kTileBlock && dense_row_path(ra) && !sel_kernel;
+  ra.sel_defer = sel_gu ? 1 : 0;
   if ((st = dense_matmul(ra, s))) return st;
   if (!fuse_sel && (st = launch_select(L, T, idx_out, p_out, s))) return st;
+  const int nxpart = ra.pack_dtype ? L->E : 0;
   int nchunks = 0;
-  if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s); });
-  else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s); });
+  if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out); });
+  else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out); });
   if ((st = check_hip(hipGetLastError(), "gate_up launch"))) return st;
   if (q4) with_geom<true>(L->rbd, [&](auto g) { launch_down<true, decltype(g)>(L, T, nchunks, resid, out, s); });
   else with_geom<false>(L->rbd, [&](auto g) { launch_down<false, decltype(g)>(L, T, nchunks, resid, out, s); });

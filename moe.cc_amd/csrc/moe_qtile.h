@@ -376,14 +376,20 @@ __device__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K, 
 // fits in registers.  make_epi(t0) returns the epilogue for token slots
 // t0 .. t0+MTI-1 (an object with a templated operator()(row, tot)).
 // xs[t] are the fp32 activation rows, used only by the exact fallback.
+// nl_in > 0: the limb count of all tokens, and asum_in (per token, may be
+// null) their activation sums, given instead of read from the headers.
 template <bool Q4, class G, int NM, int MT, class MakeEpi>
 __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
                               const uint8_t* const* tabs, const float* const* xs, int ntok, int r0,
-                              int r1, MakeEpi& make_epi, int wv, int nwv) {
-  int nl = 1;
-  for (int t = 0; t < ntok; ++t) {
-    const int v = act_nl(tabs[t]);
-    nl = v > nl ? v : nl;
+                              int r1, MakeEpi& make_epi, int wv, int nwv, int nl_in = 0,
+                              const uint32_t* asum_in = nullptr) {
+  int nl = nl_in;
+  if (nl <= 0) {
+    nl = 1;
+    for (int t = 0; t < ntok; ++t) {
+      const int v = act_nl(tabs[t]);
+      nl = v > nl ? v : nl;
+    }
   }
   auto run = [&](auto nl_tag) {
     constexpr int NL = decltype(nl_tag)::value;
@@ -399,8 +405,12 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
         const uint8_t* tb[MTI];
 #pragma unroll
         for (int t = 0; t < MTI; ++t) tb[t] = tabs[t0 + t < ntok ? t0 + t : ntok - 1];
+        uint32_t as[MTI];
+#pragma unroll
+        for (int t = 0; t < MTI; ++t) as[t] = asum_in ? asum_in[t0 + t < ntok ? t0 + t : ntok - 1] : 0u;
         auto epi = make_epi.template at<MTI>(t0);
-        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi, wv, nwv);
+        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi, wv, nwv,
+                                        asum_in ? as : nullptr);
       }
     }
   };
@@ -416,9 +426,11 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
 template <bool Q4, class G, int NM, int MT, class MakeEpi>
 __device__ __forceinline__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
                                               const uint8_t* const* tabs, const float* const* xs,
-                                              int ntok, int r0, int r1, MakeEpi& make_epi) {
+                                              int ntok, int r0, int r1, MakeEpi& make_epi,
+                                              int nl_in = 0, const uint32_t* asum_in = nullptr) {
   stream_tokens<Q4, G, NM, MT>(W, rs, K, tabs, xs, ntok, r0, r1, make_epi,
-                               (int)(threadIdx.x / kWave), (int)(blockDim.x / kWave));
+                               (int)(threadIdx.x / kWave), (int)(blockDim.x / kWave), nl_in,
+                               asum_in);
 }
 
 // One wave alone streams rows [r0, r1) for one activation row whose limb

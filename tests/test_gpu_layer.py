@@ -91,6 +91,12 @@ CASES = [  # dtype, T, E, D, d_ff, bias, resid
     (2, 37, 64, 1024, 512, True, True),
     (3, 9, 32, 512, 384, False, True),
     (2, 3, 16, 96, 64, False, True),     # generic (untiled) expert rows
+    # one token: the gate/up blocks rank the logits (E <= 256: 4, 2, 1 key
+    # parts; E a power of two or not); E > 256 keeps the selection kernel
+    (3, 1, 60, 512, 256, False, True),
+    (2, 1, 200, 512, 256, True, True),
+    (3, 1, 256, 512, 256, False, True),
+    (3, 1, 300, 512, 256, True, True),
 ]
 
 
@@ -113,9 +119,10 @@ def test_layer_vs_oracle(moehip, dtype, T, E, D, dff, bias, resid):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
-def test_router_ties_and_nan(moehip):
+@pytest.mark.parametrize("T", [3, 1])
+def test_router_ties_and_nan(moehip, T):
     """Equal logits keep the lower expert first; NaN logits are never chosen."""
-    dtype, T, E, D, dff = 2, 3, 32, 256, 128
+    dtype, E, D, dff = 2, 32, 256, 128
     ex = random_experts(dtype, E, D, dff, 99)
     rw = O.normal(E * D, 98, 0.0, 0.02).reshape(E, D)
     rw[5] = rw[17]          # experts 5 and 17 tie exactly
@@ -178,6 +185,26 @@ def test_rmsnorm_parallel_sum_paths(moehip):
     for rows in (finite[:1], finite[:3]):
         want = O.moe_block(O.rmsnorm(rows, rms2), rows, rw, None, ex)[0]
         np.testing.assert_array_equal(bits(layer.block_forward(rows)), bits(want))
+
+
+@pytest.mark.parametrize("dtype,E,bias", [(3, 60, False), (2, 200, True), (3, 300, False)])
+def test_block_forward_one_token(moehip, dtype, E, bias):
+    """One token through rmsnorm fused into the router: the x tables' headers
+    come from the router blocks' partials, reduced where the experts are
+    selected (inside the gate/up blocks for E <= 256, a kernel of its own
+    above)."""
+    D, dff = 512, 256
+    seed = 4100 + E
+    print("case", dtype, E, bias, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 1, 0.0, 0.02).reshape(E, D)
+    rb = O.normal(E, seed + 2, 0.0, 0.05) if bias else None
+    x = O.normal(D, seed + 4, 0.0, 1.0).reshape(1, D)
+    for wscale in (1.0, 40.0):   # one- and two-limb activations
+        rms2 = (O.normal(D, seed + 3, 1.0, 0.1) * wscale).astype(np.float32)
+        layer = make_layer(moehip, dtype, ex, rw, rb, rms2)
+        want = O.moe_block(O.rmsnorm(x, rms2), x, rw, rb, ex)[0]
+        np.testing.assert_array_equal(bits(layer.block_forward(x)), bits(want))
 
 
 def test_repeated_forward_and_growing_T(moehip):
