@@ -90,12 +90,11 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterTileArgs a) {
   const int t0 = blockIdx.y * RX, e0 = blockIdx.x * RW;
   const int D = a.D;
   const int nc = D / KC;
-  // this thread's 4 staging slots: source (float4 units) and LDS offsets
-  static_assert(NV == 4, "staging is written for 4 float4 per thread");
-  const float4* srcp[4];
-  int dst[4];
+  // this thread's staging slots: source (float4 units) and LDS offsets
+  const float4* srcp[NV];
+  int dst[NV];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
+  for (int v = 0; v < NV; ++v) {
     const int i = tid + 256 * v;
     const int row = i / V4, c4 = i % V4;
     const float* base = row < RX ? a.x + (size_t)min(t0 + row, a.T - 1) * D
@@ -103,20 +102,17 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterTileArgs a) {
     srcp[v] = reinterpret_cast<const float4*>(base) + c4;
     dst[v] = row * LD + 4 * c4;
   }
-  float4 r0, r1, r2, r3;
-#define ROUTER_LOAD(c)                                                         \
-  {                                                                            \
-    const size_t o_ = (size_t)(c) * V4;                                        \
-    r0 = srcp[0][o_]; r1 = srcp[1][o_]; r2 = srcp[2][o_]; r3 = srcp[3][o_];    \
-  }
-#define ROUTER_STORE(bsel)                                                     \
-  {                                                                            \
-    float* b_ = buf + (bsel) * R * LD;                                         \
-    *reinterpret_cast<float4*>(b_ + dst[0]) = r0;                              \
-    *reinterpret_cast<float4*>(b_ + dst[1]) = r1;                              \
-    *reinterpret_cast<float4*>(b_ + dst[2]) = r2;                              \
-    *reinterpret_cast<float4*>(b_ + dst[3]) = r3;                              \
-  }
+  float4 rg[NV];
+  auto load = [&](int c) {
+    const size_t o = (size_t)c * V4;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) rg[v] = srcp[v][o];
+  };
+  auto store = [&](int bsel) {
+    float* b = buf + bsel * R * LD;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) *reinterpret_cast<float4*>(b + dst[v]) = rg[v];
+  };
   float acc[CT][CE];
 #pragma unroll
   for (int i = 0; i < CT; ++i)
@@ -124,9 +120,9 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterTileArgs a) {
     for (int j = 0; j < CE; ++j) acc[i][j] = 0.0f;
   // loads and stores are unconditional (chunk index clamped; a store past
   // the last chunk fills the idle buffer) so `reg` stays in registers
-  ROUTER_LOAD(0)
-  ROUTER_STORE(0)
-  ROUTER_LOAD(min(1, nc - 1))
+  load(0);
+  store(0);
+  load(min(1, nc - 1));
   __syncthreads();
   for (int c = 0; c < nc; ++c) {
     const float* B = buf + (c & 1) * R * LD;
@@ -157,12 +153,10 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterTileArgs a) {
           acc[i][j] = s;
         }
     }
-    ROUTER_STORE((c + 1) & 1)
-    ROUTER_LOAD(min(c + 2, nc - 1))
+    store((c + 1) & 1);
+    load(min(c + 2, nc - 1));
     __syncthreads();
   }
-#undef ROUTER_LOAD
-#undef ROUTER_STORE
 #pragma unroll
   for (int i = 0; i < CT; ++i)
 #pragma unroll
@@ -1325,8 +1319,10 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   }
   // 2. router logits
   RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E};
-  if (T >= 512) st = launch_router_tile<2, 2, 64>(ra, s);
-  else st = launch_router_tile<1, 1, 128>(ra, s);
+  // one chain per lane at every T (2x2 chains per lane left three quarters
+  // of the SIMDs idle at T = 512 and were slower at 2048 too; 256-column
+  // chunks were no faster, measured)
+  st = launch_router_tile<1, 1, 128>(ra, s);
   if (st) return st;
   // 3. top-k and gates
   if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
