@@ -97,6 +97,10 @@ CASES = [  # dtype, T, E, D, d_ff, bias, resid
     (2, 1, 200, 512, 256, True, True),
     (3, 1, 256, 512, 256, False, True),
     (3, 1, 300, 512, 256, True, True),
+    # few tokens, 8 experts: every token takes all 8, so each expert's
+    # gate/up stream serves every token (up to 31 slots)
+    (3, 20, 8, 512, 256, False, True),
+    (2, 31, 8, 256, 128, True, True),
 ]
 
 
