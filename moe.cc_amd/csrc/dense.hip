@@ -1369,7 +1369,10 @@ bool dense_amax_ok(const DenseArgs& a) {
          al16(a.W) && !a.norm && !a.sel_counter;
 }
 
-int dense_amax_rows(int N) { return N >= 65536 ? 64 : 16; }
+// 16 rows a block also for the vocabulary head: each chunk then reads 1 KB
+// of every row (64-row blocks read 256 B pieces), measured ~0.4% faster per
+// decode token even though the greedy choice then reads 4x the block maxima.
+int dense_amax_rows(int) { return 16; }
 
 // One token against few rows: the row kernel.
 bool dense_row_ok(const DenseArgs& a, bool vec) {
@@ -1399,8 +1402,7 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (a.amax_part) {
     if (!dense_amax_ok(a))
       return set_error(MOE_ERR_ARG, "dense matmul: block maxima need one aligned row");
-    return dense_amax_rows(a.N) == 64 ? launch_gemv<64, false, 0, kNpWide>(a, s)
-                                      : launch_gemv<16, false, 0, kNpOne>(a, s);
+    return launch_gemv<16, false, 0, kNpOne>(a, s);
   }
   if (a.sel_counter && (!dense_select_ok(a.M, a.N) || a.sel_topk < 1 || a.sel_topk > kMaxTopK ||
                         a.ldc != a.N))
