@@ -1223,8 +1223,23 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(const float* __r
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const float* src = part ? part : v;
   const int ns = part ? (n + rows - 1) / rows : n;
+  // up to GR values a thread are loaded at once and kept in registers for
+  // both scans (a loop of dependent loads costs a round trip per value)
+  constexpr int GR = 12;
+  const bool in_regs = ns <= GR * kGreedyThreads;
+  float sv[GR];
   float mx = -__builtin_inff();
-  for (int i = tid; i < ns; i += kGreedyThreads) mx = nan_max(mx, src[i]);
+  if (in_regs) {
+#pragma unroll
+    for (int u = 0; u < GR; ++u) {
+      const int i = tid + kGreedyThreads * u;
+      sv[u] = i < ns ? src[i] : -__builtin_inff();
+    }
+#pragma unroll
+    for (int u = 0; u < GR; ++u) mx = nan_max(mx, sv[u]);
+  } else {
+    for (int i = tid; i < ns; i += kGreedyThreads) mx = nan_max(mx, src[i]);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = nan_max(mx, __shfl_xor(mx, off, kWave));
   if (lane == 0) fred[wave] = mx;
@@ -1234,8 +1249,18 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(const float* __r
   int ans = 0;
   if (m == m && m != __builtin_inff() && m != -__builtin_inff()) {
     int first = INT_MAX;
-    for (int i = tid; i < ns; i += kGreedyThreads)
-      if (expf_glibc(src[i] - m) == 1.0f) { first = i; break; }
+    if (in_regs) {
+#pragma unroll
+      for (int u = GR - 1; u >= 0; --u) {
+        // (d < -1e-6: e^d < 1 - 9.9e-7, 16 ulps under 1, so expf(d) < 1)
+        const int i = tid + kGreedyThreads * u;
+        const float d = sv[u] - m;
+        if (i < ns && !(d < -1e-6f) && expf_glibc(d) == 1.0f) first = i;
+      }
+    } else {
+      for (int i = tid; i < ns; i += kGreedyThreads)
+        if (expf_glibc(src[i] - m) == 1.0f) { first = i; break; }
+    }
     first = block_min(first, ired);
     if (part && first != INT_MAX) {
       const int lo = first * rows, hi = min(n, lo + rows);
