@@ -1319,10 +1319,12 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   }
   // 2. router logits
   RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E};
-  // one chain per lane at every T (2x2 chains per lane left three quarters
-  // of the SIMDs idle at T = 512 and were slower at 2048 too; 256-column
-  // chunks were no faster, measured)
-  st = launch_router_tile<1, 1, 128>(ra, s);
+  // one chain per lane below 2048 tokens (2x2 chains per lane left three
+  // quarters of the SIMDs idle at T = 512; 256-column chunks were no
+  // faster); from 2048 tokens two token chains per lane (512 blocks at E =
+  // 128, a third fewer LDS reads per product: T = 2048 layer 449 -> 437 us,
+  // no gain at 1024), measured
+  st = T >= 2048 ? launch_router_tile<2, 1, 128>(ra, s) : launch_router_tile<1, 1, 128>(ra, s);
   if (st) return st;
   // 3. top-k and gates
   if ((st = launch_select(L, T, idx_out, p_out, s))) return st;

@@ -240,6 +240,7 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     (3, 300, 8, 512, 256, False, True, 1.0),
     (3, 520, 8, 256, 256, False, True, 40.0),    # split and flagged (2-limb Q4)
     (2, 280, 8, 512, 256, True, True, 0.3),      # split, one-limb Q8
+    (3, 2048, 8, 256, 256, False, True, 1.0),    # router with two token chains per lane
 ]
 
 
