@@ -11,7 +11,11 @@ x ~ N(0, 1).  A step is one pass over a rotating pool of distinct matrices
 launch per shape, inputs resident in HBM.  `value` is algorithmic GB/s:
 weights + scales + x + y of every GEMV, each counted once.
 
-Other workloads: q8_gemv (configs[0], [768 x 2048]).
+The same line carries configs[0] (`q8_gemv`: Q8 rowwise GEMV [768 x 2048],
+its own roofline and CPU baseline), configs[2] (`moe_decode_q8`), configs[3]
+(`moe_prefill_q4`) and configs[4] (`model_decode_q4`), each with the
+reference's CPU path timed on this host beside it.  --workload q8_gemv makes
+the Q8 GEMV the headline instead.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -125,7 +129,7 @@ def cpu_baseline(shapes, budget_s: float):
     return {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
             "sample": f"{calls} batch-1 GEMVs over {pool} matrices per shape "
                       f"{[f'{N}x{K}' for _, N, K in shapes]}, {tot_s:.1f} s, 1 thread of "
-                      f"{os.cpu_count()} host cores"}
+                      f"{host_cores()} host cores"}
 
 
 COPY_CALIB_BYTES = 256 << 20
@@ -154,6 +158,14 @@ def measured_traffic(kernel_name):
         return t["kernels"].get(kernel_name, {}).get("traffic_bytes_per_launch")
     except (OSError, ValueError, KeyError):
         return None
+
+
+def host_cores() -> int:
+    """Host threads this process may use (the box's share, not the machine's)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
 
 
 def run_gemv(args, dtype, shapes, workload):
@@ -268,6 +280,59 @@ class LayerPool:
             self.layers.append(M.MoeLayer(h.value, dtype, D, dff, E, 8))
         tmp.free()
         M.synchronize()
+
+
+def layer_cpu_baseline(dtype, T, runs, E=128, D=2048, dff=768, top_k=8, seed=9):
+    """One MoE layer at the config shape on one host thread: the reference's
+    own layer_forward_f32 MoE block (oracle/_ref, compiled from the
+    reference sources: router, top-8, softmax, the per-(token, rank) GEMV
+    loop, weighted sum, residual; its attention part is given zero weights
+    and a 2-wide head and costs nothing) when that library is present, else
+    the oracle's restatement of the same loops.  One warm-up run, then the
+    median of `runs`.  The weights are random bytes with constant scales:
+    the CPU loops' time does not depend on their values."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    rng = np.random.default_rng(seed)
+    rb_g = D if dtype == 2 else D // 2
+    rb_d = dff if dtype == 2 else dff // 2
+    if dtype == 2:
+        q = lambda *sh: rng.integers(-127, 128, sh, dtype=np.int8)  # noqa: E731
+    else:
+        q = lambda *sh: rng.integers(0, 256, sh, dtype=np.uint8)  # noqa: E731
+    ex = O.ExpertSet(dtype, q(E, dff, rb_g), np.full((E, dff), 1e-3, np.float32),
+                     q(E, dff, rb_g), np.full((E, dff), 1e-3, np.float32),
+                     q(E, D, rb_d), np.full((E, D), 1e-3, np.float32), D, dff)
+    rw = (rng.standard_normal((E, D), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal((T, D), dtype=np.float32)
+    ones = np.ones(D, np.float32)
+    kind = "reference" if O.ref_available() else "port"
+    out = np.empty((T, D), np.float32)
+
+    def once():
+        if kind == "reference":
+            xx = x.copy()
+            t0 = time.perf_counter()
+            O.ref_trace().ref_moe_layer(xx.ctypes.data, T, D, E, top_k, dff, ones.ctypes.data,
+                                        rw.ctypes.data, None, ctypes.addressof(ex.Wg),
+                                        ctypes.addressof(ex.Wu), ctypes.addressof(ex.Wd))
+            return time.perf_counter() - t0
+        t0 = time.perf_counter()
+        O.orc_single().orc_moe_block(x.ctypes.data, x.ctypes.data, T, D, E, top_k, dff,
+                                     rw.ctypes.data, None, ctypes.addressof(ex.Wg),
+                                     ctypes.addressof(ex.Wu), ctypes.addressof(ex.Wd),
+                                     out.ctypes.data, None, None, None)
+        return time.perf_counter() - t0
+
+    once()
+    ts = [once() for _ in range(runs)]
+    med = float(np.median(ts))
+    return {"us_per_layer_median": round(med * 1e6, 1), "tokens_per_s_one_layer": round(T / med, 2),
+            "unit": "us per layer", "cores": 1, "kind": kind,
+            "sample": f"1 warm-up + median of {runs} single-thread runs of one {E}-expert "
+                      f"{'Q8' if dtype == 2 else 'Q4'} layer at T={T} "
+                      f"({'compiled reference layer_forward_f32 MoE block' if kind == 'reference' else 'oracle restatement'}), "
+                      f"1 thread of {host_cores()} host cores"}
 
 
 def run_decode(dtype, Ts, n_layers, steps, warmup):
@@ -415,14 +480,19 @@ def run_model(args):
     return res
 
 
-def model_cpu_baseline(budget_s: float):
+def model_cpu_baseline(budget_s: float, threaded: bool = False):
     """The oracle's KV-cached restatement (oracle/model_oracle.c, the
     reference's loops) on one host thread: one full-size layer's decode
     step at context 512 and the 151936-row head, timed separately and
     combined as 48 layers + head per token (the full model does not fit a
-    bounded CPU sample)."""
+    bounded CPU sample).  threaded: the same sources built with -fopenmp
+    (liboracle_omp.so), output rows, heads and tokens split over all the
+    host threads, each row in the reference's order (bit-identical to the
+    single-thread build)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    lib = O.orc_omp() if threaded else O.orc_single()
+    threads = lib.orc_threads()
     c = QWEN3_30B_A3B
     D, hd, nq, nkv, dff, E, V = c["D"], c["hd"], c["nq"], c["nkv"], c["dff"], c["E"], c["V"]
     rng = np.random.default_rng(7)
@@ -460,21 +530,24 @@ def model_cpu_baseline(budget_s: float):
     while t_layer < budget_s * 0.6:
         xx = x.copy()
         t0 = time.perf_counter()
-        O.orc().orc_layer_rows(ctypes.byref(cfg), ctypes.byref(layer), xx.ctypes.data, 1, ctx,
-                               kc.ctypes.data, vc.ctypes.data, max_seq)
+        lib.orc_layer_rows(ctypes.byref(cfg), ctypes.byref(layer), xx.ctypes.data, 1, ctx,
+                           kc.ctypes.data, vc.ctypes.data, max_seq)
         t_layer += time.perf_counter() - t0
         n_layer += 1
     head = w(V, D)
     out = np.empty((1, V), np.float32)
     t0 = time.perf_counter()
-    O.orc().orc_matmul_f32(x.ctypes.data, head.ctypes.data, out.ctypes.data, 1, V, D)
+    lib.orc_matmul_f32(x.ctypes.data, head.ctypes.data, out.ctypes.data, 1, V, D)
     t_head = time.perf_counter() - t0
     per_token = c["L"] * t_layer / n_layer + t_head
-    return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+    how = (f"{threads} threads (-fopenmp build, rows split over threads)" if threaded
+           else "1 thread")
+    return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
             "sample": f"{n_layer} decode steps of one full-size layer at context {ctx} "
                       f"({t_layer / n_layer * 1e3:.1f} ms each) and one lm_head product "
-                      f"({t_head * 1e3:.1f} ms), per token = 48 layers + head, 1 thread of "
-                      f"{os.cpu_count()} host cores"}
+                      f"({t_head * 1e3:.1f} ms), per token = 48 layers + head, {how} of "
+                      f"{host_cores()} host cores"}
 
 
 def main():
@@ -484,7 +557,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="q4_gemv", choices=["q4_gemv", "q8_gemv"])
     ap.add_argument("--pool-gib", type=float, default=1.0)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-layer-runs", type=int, default=5,
+                    help="timed runs (after one warm-up) of each single-thread layer baseline")
+    ap.add_argument("--cpu-prefill", default="128",
+                    help="prefill T values that get a CPU baseline ('' for none)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode", default="1,4,16",
                     help="also time one Q8 MoE decode layer at these T (configs[2]); '' to skip")
@@ -500,24 +577,40 @@ def main():
               "(multi-GPU sharding is a design note, not implemented); use --gpus 1",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "q4_gemv":
-        out = run_gemv(args, 3, [(2048, 768), (768, 2048)],
-                       "q4_rowwise_gemv_batch1 down[2048x768]+gate[768x2048] (BASELINE configs[1])")
-    else:
-        out = run_gemv(args, 2, [(768, 2048)],
-                       "q8_rowwise_gemv_batch1 gate[768x2048] (BASELINE configs[0])")
+    q4_args = (3, [(2048, 768), (768, 2048)],
+               "q4_rowwise_gemv_batch1 down[2048x768]+gate[768x2048] (BASELINE configs[1])")
+    q8_args = (2, [(768, 2048)], "q8_rowwise_gemv_batch1 gate[768x2048] (BASELINE configs[0])")
+    head, other = (q4_args, q8_args) if args.workload == "q4_gemv" else (q8_args, q4_args)
+    out = run_gemv(args, *head)
+    sub = run_gemv(args, *other)
+    out["q8_gemv" if other is q8_args else "q4_gemv"] = {
+        k: sub[k] for k in ("value", "unit", "ms_per_step", "config", "pct_hbm_peak", "roofline",
+                            "kernels", "cpu_baseline") if k in sub}
     if args.decode:
         Ts = [int(t) for t in args.decode.split(",") if t]
         out["moe_decode_q8"] = run_decode(2, Ts, args.decode_layers, max(args.steps, 20),
                                           args.warmup)
+        if not args.no_cpu:
+            for r in out["moe_decode_q8"]:
+                log(f"[bench] decode layer cpu baseline T={r['T']} ...")
+                r["cpu_baseline"] = layer_cpu_baseline(2, r["T"], args.cpu_layer_runs)
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
         out["moe_prefill_q4"] = run_prefill(3, Ts, args.decode_layers, 10, 2)
+        cpu_T = {int(t) for t in args.cpu_prefill.split(",") if t}
+        if not args.no_cpu:
+            for r in out["moe_prefill_q4"]:
+                if r["T"] in cpu_T:
+                    log(f"[bench] prefill layer cpu baseline T={r['T']} ...")
+                    r["cpu_baseline"] = layer_cpu_baseline(3, r["T"], args.cpu_layer_runs)
     if args.model_steps > 0:
         out["model_decode_q4"] = run_model(args)
         if not args.no_cpu:
-            log("[bench] model cpu baseline ...")
+            log("[bench] model cpu baseline (1 thread) ...")
             out["model_decode_q4"]["cpu_baseline"] = model_cpu_baseline(args.cpu_seconds)
+            log("[bench] model cpu baseline (all cores) ...")
+            out["model_decode_q4"]["cpu_baseline_all_cores"] = model_cpu_baseline(
+                args.cpu_seconds / 2, threaded=True)
     print(json.dumps(out), flush=True)
 
 

@@ -261,6 +261,12 @@ moe_status moe_model_create(const QwenConfig* cfg, const QwenWeights* w, int max
  * then moe_model_create.  Replaces bin_load + load_all_weights + the
  * reference's per-call host loops. */
 moe_status moe_model_load_file(const char* path, int max_seq, moe_model** out);
+/* The host half of moe_model_load_file, with no GPU call: reads a QW3W
+ * file's index (io.c:193-285), infers the config as load_all_weights does
+ * (model.h:110-163) and checks that every tensor the model binds has the
+ * dtype, rank and size that config implies.  cfg (and *expert_dtype, 2 or 3,
+ * if not NULL) receive the result.  MOE_ERR_ARG names the first bad tensor. */
+moe_status moe_model_inspect_file(const char* path, QwenConfig* cfg, int* expert_dtype);
 /* A synthetic model generated on the device: every weight ~ N(0, std^2)
  * (counter-based, seeded), norm weights 1, experts quantized with the
  * exporter's rule (export.py:23-36), no biases; lm_head untied if

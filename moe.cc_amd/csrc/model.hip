@@ -19,6 +19,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <initializer_list>
 #include <mutex>
 #include <new>
 #include <string>
@@ -331,15 +332,23 @@ moe_status bin_open(const char* path, BinIndex* b) {
     off += 8;
     if (e.dtype < 0 || e.dtype > 3 || nd > 8 || off + 4 * (size_t)nd > b->size)
       return set_error(MOE_ERR_ARG, "load: bad entry %s in %s", name.c_str(), path);
+    // every dimension positive and within int; the element count may not
+    // exceed what is left of the file (checked before each multiply, so the
+    // product cannot wrap)
     size_t elems = 1;
     for (uint32_t d = 0; d < nd; ++d) {
-      e.shape.push_back((int)u32(off));
-      elems *= (size_t)e.shape.back();
+      const uint32_t dim = u32(off);
       off += 4;
+      if (dim == 0 || dim > 0x7fffffffu)
+        return set_error(MOE_ERR_ARG, "load: %s has dimension %u", name.c_str(), dim);
+      if (elems > (b->size - off) / dim)
+        return set_error(MOE_ERR_ARG, "load: truncated %s", name.c_str());
+      elems *= dim;
+      e.shape.push_back((int)dim);
     }
     const size_t bpe = e.dtype == 0 ? 4 : (e.dtype == 1 ? 2 : 1);
+    if (elems > (b->size - off) / bpe) return set_error(MOE_ERR_ARG, "load: truncated %s", name.c_str());
     e.bytes = elems * bpe;
-    if (off + e.bytes > b->size) return set_error(MOE_ERR_ARG, "load: truncated %s", name.c_str());
     e.data = p + off;
     off += e.bytes;
     b->idx[name] = std::move(e);
@@ -353,6 +362,145 @@ const float* f32_of(const Entry* e, std::vector<std::vector<float>>& keep) {
   keep.emplace_back(e->bytes / 4);
   memcpy(keep.back().data(), e->data, e->bytes);
   return keep.back().data();
+}
+
+// True if e has dtype `dt` and exactly the dimensions `dims`.
+bool has_shape(const Entry* e, int dt, std::initializer_list<long long> dims) {
+  if (!e || e->dtype != dt || e->shape.size() != dims.size()) return false;
+  size_t i = 0;
+  for (long long d : dims)
+    if (e->shape[i++] != d) return false;
+  return true;
+}
+
+// The names load_all_weights binds (model.h:107-323) and the first of the
+// alternative names it accepts that the file holds.
+const char* kProj[3] = {"gate", "up", "down"};
+
+const Entry* find_layer(const BinIndex& b, char* k, size_t kn, int L, const char* fmt,
+                        const char* alt = nullptr) {
+  snprintf(k, kn, fmt, L);
+  const Entry* e = b.find(k);
+  if (!e && alt) {
+    snprintf(k, kn, alt, L);
+    e = b.find(k);
+  }
+  return e;
+}
+
+// Infers the config from the tensor shapes as load_all_weights does
+// (model.h:110-163; top_k 8, theta 1e7, eps 1e-6 fixed) and checks, before
+// anything is copied or uploaded, that every tensor the model binds exists
+// with the rank, dtype and size that config implies: embedding and head
+// [V][D], final and layer norms [D], q/k/v/o [nq*hd | nkv*hd][D] and
+// [D][nq*hd], biases, q/k norms [hd], router [E][D] (+ [E]), and for every
+// layer and expert the gate/up [d_ff][D] and down [D][d_ff] weights (Q4:
+// half the columns in bytes) with their [rows] scales.  The reference reads
+// such a file without checks; a mismatch there is an out-of-bounds read,
+// here it is MOE_ERR_ARG.
+moe_status validate_file(const BinIndex& b, const char* path, QwenConfig* out, int* dtype_out) {
+  char k[256];
+  const Entry* wq0 = b.find("model.layers.0.self_attn.q_proj.weight");
+  const Entry* wk0 = b.find("model.layers.0.self_attn.k_proj.weight");
+  const Entry* emb = b.find("model.embed_tokens.weight");
+  const Entry* fnorm = b.find("model.norm.weight");
+  if (!fnorm) fnorm = b.find("model.final_layernorm.weight");
+  if (!wq0 || !wk0 || !emb || !fnorm || wq0->shape.size() != 2 || wk0->shape.size() != 2 ||
+      emb->shape.size() != 2)
+    return set_error(MOE_ERR_ARG, "load: %s lacks the layer-0 attention / embedding / norm", path);
+  QwenConfig cfg{};
+  cfg.d_model = wq0->shape[1];
+  const Entry* qn0 = b.find("model.layers.0.self_attn.q_norm.weight");
+  if (qn0 && qn0->shape.size() != 1)
+    return set_error(MOE_ERR_ARG, "load: q_norm of layer 0 is not a vector");
+  cfg.head_dim = qn0 ? qn0->shape[0] : wq0->shape[0] / 32;
+  if (cfg.head_dim <= 0 || wq0->shape[0] % cfg.head_dim || wk0->shape[0] % cfg.head_dim)
+    return set_error(MOE_ERR_ARG, "load: q/k rows %d/%d are not multiples of head_dim %d",
+                     wq0->shape[0], wk0->shape[0], cfg.head_dim);
+  cfg.n_q = wq0->shape[0] / cfg.head_dim;
+  cfg.n_kv = wk0->shape[0] / cfg.head_dim;
+  cfg.vocab_size = emb->shape[0];
+  for (cfg.n_layers = 0;; ++cfg.n_layers) {
+    snprintf(k, sizeof k, "model.layers.%d.self_attn.q_proj.weight", cfg.n_layers);
+    if (!b.find(k)) break;
+  }
+  int dtype = 0;
+  for (cfg.n_experts = 0;; ++cfg.n_experts) {
+    snprintf(k, sizeof k, "model.layers.0.mlp.experts.%d.down_proj.weight", cfg.n_experts);
+    const std::string base = k;
+    const Entry* e = b.find(base.c_str());
+    int dt = 0;
+    if (!e && (e = b.find((base + ".q8").c_str()))) dt = 2;
+    if (!e && (e = b.find((base + ".q4").c_str()))) dt = 3;
+    if (!e) break;
+    if (e->shape.size() != 2)
+      return set_error(MOE_ERR_ARG, "load: %s is not a matrix", base.c_str());
+    const int dff = e->shape[1] * (dt == 3 ? 2 : 1);
+    if (cfg.n_experts > 0 && (dt != dtype || dff != cfg.d_ff))
+      return set_error(MOE_ERR_ARG, "load: expert %d of layer 0 differs from expert 0", cfg.n_experts);
+    cfg.d_ff = dff;
+    dtype = dt;
+  }
+  if (cfg.n_experts == 0 || cfg.d_ff <= 0) return set_error(MOE_ERR_ARG, "load: no experts in %s", path);
+  if (dtype == 0) return set_error(MOE_ERR_UNSUPPORTED, "load: fp32 experts are not supported");
+  cfg.top_k = 8;
+  cfg.causal = 1;
+  cfg.rope_theta = 10000000.f;
+  cfg.rms_eps = 1e-6f;
+  const long long D = cfg.d_model, V = cfg.vocab_size, hd = cfg.head_dim, E = cfg.n_experts;
+  const long long Dq = (long long)cfg.n_q * hd, Dkv = (long long)cfg.n_kv * hd, dff = cfg.d_ff;
+  if (dtype == 3 && (D % 2 || dff % 2))
+    return set_error(MOE_ERR_ARG, "load: Q4 experts need even d_model and d_ff");
+  if (!has_shape(emb, 0, {V, D}) || !has_shape(fnorm, 0, {D}))
+    return set_error(MOE_ERR_ARG, "load: embedding or final norm is not f32 [%lld x %lld] / [%lld]",
+                     V, D, D);
+  const Entry* head = b.find("lm_head.weight");
+  if (head && !has_shape(head, 0, {V, D}))
+    return set_error(MOE_ERR_ARG, "load: lm_head is not f32 [%lld x %lld]", V, D);
+  struct Req { const char* fmt; const char* alt; long long r, c; bool need; };
+  const Req reqs[] = {
+      {"model.layers.%d.self_attn.q_proj.weight", nullptr, Dq, D, true},
+      {"model.layers.%d.self_attn.k_proj.weight", nullptr, Dkv, D, true},
+      {"model.layers.%d.self_attn.v_proj.weight", nullptr, Dkv, D, true},
+      {"model.layers.%d.self_attn.o_proj.weight", nullptr, D, Dq, true},
+      {"model.layers.%d.self_attn.q_proj.bias", nullptr, Dq, 0, false},
+      {"model.layers.%d.self_attn.k_proj.bias", nullptr, Dkv, 0, false},
+      {"model.layers.%d.self_attn.v_proj.bias", nullptr, Dkv, 0, false},
+      {"model.layers.%d.self_attn.o_proj.bias", nullptr, D, 0, false},
+      {"model.layers.%d.self_attn.q_norm.weight", nullptr, hd, 0, false},
+      {"model.layers.%d.self_attn.k_norm.weight", nullptr, hd, 0, false},
+      {"model.layers.%d.input_layernorm.weight", "model.layers.%d.rms_1.weight", D, 0, true},
+      {"model.layers.%d.post_attention_layernorm.weight", "model.layers.%d.rms_2.weight", D, 0, true},
+      {"model.layers.%d.mlp.gate.weight", "model.layers.%d.mlp.router.gate.weight", E, D, true},
+      {"model.layers.%d.mlp.gate.bias", nullptr, E, 0, false},
+  };
+  const char* qsuf = dtype == 2 ? ".q8" : ".q4";
+  const long long cg = dtype == 2 ? D : D / 2, cd = dtype == 2 ? dff : dff / 2;
+  for (int L = 0; L < cfg.n_layers; ++L) {
+    for (const Req& r : reqs) {
+      const Entry* e = find_layer(b, k, sizeof k, L, r.fmt, r.alt);
+      if (!e) {
+        if (r.need) return set_error(MOE_ERR_ARG, "load: layer %d is incomplete in %s (%s)", L, path, k);
+        continue;
+      }
+      const bool ok = r.c ? has_shape(e, 0, {r.r, r.c}) : has_shape(e, 0, {r.r});
+      if (!ok) return set_error(MOE_ERR_ARG, "load: %s has the wrong dtype or shape", k);
+    }
+    for (int e = 0; e < E; ++e)
+      for (int j = 0; j < 3; ++j) {
+        snprintf(k, sizeof k, "model.layers.%d.mlp.experts.%d.%s_proj.weight", L, e, kProj[j]);
+        const std::string base = k;
+        const Entry* q = b.find((base + qsuf).c_str());
+        const Entry* sc = b.find((base + ".scale").c_str());
+        const long long rows = j < 2 ? dff : D, cols = j < 2 ? cg : cd;
+        if (!has_shape(q, dtype, {rows, cols}) || !has_shape(sc, 0, {rows}))
+          return set_error(MOE_ERR_ARG, "load: %s%s / .scale missing or not [%lld x %lld] / [%lld]",
+                           base.c_str(), qsuf, rows, cols, rows);
+      }
+  }
+  *out = cfg;
+  *dtype_out = dtype;
+  return MOE_OK;
 }
 
 }  // namespace
@@ -512,6 +660,17 @@ moe_status moe_model_create_synthetic(const QwenConfig* cfg, int expert_dtype, i
   return MOE_OK;
 }
 
+moe_status moe_model_inspect_file(const char* path, QwenConfig* cfg, int* expert_dtype) {
+  if (!path || !cfg) return set_error(MOE_ERR_ARG, "model_inspect_file: null argument");
+  BinIndex b;
+  moe_status st = bin_open(path, &b);
+  if (st) return st;
+  int dtype = 0;
+  if ((st = validate_file(b, path, cfg, &dtype))) return st;
+  if (expert_dtype) *expert_dtype = dtype;
+  return MOE_OK;
+}
+
 moe_status moe_model_load_file(const char* path, int max_seq, moe_model** out) {
   moe_status st = ensure_init();
   if (st) return st;
@@ -519,56 +678,23 @@ moe_status moe_model_load_file(const char* path, int max_seq, moe_model** out) {
   *out = nullptr;
   BinIndex b;
   if ((st = bin_open(path, &b))) return st;
+  QwenConfig cfg{};
+  int dtype = 0;
+  // every shape is checked before anything is copied or uploaded
+  if ((st = validate_file(b, path, &cfg, &dtype))) return st;
   std::vector<std::vector<float>> keep;
   char k[256];
-  auto need = [&](const char* name) { return b.find(name); };
-  // model.h:110-163: sizes from tensor shapes, fixed top_k / theta / eps
-  const Entry* wq0 = need("model.layers.0.self_attn.q_proj.weight");
-  const Entry* wk0 = need("model.layers.0.self_attn.k_proj.weight");
-  const Entry* emb = need("model.embed_tokens.weight");
-  const Entry* fnorm = need("model.norm.weight");
-  if (!fnorm) fnorm = need("model.final_layernorm.weight");
-  if (!wq0 || !wk0 || !emb || !fnorm || wq0->shape.size() != 2 || wk0->shape.size() != 2)
-    return set_error(MOE_ERR_ARG, "load: %s lacks the layer-0 attention / embedding / norm", path);
-  QwenConfig cfg{};
-  cfg.d_model = wq0->shape[1];
-  const Entry* qn0 = need("model.layers.0.self_attn.q_norm.weight");
-  cfg.head_dim = qn0 ? qn0->shape[0] : wq0->shape[0] / 32;
-  cfg.n_q = wq0->shape[0] / cfg.head_dim;
-  cfg.n_kv = wk0->shape[0] / cfg.head_dim;
-  cfg.vocab_size = emb->shape[0];
-  for (cfg.n_layers = 0;; ++cfg.n_layers) {
-    snprintf(k, sizeof k, "model.layers.%d.self_attn.q_proj.weight", cfg.n_layers);
-    if (!need(k)) break;
-  }
-  int dtype = 0;
-  for (cfg.n_experts = 0;; ++cfg.n_experts) {
-    snprintf(k, sizeof k, "model.layers.0.mlp.experts.%d.down_proj.weight", cfg.n_experts);
-    const std::string base = k;
-    const Entry* e = need(base.c_str());
-    int dt = 0;
-    if (!e && (e = need((base + ".q8").c_str()))) dt = 2;
-    if (!e && (e = need((base + ".q4").c_str()))) dt = 3;
-    if (!e) break;
-    cfg.d_ff = e->shape[1] * (dt == 3 ? 2 : 1);
-    dtype = dt;
-  }
-  if (cfg.n_experts == 0 || cfg.d_ff <= 0) return set_error(MOE_ERR_ARG, "load: no experts in %s", path);
-  if (dtype == 0) return set_error(MOE_ERR_UNSUPPORTED, "load: fp32 experts are not supported");
-  cfg.top_k = 8;
-  cfg.causal = 1;
-  cfg.rope_theta = 10000000.f;
-  cfg.rms_eps = 1e-6f;
   QwenWeights w{};
-  w.tok_emb = f32_of(emb, keep);
+  const Entry* fnorm = b.find("model.norm.weight");
+  if (!fnorm) fnorm = b.find("model.final_layernorm.weight");
+  w.tok_emb = f32_of(b.find("model.embed_tokens.weight"), keep);
   w.final_norm_w = f32_of(fnorm, keep);
-  w.lm_head = f32_of(need("lm_head.weight"), keep);
+  w.lm_head = f32_of(b.find("lm_head.weight"), keep);
   std::vector<QwenLayerWeights> lws((size_t)cfg.n_layers);
   std::vector<std::vector<QuantizedWeight>> qws((size_t)cfg.n_layers * 3);
   std::vector<std::vector<uint8_t>> qkeep;
-  auto layer_f32 = [&](int L, const char* fmt) {
-    snprintf(k, sizeof k, fmt, L);
-    return f32_of(need(k), keep);
+  auto layer_f32 = [&](int L, const char* fmt, const char* alt = nullptr) {
+    return f32_of(find_layer(b, k, sizeof k, L, fmt, alt), keep);
   };
   for (int L = 0; L < cfg.n_layers; ++L) {
     QwenLayerWeights& lw = lws[L];
@@ -582,26 +708,19 @@ moe_status moe_model_load_file(const char* path, int max_seq, moe_model** out) {
     lw.bo = layer_f32(L, "model.layers.%d.self_attn.o_proj.bias");
     lw.q_norm = layer_f32(L, "model.layers.%d.self_attn.q_norm.weight");
     lw.k_norm = layer_f32(L, "model.layers.%d.self_attn.k_norm.weight");
-    lw.rms1_w = layer_f32(L, "model.layers.%d.input_layernorm.weight");
-    if (!lw.rms1_w) lw.rms1_w = layer_f32(L, "model.layers.%d.rms_1.weight");
-    lw.rms2_w = layer_f32(L, "model.layers.%d.post_attention_layernorm.weight");
-    if (!lw.rms2_w) lw.rms2_w = layer_f32(L, "model.layers.%d.rms_2.weight");
-    lw.router_w = layer_f32(L, "model.layers.%d.mlp.gate.weight");
-    if (!lw.router_w) lw.router_w = layer_f32(L, "model.layers.%d.mlp.router.gate.weight");
+    lw.rms1_w = layer_f32(L, "model.layers.%d.input_layernorm.weight", "model.layers.%d.rms_1.weight");
+    lw.rms2_w = layer_f32(L, "model.layers.%d.post_attention_layernorm.weight",
+                          "model.layers.%d.rms_2.weight");
+    lw.router_w = layer_f32(L, "model.layers.%d.mlp.gate.weight", "model.layers.%d.mlp.router.gate.weight");
     lw.router_b = layer_f32(L, "model.layers.%d.mlp.gate.bias");
-    if (!lw.Wq || !lw.Wk || !lw.Wv || !lw.Wo || !lw.rms1_w || !lw.rms2_w || !lw.router_w)
-      return set_error(MOE_ERR_ARG, "load: layer %d is incomplete in %s", L, path);
-    const char* projs[3] = {"gate", "up", "down"};
     for (int j = 0; j < 3; ++j) {
       std::vector<QuantizedWeight>& v = qws[(size_t)L * 3 + j];
       v.resize((size_t)cfg.n_experts);
       for (int e = 0; e < cfg.n_experts; ++e) {
-        snprintf(k, sizeof k, "model.layers.%d.mlp.experts.%d.%s_proj.weight", L, e, projs[j]);
+        snprintf(k, sizeof k, "model.layers.%d.mlp.experts.%d.%s_proj.weight", L, e, kProj[j]);
         const std::string base = k;
-        const Entry* q = need((base + (dtype == 2 ? ".q8" : ".q4")).c_str());
-        const Entry* sc = need((base + ".scale").c_str());
-        if (!q || !sc || sc->dtype != 0 || q->shape.size() != 2)
-          return set_error(MOE_ERR_ARG, "load: %s missing or malformed", base.c_str());
+        const Entry* q = b.find((base + (dtype == 2 ? ".q8" : ".q4")).c_str());
+        const Entry* sc = b.find((base + ".scale").c_str());
         qkeep.emplace_back((const uint8_t*)q->data, (const uint8_t*)q->data + q->bytes);
         v[e].q = (const int8_t*)qkeep.back().data();
         v[e].s = f32_of(sc, keep);

@@ -327,7 +327,10 @@ std::mutex g_layer_mu;
 moe_status grow(ScratchBuf& b, size_t need, bool* synced) {
   if (need <= b.bytes) return MOE_OK;
   if (!*synced) {
+    // both streams: the expert-major path packs x tables on the side stream,
+    // and a forward that failed after forking it may not have joined it back
     moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
+    if (!st) st = check_hip(hipStreamSynchronize(side_stream()), "sync side stream");
     if (st) return st;
     *synced = true;
   }
@@ -616,8 +619,26 @@ moe_status moe_layer_create(const QwenConfig* cfg, const QwenLayerWeights* lw, m
   if (!lw->experts_quantized || !lw->Wg_q || !lw->Wu_q || !lw->Wd_q)
     return set_error(MOE_ERR_UNSUPPORTED, "layer_create: experts are not quantized");
   const int E = cfg->n_experts, D = cfg->d_model, dff = cfg->d_ff;
+  if (E <= 0 || D <= 0 || dff <= 0)
+    return set_error(MOE_ERR_ARG, "layer_create: bad dims D=%d d_ff=%d E=%d", D, dff, E);
   const int dtype = lw->Wg_q[0].dtype;
+  if (dtype != 2 && dtype != 3) return set_error(MOE_ERR_ARG, "layer_create: expert dtype %d", dtype);
   const long long rbg = dtype == 2 ? D : D / 2, rbd = dtype == 2 ? dff : dff / 2;
+  // Every expert's descriptor must describe the [d_ff x D] (gate, up) or
+  // [D x d_ff] (down) matrix the config implies (model.h:256, 279, 302 set
+  // rows / cols from the tensor shapes; cols is the logical column count):
+  // the copy below reads that many bytes from each.
+  for (int e = 0; e < E; ++e) {
+    const QuantizedWeight* ws[3] = {&lw->Wg_q[e], &lw->Wu_q[e], &lw->Wd_q[e]};
+    for (int j = 0; j < 3; ++j) {
+      const int rows = j < 2 ? dff : D, cols = j < 2 ? D : dff;
+      if (!ws[j]->q || !ws[j]->s || ws[j]->rows != rows || ws[j]->cols != cols)
+        return set_error(MOE_ERR_ARG,
+                         "layer_create: expert %d %s is %d x %d (q %p, s %p), expected %d x %d",
+                         e, j == 0 ? "gate" : (j == 1 ? "up" : "down"), ws[j]->rows, ws[j]->cols,
+                         (const void*)ws[j]->q, (const void*)ws[j]->s, rows, cols);
+    }
+  }
   // The reference binds one tensor per expert (model.h:228-305); the device
   // keeps each projection of all experts in one contiguous array.
   std::vector<uint8_t> g((size_t)E * dff * rbg), u((size_t)E * dff * rbg), d((size_t)E * D * rbd);

@@ -99,6 +99,7 @@ _SIGS = {
                                      ctypes.POINTER(_P)]),
     "moe_model_create": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
     "moe_model_load_file": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
+    "moe_model_inspect_file": (_I, [ctypes.c_char_p, _P, _P]),
     "moe_model_create_synthetic": (_I, [_P, _I, _I, ctypes.c_uint64, ctypes.c_float, _I,
                                         ctypes.POINTER(_P)]),
     "moe_model_destroy": (_I, [_P]),

@@ -84,6 +84,42 @@ void orc_rope_tables(int hd, float theta, int n_pos, float* cos_out, float* sin_
   }
 }
 
+/* test_model_trace.c:402-426 for one query row qv of one head at position
+ * P: scores over cache positions 0..P (k rows kbase + tk*hd), the softmax
+ * (max, expf, sequential sum, 1/(sum + 1e-9)), then the weighted V sum in
+ * position order into out[hd].  S: scratch of P + 1 floats. */
+static void attention_row(const float* qv, const float* kbase, const float* vbase, int P, int hd,
+                          float scale, float* S, float* out) {
+  for (int tk = 0; tk <= P; ++tk) {
+    const float* kv = kbase + (size_t)tk * hd;
+    float dot = 0.0f;
+    for (int d = 0; d < hd; ++d) {
+      float pr = qv[d] * kv[d];
+      dot = dot + pr;
+    }
+    S[tk] = dot * scale;
+  }
+  float m = S[0];
+  for (int i = 1; i <= P; ++i) if (S[i] > m) m = S[i];
+  float ssum = 0.0f;
+  for (int i = 0; i <= P; ++i) {
+    float e = expf(S[i] - m);
+    S[i] = e;
+    ssum = ssum + e;
+  }
+  float inv = 1.0f / (ssum + 1e-9f);
+  for (int i = 0; i <= P; ++i) S[i] = S[i] * inv;
+  for (int d = 0; d < hd; ++d) out[d] = 0.0f;
+  for (int tk = 0; tk <= P; ++tk) {
+    const float* vv = vbase + (size_t)tk * hd;
+    const float pk = S[tk];
+    for (int d = 0; d < hd; ++d) {
+      float pv = pk * vv[d];
+      out[d] = out[d] + pv;
+    }
+  }
+}
+
 /* test_model_trace.c:341-430 for the T rows at positions pos0..pos0+T-1 of
  * one layer: projections (+ bias), q/k norm, RoPE, K/V appended to the
  * cache (kc/vc: [n_kv][max_seq][hd] of this layer), causal attention of each
@@ -97,7 +133,8 @@ static void orc_attention_rows(const orc_config* cfg, const orc_layer* lw, const
   float* K = (float*)malloc(sizeof(float) * (size_t)T * Dkv);
   float* V = (float*)malloc(sizeof(float) * (size_t)T * Dkv);
   float* H = (float*)malloc(sizeof(float) * (size_t)T * Dq);
-  float* S = (float*)malloc(sizeof(float) * (size_t)(pos0 + T));
+  const size_t ns = (size_t)(pos0 + T);   /* scores of one row, one buffer per head */
+  float* Sall = (float*)malloc(sizeof(float) * ns * (size_t)nq);
   orc_matmul_f32(xn, lw->Wq, Q, T, Dq, D);
   orc_matmul_f32(xn, lw->Wk, K, T, Dkv, D);
   orc_matmul_f32(xn, lw->Wv, V, T, Dkv, D);
@@ -117,45 +154,16 @@ static void orc_attention_rows(const orc_config* cfg, const orc_layer* lw, const
     }
   }
   const int group = nq / nkv;
-  for (int h = 0; h < nq; ++h) {
-    const int kvh = h / group;
-    for (int t = 0; t < T; ++t) {
-      const int P = pos0 + t;        /* attends to positions 0..P */
-      const float* qv = Q + (size_t)t * Dq + (size_t)h * hd;
-      for (int tk = 0; tk <= P; ++tk) {
-        const float* kv = kc + ((size_t)kvh * max_seq + tk) * hd;
-        float dot = 0.0f;
-        for (int d = 0; d < hd; ++d) {
-          float pr = qv[d] * kv[d];
-          dot = dot + pr;
-        }
-        S[tk] = dot * scale;
-      }
-      float m = S[0];
-      for (int i = 1; i <= P; ++i) if (S[i] > m) m = S[i];
-      float ssum = 0.0f;
-      for (int i = 0; i <= P; ++i) {
-        float e = expf(S[i] - m);
-        S[i] = e;
-        ssum = ssum + e;
-      }
-      float inv = 1.0f / (ssum + 1e-9f);
-      for (int i = 0; i <= P; ++i) S[i] = S[i] * inv;
-      float* out = H + (size_t)t * Dq + (size_t)h * hd;
-      for (int d = 0; d < hd; ++d) out[d] = 0.0f;
-      for (int tk = 0; tk <= P; ++tk) {
-        const float* vv = vc + ((size_t)kvh * max_seq + tk) * hd;
-        const float pk = S[tk];
-        for (int d = 0; d < hd; ++d) {
-          float pv = pk * vv[d];
-          out[d] = out[d] + pv;
-        }
-      }
-    }
-  }
+  /* heads are independent: with -fopenmp each thread takes whole heads */
+#pragma omp parallel for schedule(static) if ((size_t)nq * ns * (size_t)hd >= 65536)
+  for (int h = 0; h < nq; ++h)
+    for (int t = 0; t < T; ++t)
+      attention_row(Q + (size_t)t * Dq + (size_t)h * hd, kc + (size_t)(h / group) * max_seq * hd,
+                    vc + (size_t)(h / group) * max_seq * hd, pos0 + t, hd, scale,
+                    Sall + (size_t)h * ns, H + (size_t)t * Dq + (size_t)h * hd);
   orc_matmul_f32(H, lw->Wo, y, T, D, Dq);
   if (lw->bo) for (int t = 0; t < T; ++t) for (int i = 0; i < D; ++i) y[(size_t)t * D + i] += lw->bo[i];
-  free(Q); free(K); free(V); free(H); free(S);
+  free(Q); free(K); free(V); free(H); free(Sall);
 }
 
 /* test_model_trace.c:433-521, one layer for T rows, x updated in place. */

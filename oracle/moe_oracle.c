@@ -9,12 +9,22 @@
  * Integer dot products use uint32_t so that the wrap-around the reference
  * gets from int32 overflow (signed overflow compiled by gcc to plain add/imul)
  * is reproduced with defined behaviour.
+ *
+ * The same file is also built with -fopenmp (liboracle_omp.so): the loops
+ * marked `omp parallel for` hand whole output rows (or whole tokens, or whole
+ * heads) to threads, each of which runs the row's arithmetic in the
+ * reference's order, so that build's results are bit-identical to the
+ * single-thread one (tests/test_oracle_omp.py).  Without -fopenmp the
+ * pragmas are ignored.
  */
 #include "oracle.h"
 
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 int32_t orc_f2i_trunc(float v) {
   /* cvttss2si: in-range iff -2^31 <= v < 2^31 (NaN fails both tests). */
@@ -25,23 +35,27 @@ int32_t orc_f2i_trunc(float v) {
 /* kernels.c:51-74.  Loop order m, n, k; the activation is truncated to int
  * (kernels.c:66) and multiplied by the int8 weight in int32 (kernels.c:67);
  * epilogue (kernels.c:71): one int->float conversion, a division by 127.0f,
- * a multiplication by the row scale. */
+ * a multiplication by the row scale.  One output row per call of q8_row (a
+ * function of its own, so that the threaded build's loop body is the same
+ * code as the single-thread one's). */
+static float q8_row(const float* a, const int8_t* w, int K, float scale) {
+  uint32_t acc = 0;
+  for (int k = 0; k < K; ++k) {
+    int32_t ai = orc_f2i_trunc(a[k] * 127.0f);
+    acc += (uint32_t)ai * (uint32_t)(int32_t)w[k];
+  }
+  float f = (float)(int32_t)acc;
+  f = f / 127.0f;
+  return f * scale;
+}
+
 void orc_gemv_q8(const float* A, const int8_t* Bq, const float* Bs, float* C,
                  int M, int N, int K) {
   for (int m = 0; m < M; ++m) {
     const float* a = A + (size_t)m * K;
     float* c = C + (size_t)m * N;
-    for (int n = 0; n < N; ++n) {
-      const int8_t* w = Bq + (size_t)n * K;
-      uint32_t acc = 0;
-      for (int k = 0; k < K; ++k) {
-        int32_t ai = orc_f2i_trunc(a[k] * 127.0f);
-        acc += (uint32_t)ai * (uint32_t)(int32_t)w[k];
-      }
-      float f = (float)(int32_t)acc;
-      f = f / 127.0f;
-      c[n] = f * Bs[n];
-    }
+#pragma omp parallel for schedule(static) if ((size_t)N * (size_t)K >= 65536)
+    for (int n = 0; n < N; ++n) c[n] = q8_row(a, Bq + (size_t)n * K, K, Bs[n]);
   }
 }
 
@@ -50,47 +64,51 @@ void orc_gemv_q8(const float* A, const int8_t* Bq, const float* Bs, float* C,
  * column k in its low nibble and column k+1 in its high nibble, both stored
  * with a +8 offset (kernels.c:110-112).  For odd K the final high nibble is
  * skipped (kernels.c:116-121).  Epilogue divides by 7.0f (kernels.c:125). */
+static float q4_row(const float* a, const uint8_t* w, int K, float scale) {
+  uint32_t acc = 0;
+  for (int k = 0; k < K; k += 2) {
+    uint8_t byte = w[k / 2];
+    int32_t lo = (int32_t)(byte & 0x0F) - 8;
+    int32_t hi = (int32_t)((byte >> 4) & 0x0F) - 8;
+    int32_t a0 = orc_f2i_trunc(a[k] * 7.0f);
+    acc += (uint32_t)a0 * (uint32_t)lo;
+    if (k + 1 < K) {
+      int32_t a1 = orc_f2i_trunc(a[k + 1] * 7.0f);
+      acc += (uint32_t)a1 * (uint32_t)hi;
+    }
+  }
+  float f = (float)(int32_t)acc;
+  f = f / 7.0f;
+  return f * scale;
+}
+
 void orc_gemv_q4(const float* A, const uint8_t* Bq, const float* Bs, float* C,
                  int M, int N, int K) {
   for (int m = 0; m < M; ++m) {
     const float* a = A + (size_t)m * K;
     float* c = C + (size_t)m * N;
-    for (int n = 0; n < N; ++n) {
-      const uint8_t* w = Bq + (size_t)n * (size_t)(K / 2);
-      uint32_t acc = 0;
-      for (int k = 0; k < K; k += 2) {
-        uint8_t byte = w[k / 2];
-        int32_t lo = (int32_t)(byte & 0x0F) - 8;
-        int32_t hi = (int32_t)((byte >> 4) & 0x0F) - 8;
-        int32_t a0 = orc_f2i_trunc(a[k] * 7.0f);
-        acc += (uint32_t)a0 * (uint32_t)lo;
-        if (k + 1 < K) {
-          int32_t a1 = orc_f2i_trunc(a[k + 1] * 7.0f);
-          acc += (uint32_t)a1 * (uint32_t)hi;
-        }
-      }
-      float f = (float)(int32_t)acc;
-      f = f / 7.0f;
-      c[n] = f * Bs[n];
-    }
+#pragma omp parallel for schedule(static) if ((size_t)N * (size_t)K >= 65536)
+    for (int n = 0; n < N; ++n) c[n] = q4_row(a, Bq + (size_t)n * (size_t)(K / 2), K, Bs[n]);
   }
 }
 
 /* test_model_trace.c:213-227: fp32 accumulator, k ascending, one rounding
  * for each product and each sum. */
-void orc_matmul_f32(const float* A, const float* B, float* C, int M, int N, int K) {
-  for (int m = 0; m < M; ++m) {
-    const float* a = A + (size_t)m * K;
-    for (int n = 0; n < N; ++n) {
-      const float* b = B + (size_t)n * K;
-      float acc = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        float p = a[k] * b[k];
-        acc = acc + p;
-      }
-      C[(size_t)m * N + n] = acc;
-    }
+static float f32_dot(const float* a, const float* b, int K) {
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    float p = a[k] * b[k];
+    acc = acc + p;
   }
+  return acc;
+}
+
+void orc_matmul_f32(const float* A, const float* B, float* C, int M, int N, int K) {
+#pragma omp parallel for collapse(2) schedule(static) \
+    if ((size_t)M * (size_t)N * (size_t)K >= 65536)
+  for (int m = 0; m < M; ++m)
+    for (int n = 0; n < N; ++n)
+      C[(size_t)m * N + n] = f32_dot(A + (size_t)m * K, B + (size_t)n * K, K);
 }
 
 /* kernels.c:149-181 */
@@ -167,6 +185,44 @@ void orc_softmax_topk(float* val, int k) {
   for (int i = 0; i < k; ++i) val[i] = val[i] * inv;
 }
 
+/* test_model_trace.c:478-515 for one token t: top-k and softmax of its
+ * logits, then per rank gate -> SiLU -> up -> g*u -> down and the weighted
+ * sum in rank order into at[D] (starting from zeros). */
+static void moe_token(const float* xt, const float* lg, int D, int E, int top_k, int d_ff,
+                      const orc_qweight* Wg, const orc_qweight* Wu, const orc_qweight* Wd,
+                      float* at, int* idx_out, float* p_out) {
+  float* g = (float*)malloc(sizeof(float) * (size_t)d_ff);
+  float* u = (float*)malloc(sizeof(float) * (size_t)d_ff);
+  float* y = (float*)malloc(sizeof(float) * (size_t)D);
+  int* idx = (int*)malloc(sizeof(int) * (size_t)top_k);
+  float* val = (float*)malloc(sizeof(float) * (size_t)top_k);
+  /* :480-487 top-k then softmax over the selected logits */
+  orc_topk_desc(lg, E, top_k, idx, val);
+  orc_softmax_topk(val, top_k);
+  if (idx_out) memcpy(idx_out, idx, sizeof(int) * (size_t)top_k);
+  if (p_out) memcpy(p_out, val, sizeof(float) * (size_t)top_k);
+  for (int j = 0; j < top_k; ++j) {
+    int e = idx[j];
+    float p = val[j];
+    /* Fewer than top_k selectable logits (NaN / -inf) leave idx -1, which
+     * the reference dereferences (UB at :496); here such a slot adds
+     * nothing. */
+    if (e < 0) continue;
+    /* :496-503 gate -> SiLU -> up -> g*u -> down */
+    orc_matmul_adaptive(xt, NULL, &Wg[e], g, 1, d_ff, D);
+    orc_silu(g, d_ff);
+    orc_matmul_adaptive(xt, NULL, &Wu[e], u, 1, d_ff, D);
+    for (int i = 0; i < d_ff; ++i) g[i] = g[i] * u[i];
+    orc_matmul_adaptive(g, NULL, &Wd[e], y, 1, D, d_ff);
+    /* :513 weighted sum in rank order */
+    for (int i = 0; i < D; ++i) {
+      float py = p * y[i];
+      at[i] = at[i] + py;
+    }
+  }
+  free(g); free(u); free(y); free(idx); free(val);
+}
+
 /* test_model_trace.c:463-517 (quantized-expert branch, 494-503). */
 void orc_moe_block(const float* x_norm, const float* x_resid, int T, int D,
                    int E, int top_k, int d_ff,
@@ -175,11 +231,6 @@ void orc_moe_block(const float* x_norm, const float* x_resid, int T, int D,
                    float* out, int* idx_out, float* p_out, float* logits_out) {
   float* logits = (float*)malloc(sizeof(float) * (size_t)T * (size_t)E);
   float* acc = (float*)calloc((size_t)T * (size_t)D, sizeof(float));
-  float* g = (float*)malloc(sizeof(float) * (size_t)d_ff);
-  float* u = (float*)malloc(sizeof(float) * (size_t)d_ff);
-  float* y = (float*)malloc(sizeof(float) * (size_t)D);
-  int* idx = (int*)malloc(sizeof(int) * (size_t)top_k);
-  float* val = (float*)malloc(sizeof(float) * (size_t)top_k);
 
   /* :465-468 router logits (+ optional bias) */
   orc_matmul_f32(x_norm, router_w, logits, T, E, D);
@@ -189,40 +240,25 @@ void orc_moe_block(const float* x_norm, const float* x_resid, int T, int D,
   }
   if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)T * (size_t)E);
 
-  for (int t = 0; t < T; ++t) {
-    /* :480-487 top-k then softmax over the selected logits */
-    orc_topk_desc(logits + (size_t)t * E, E, top_k, idx, val);
-    orc_softmax_topk(val, top_k);
-    if (idx_out) memcpy(idx_out + (size_t)t * top_k, idx, sizeof(int) * (size_t)top_k);
-    if (p_out) memcpy(p_out + (size_t)t * top_k, val, sizeof(float) * (size_t)top_k);
-
-    const float* xt = x_norm + (size_t)t * D;
-    float* at = acc + (size_t)t * D;
-    for (int j = 0; j < top_k; ++j) {
-      int e = idx[j];
-      float p = val[j];
-      /* Fewer than top_k selectable logits (NaN / -inf) leave idx -1, which
-       * the reference dereferences (UB at :496); here such a slot adds
-       * nothing. */
-      if (e < 0) continue;
-      /* :496-503 gate -> SiLU -> up -> g*u -> down */
-      orc_matmul_adaptive(xt, NULL, &Wg[e], g, 1, d_ff, D);
-      orc_silu(g, d_ff);
-      orc_matmul_adaptive(xt, NULL, &Wu[e], u, 1, d_ff, D);
-      for (int i = 0; i < d_ff; ++i) g[i] = g[i] * u[i];
-      orc_matmul_adaptive(g, NULL, &Wd[e], y, 1, D, d_ff);
-      /* :513 weighted sum in rank order */
-      for (int i = 0; i < D; ++i) {
-        float py = p * y[i];
-        at[i] = at[i] + py;
-      }
-    }
+  /* Tokens are independent after the router: with -fopenmp each thread
+   * takes whole tokens from 4 tokens on; fewer run one at a time outside
+   * any parallel region, so that their GEMVs split by rows instead. */
+#define MOE_TOKEN(t)                                                                      \
+  moe_token(x_norm + (size_t)(t) * D, logits + (size_t)(t) * E, D, E, top_k, d_ff, Wg, Wu, \
+            Wd, acc + (size_t)(t) * D, idx_out ? idx_out + (size_t)(t) * top_k : NULL,      \
+            p_out ? p_out + (size_t)(t) * top_k : NULL)
+  if (T >= 4) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int t = 0; t < T; ++t) MOE_TOKEN(t);
+  } else {
+    for (int t = 0; t < T; ++t) MOE_TOKEN(t);
   }
+#undef MOE_TOKEN
   /* :517 residual */
   for (size_t i = 0; i < (size_t)T * (size_t)D; ++i)
     out[i] = x_resid ? x_resid[i] + acc[i] : acc[i];
 
-  free(logits); free(acc); free(g); free(u); free(y); free(idx); free(val);
+  free(logits); free(acc);
 }
 
 /* export.py:23-27.  amax per row, clamped below at 1e-8 (as an fp32 value),
@@ -331,4 +367,13 @@ uint64_t orc_expf_mismatch_u32range(uint32_t lo, uint32_t count, const float* de
     }
   }
   return bad;
+}
+
+/* Threads the row-parallel loops use: 1 in the single-thread build. */
+int orc_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
 }

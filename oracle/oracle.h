@@ -128,6 +128,10 @@ void orc_expf_array(const float* x, float* y, size_t n);
 uint64_t orc_expf_mismatch_u32range(uint32_t lo, uint32_t count, const float* dev,
                                     uint32_t* first_bad);
 
+/* Threads of the row-parallel loops: omp_get_max_threads() in the -fopenmp
+ * build (liboracle_omp.so), 1 in the single-thread build. */
+int orc_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

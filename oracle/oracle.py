@@ -18,6 +18,8 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_LIB = os.path.join(_HERE, "liboracle.so")
+# the same sources built with -fopenmp (rows split over threads, bit-identical)
+ORACLE_OMP_LIB = os.path.join(_HERE, "liboracle_omp.so")
 REF_KERNELS_LIB = os.path.join(_HERE, "_ref", "libref_kernels.so")
 REF_TRACE_LIB = os.path.join(_HERE, "_ref", "libref_trace.so")
 
@@ -55,25 +57,63 @@ _ORC_SIGS = {
     "orc_rope_tables": (None, [_I, ctypes.c_float, _I, _P, _P]),
     "orc_greedy": (_I, [_P, _I]),
     "orc_softmax_rows": (None, [_P, _I, _I]),
+    "orc_threads": (_I, []),
 }
 
 _orc = None
+_orc_omp = None
+_threaded = False
 _refk = None
 _reft = None
 
 
-def orc():
+def _load_orc(path):
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} not built (make -C oracle)")
+    L = ctypes.CDLL(path)
+    for n, (r, a) in _ORC_SIGS.items():
+        f = getattr(L, n)
+        f.restype = r
+        f.argtypes = a
+    return L
+
+
+def orc_single():
+    """The single-thread build (liboracle.so)."""
     global _orc
     if _orc is None:
-        if not os.path.exists(ORACLE_LIB):
-            raise RuntimeError(f"{ORACLE_LIB} not built (make -C oracle)")
-        L = ctypes.CDLL(ORACLE_LIB)
-        for n, (r, a) in _ORC_SIGS.items():
-            f = getattr(L, n)
-            f.restype = r
-            f.argtypes = a
-        _orc = L
+        _orc = _load_orc(ORACLE_LIB)
     return _orc
+
+
+def orc_omp():
+    """The -fopenmp build (liboracle_omp.so): bit-identical, rows on threads."""
+    global _orc_omp
+    if _orc_omp is None:
+        _orc_omp = _load_orc(ORACLE_OMP_LIB)
+    return _orc_omp
+
+
+def orc():
+    """The build the wrappers below call: single-thread unless inside
+    `threaded()`."""
+    return orc_omp() if _threaded else orc_single()
+
+
+class threaded:
+    """Context manager: the wrappers use the -fopenmp build inside it (when
+    that build exists; otherwise the single-thread one)."""
+
+    def __enter__(self):
+        global _threaded
+        self._prev = _threaded
+        _threaded = os.path.exists(ORACLE_OMP_LIB)
+        return self
+
+    def __exit__(self, *exc):
+        global _threaded
+        _threaded = self._prev
+        return False
 
 
 def ref_available() -> bool:

@@ -38,3 +38,22 @@ def test_quantize_ties(moehip, dtype):
     moehip.check(moehip.lib().moe_quantize_rows_dev(dtype, dW.ptr, 1, 8, dq.ptr, ds.ptr), "quantize")
     np.testing.assert_array_equal(dq.download(q_want.shape, q_want.dtype), q_want)
     assert ds.download((1,), np.float32)[0] == 1.0
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_quantize_rows_exact_exporter(moehip, dtype):
+    """The device quantizer against the exporter's exact answer
+    (quant_pin_cases: RN32 division, half-to-even) on rows where a
+    reciprocal multiply, a double-precision scale, an unrounded quotient or
+    half-away rounding would each give another integer."""
+    import quant_pin_cases as Q
+    div = 127 if dtype == 2 else 7
+    W, _ = Q.find_rows(div)
+    N, K = W.shape
+    q_exact, s_want = Q.expected_rows(W, div)
+    q_want = q_exact.astype(np.int8) if dtype == 2 else Q.pack_q4(q_exact)
+    dW = moehip.DeviceBuffer.from_array(W)
+    dq, ds = moehip.DeviceBuffer(q_want.nbytes), moehip.DeviceBuffer(4 * N)
+    moehip.check(moehip.lib().moe_quantize_rows_dev(dtype, dW.ptr, N, K, dq.ptr, ds.ptr), "quantize")
+    np.testing.assert_array_equal(ds.download((N,), np.float32).view(np.uint32), s_want.view(np.uint32))
+    np.testing.assert_array_equal(dq.download(q_want.shape, q_want.dtype), q_want)
