@@ -237,6 +237,20 @@ moe_status moe_layer_set_grouped_min_tokens(moe_layer* layer, int min_tokens);
  *   Bit-identical to the reference on the same inputs. */
 moe_status moe_layer_forward(moe_layer* layer, const float* x_norm, const float* x_resid, int T,
                              float* out, int32_t* idx_out, float* p_out);
+/* moe_layer_forward that allocates nothing: no reference counterpart (the
+ * reference allocates its temporaries per call, test_model_trace.c:474-476);
+ * it is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments and bit-identical results; always the per-(token, rank) kernels.
+ * Its scratch (logits, selection, packed tables, h) lives in a 4 MiB
+ * file-scope device array each GPU holds until the process ends; T is at
+ * most 32 tokens and the scratch need at most 4 MiB (about 72 KiB per token
+ * at d_model 2048, d_ff 768, 128 experts, top-8), else MOE_ERR_ARG with a
+ * message.  The first call on a device looks up the array's address.  All
+ * no-allocation calls on one GPU share the array: calls that overlap on one
+ * GPU race (the library's own stream serialises its calls). */
+moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, const float* x_resid,
+                                     int T, float* out, int32_t* idx_out, float* p_out);
 /* test_model_trace.c:460-517 including norm2: out = x + MoE(rmsnorm(x, rms2_w)) */
 moe_status moe_block_forward(moe_layer* layer, const float* x, int T, float* out, float eps);
 /* test_model_trace.c:241-255 on device arrays: y = (x / sqrt(mean(x^2)+eps)) * w

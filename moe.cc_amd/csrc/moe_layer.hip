@@ -463,16 +463,18 @@ int grouped_min_tokens(const LayerDev* L) {
 
 moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps);
 
-// The MoE block of T tokens.  norm_eps >= 0: `x` is the raw residual stream
+// The MoE block of T tokens on scratch already bound to L (ensure_scratch or
+// the no-allocation array).  norm_eps >= 0: `x` is the raw residual stream
 // and the block starts with rmsnorm(x, rms2_w) (:461), fused into the router
 // product for few tokens; norm_eps < 0: `x` is already x_norm.
-moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const float* resid,
-                              int T, float* out, int32_t* idx_out, float* p_out) {
-  if (T <= 0) return MOE_OK;
-  moe_status st = ensure_scratch(L, T);
-  if (st) return st;
+// allow_grouped: many tokens may take the expert-major kernels (their
+// scratch bound too); otherwise every T runs the per-pair kernels.
+moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const float* resid,
+                             int T, float* out, int32_t* idx_out, float* p_out,
+                             bool allow_grouped) {
+  moe_status st = MOE_OK;
   hipStream_t s = stream();
-  const bool grouped = T >= grouped_min_tokens(L) && grouped_ok(L);
+  const bool grouped = allow_grouped && T >= grouped_min_tokens(L) && grouped_ok(L);
   const bool fuse_norm = norm_eps >= 0.0f && !grouped && dense_norm_ok(T, L->D) &&
                          dense_select_ok(T, L->E) && aligned16(x) && aligned16(L->router_w);
   const float* xn = x;
@@ -519,10 +521,93 @@ moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const
   return check_hip(hipGetLastError(), "down launch");
 }
 
+moe_status layer_forward_impl(LayerDev* L, const float* x, float norm_eps, const float* resid,
+                              int T, float* out, int32_t* idx_out, float* p_out) {
+  if (T <= 0) return MOE_OK;
+  moe_status st = ensure_scratch(L, T);
+  if (st) return st;
+  return layer_forward_run(L, x, norm_eps, resid, T, out, idx_out, p_out, true);
+}
+
 moe_status layer_forward(LayerDev* L, const float* xn, const float* resid, int T, float* out,
                          int32_t* idx_out, float* p_out) {
   return layer_forward_impl(L, xn, -1.0f, resid, T, out, idx_out, p_out);
 }
+
+// ---- the no-allocation forward ----
+//
+// Its scratch is this file-scope device array: each GPU holds its own copy
+// from module load until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol); it uses the device address hipGetSymbolAddress returns, looked up
+// once per device.  Every no-allocation call on a GPU shares the array, so
+// calls that overlap on one GPU race: the library serialises its own calls
+// (one stream, g_layer_mu), callers that enqueue on other streams must not
+// overlap two such forwards.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+constexpr int kNoAllocMaxTokens = 32;
+constexpr int kNoAllocMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_noalloc_mu;
+uint8_t* g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Byte offsets of the per-pair path's buffers inside the array (the same
+// buffers ensure_scratch sizes for that path); returns the total.
+struct NoAllocLayout {
+  size_t counter, logits, idx, p, xtab, htab, h, xn, hpart, xpart, total;
+};
+NoAllocLayout noalloc_layout(const LayerDev* L, int T) {
+  NoAllocLayout o{};
+  const size_t np = (size_t)T * L->topk;
+  size_t at = 0;
+  auto take = [&](size_t bytes) { const size_t r = at; at += align256(bytes); return r; };
+  o.counter = take(4);
+  o.logits = take((size_t)T * L->E * 4);
+  o.idx = take(np * 4);
+  o.p = take(np * 4);
+  o.xtab = take((size_t)T * act_table_bytes(L->D));
+  o.htab = take(np * act_table_bytes(L->dff));
+  o.h = take(np * L->dff * 4);
+  o.xn = take((size_t)T * L->D * 4);
+  o.hpart = take(np * (size_t)((L->dff + 7) / 8) * 8);
+  o.xpart = take((size_t)std::min(T, 4) * (L->E + 16) * 8);
+  o.total = at;
+  return o;
+}
+
+// The array's device address on the current device, looked up (and its
+// selection counter zeroed, which every launch that uses it leaves at zero
+// again) on the first call on that device.
+moe_status noalloc_scratch(uint8_t** out) {
+  int dev = 0;
+  moe_status st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st) return st;
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(MOE_ERR_UNSUPPORTED, "layer_forward_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    if ((st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")))
+      return st;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, stream(), (uint32_t*)p, 64);
+    if ((st = check_hip(hipGetLastError(), "scratch counter clear"))) return st;
+    g_noalloc_ptr[dev] = (uint8_t*)p;
+  }
+  *out = g_noalloc_ptr[dev];
+  return MOE_OK;
+}
+
+}  // namespace
 
 moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, float eps) {
   if (T <= 0) return MOE_OK;
@@ -675,6 +760,43 @@ moe_status moe_layer_forward(moe_layer* layer, const float* x_norm, const float*
   if (T < 0) return set_error(MOE_ERR_ARG, "layer_forward: T < 0");
   std::lock_guard<std::mutex> lk(g_layer_mu);
   return layer_forward(&layer->L, x_norm, x_resid, T, out, idx_out, p_out);
+}
+
+moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, const float* x_resid,
+                                     int T, float* out, int32_t* idx_out, float* p_out) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (!layer || !x_norm || !out) return set_error(MOE_ERR_ARG, "layer_forward_noalloc: null argument");
+  if (T < 0) return set_error(MOE_ERR_ARG, "layer_forward_noalloc: T < 0");
+  if (T == 0) return MOE_OK;
+  if (T > kNoAllocMaxTokens)
+    return set_error(MOE_ERR_ARG, "layer_forward_noalloc: T = %d above the maximum of %d tokens "
+                     "(use moe_layer_forward)", T, kNoAllocMaxTokens);
+  LayerDev* L = &layer->L;
+  const NoAllocLayout o = noalloc_layout(L, T);
+  if (o.total > kNoAllocScratchBytes)
+    return set_error(MOE_ERR_ARG,
+                     "layer_forward_noalloc: %d tokens need %zu scratch bytes, more than the "
+                     "%zu-byte no-allocation array (use moe_layer_forward)",
+                     T, o.total, kNoAllocScratchBytes);
+  std::lock_guard<std::mutex> lk(g_layer_mu);
+  uint8_t* base = nullptr;
+  if ((st = noalloc_scratch(&base))) return st;
+  L->sel_counter = (unsigned*)(base + o.counter);
+  L->logits = (float*)(base + o.logits);
+  L->idx = (int*)(base + o.idx);
+  L->p = (float*)(base + o.p);
+  L->xtab = base + o.xtab;
+  L->htab = base + o.htab;
+  L->h = (float*)(base + o.h);
+  L->xn = (float*)(base + o.xn);
+  L->hpart = (uint32_t*)(base + o.hpart);
+  L->xpart = (uint32_t*)(base + o.xpart);
+  L->ecount = L->eoff = L->perm = L->wsflag = nullptr;
+  L->tasks = nullptr;
+  L->y = nullptr;
+  L->capT = T;
+  return layer_forward_run(L, x_norm, -1.0f, x_resid, T, out, idx_out, p_out, false);
 }
 
 moe_status moe_block_forward(moe_layer* layer, const float* x, int T, float* out, float eps) {

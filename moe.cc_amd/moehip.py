@@ -93,6 +93,7 @@ _SIGS = {
     "moe_layer_destroy": (_I, [_P]),
     "moe_layer_set_grouped_min_tokens": (_I, [_P, _I]),
     "moe_layer_forward": (_I, [_P, _P, _P, _I, _P, _P, _P]),
+    "moe_layer_forward_noalloc": (_I, [_P, _P, _P, _I, _P, _P, _P]),
     "moe_block_forward": (_I, [_P, _P, _I, _P, ctypes.c_float]),
     "moe_rmsnorm_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
     "moe_layer_debug_buffers": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P),
