@@ -1,0 +1,728 @@
+// expert_gemm.hip - the expert products of the many-token MoE block as
+// grouped integer GEMMs on v_mfma_i32_32x32x32_i8 (gfx950), bit-identical to
+// the per-(token, rank) GEMVs of test_model_trace.c:496-503.
+//
+// One block (four waves) takes one task -- up to 32*NT (token, rank) pairs
+// routed to one expert, listed by group_kernel -- and one tile of rows:
+//   gate/up  128 rows of d_ff in both matrices: wave w owns gate and up rows
+//            32w .. 32w + 31, so a lane holds g and u of the same (row, pair)
+//            for the SwiGLU epilogue (:496-501)
+//   down     256 rows of D: wave w owns rows 64w .. 64w + 63
+// K runs outermost in stages of 64 weight bytes per row (128 Q4 columns or
+// 64 Q8 columns).  Both operands go straight from memory into a four-stage
+// LDS ring with global_load_lds_dwordx4 (three stages ahead, no registers):
+// each wave's own 64 weight rows, and the pairs' activation units (16 bytes
+// of one limb plane), which the four waves share.  Both are XOR-swizzled so
+// that the MFMA operand reads are free of bank conflicts.  One barrier per
+// stage; the wait before it counts this wave's loads.
+// Every unpacked weight operand feeds all NT pair tiles, so the Q4 nibble
+// unpack costs 6 VALU per 2*NT MFMAs, and each weight byte leaves HBM once
+// per task.  NT (1, 2, 4) is chosen per launch from the mean pairs per
+// expert; tiles past a task's pairs repeat its last pair and are dropped.
+//
+// The integer dots are exact in any order.  A quantized activation a is
+// split into int8 limbs a = sum_l b_l 256^l; a task whose activations need
+// one limb runs one pass, otherwise the limbs run one after another and
+// fold into a wrapping uint32 total (sum_l dot_l << 8l).  Q4 weights enter
+// as unsigned nibbles u = w + 8 and sum a*w = sum a*u - 8*sum a is applied
+// once per output.  The fp32 epilogues are the reference's operations in
+// the reference's order.
+//
+// MFMA layout (checked on gfx950): A lane l = row l % 32 with 16 bytes of
+// k-group l / 32; B lane l = column l % 32 with the same k-group; result
+// register i of lane l = row 8*(i/4) + 4*(l/32) + i%4, column l % 32.  The
+// columns a slot (lane half h, step s) stands for are this file's choice,
+// made identically for both operands: 16-column unit u = h*S + s of the
+// stage (S steps per stage), so a lane's weight bytes of one stage are the
+// 32 contiguous bytes 32h .. 32h + 31 of the row's 64-byte stage chunk.
+//
+// Unit tables (this path's activation tables): the header and plane
+// offsets of moe_qtile.h's act tables, but each limb plane is a sequence of
+// 16-byte units, unit u = columns 16u .. 16u + 15: Q8 in column order, Q4
+// the 8 even columns then the 8 odd ones (the order a packed weight dword's
+// low nibbles, then high nibbles, take).  pack_units_kernel writes the x
+// tables, the gate/up epilogue the h tables.
+#include <utility>
+
+#include "moe_device.h"
+#include "moe_internal.h"
+#include "moe_layer.h"
+#include "moe_lib.h"
+#include "moe_qtile.h"
+
+namespace moe {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned int v16u __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kEgWaves = 4;   // waves per block unless a shape says otherwise
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+template <bool Q4>
+struct EgStage {
+  static constexpr int S = Q4 ? 4 : 2;           // 32-column MFMA steps per stage
+  static constexpr int COLS = 32 * S;            // columns per stage
+  static constexpr int UNITS = 2 * S;            // 16-byte units per pair row
+  static constexpr int ROWB = UNITS * 16;        // LDS bytes per pair row
+  static constexpr int RPI = 1024 / ROWB;        // pair rows per LDS load instruction
+};
+
+// Slot of unit u in pair row r of an LDS stage: u ^ swz(r).  Q4 rows are 128
+// bytes (one pass over the banks), Q8 rows 64: eight consecutive rows' reads
+// of one unit then cover eight distinct 16-byte bank groups.
+template <bool Q4>
+__device__ __forceinline__ int swz(int r) {
+  return Q4 ? (r & 7) : ((r >> 1) & 3);
+}
+
+// 32 weight bytes of one row for one stage: bytes 32h .. 32h + 31 of the
+// row's 64-byte chunk.
+struct WFrag32 {
+  u32x4 w[2];
+};
+
+// A operand of step s: Q4 packed bytes 8s .. 8s + 7 of the fragment as
+// [low nibbles of dwords 2s, 2s+1][high nibbles of the same]; Q8 bytes
+// 16s .. 16s + 15.
+template <bool Q4>
+__device__ __forceinline__ v4i a_op(const WFrag32& f, int s) {
+  v4i r;
+  if constexpr (Q4) {
+    const u32x4 w = f.w[s >> 1];
+    const uint32_t w0 = (s & 1) ? w[2] : w[0];
+    const uint32_t w1 = (s & 1) ? w[3] : w[1];
+    constexpr uint32_t M = 0x0F0F0F0Fu;
+    r[0] = (int)(w0 & M);
+    r[1] = (int)(w1 & M);
+    r[2] = (int)((w0 >> 4) & M);
+    r[3] = (int)((w1 >> 4) & M);
+  } else {
+    const u32x4 w = f.w[s];
+    r[0] = (int)w[0]; r[1] = (int)w[1]; r[2] = (int)w[2]; r[3] = (int)w[3];
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------- x tables
+
+// One block per row: x -> quantized a = trunc(x * 7 or 127) (kernels.c:115
+// / :66) -> 4 limb planes of 16-byte units, header {limbs needed, sum a}.
+// K % 16 == 0.
+template <bool Q4>
+__global__ __launch_bounds__(256) void pack_units_kernel(const float* __restrict__ x, int K,
+                                                         uint8_t* __restrict__ tabs, size_t tab_bytes) {
+  __shared__ int scratch[2];
+  const float mult = Q4 ? 7.0f : 127.0f;
+  const float* xr = x + (size_t)blockIdx.x * K;
+  uint8_t* tab = tabs + (size_t)blockIdx.x * tab_bytes;
+  if (threadIdx.x == 0) { scratch[0] = 1; scratch[1] = 0; }
+  __syncthreads();
+  int nl = 1;
+  uint32_t part = 0;
+  for (int u = threadIdx.x; u < K / 16; u += blockDim.x) {
+    int32_t a[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(xr + 16 * u)[q];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[4 * q + i] = f2i_trunc_x86(v[i] * mult);
+    }
+    uint32_t b[16][4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int n = limbs_needed(a[i]);
+      nl = n > nl ? n : nl;
+      part += (uint32_t)a[i];
+      split_limbs(a[i], b[i]);
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      u32x4 o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        // Q4: dwords 0-1 the even columns, 2-3 the odd ones
+        const int c0 = Q4 ? (d < 2 ? 8 * d : 8 * (d - 2) + 1) : 4 * d;
+        const int st = Q4 ? 2 : 1;
+        o[d] = pack4(b[c0][l], b[c0 + st][l], b[c0 + 2 * st][l], b[c0 + 3 * st][l]);
+      }
+      *reinterpret_cast<u32x4*>(const_cast<uint32_t*>(act_plane(tab, K, l)) + 4 * u) = o;
+    }
+  }
+  block_max_sum(nl, part, scratch);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    reinterpret_cast<int*>(tab)[0] = scratch[0];
+    reinterpret_cast<uint32_t*>(tab)[1] = (uint32_t)scratch[1];
+  }
+}
+
+// ---------------------------------------------------------------- passes
+
+// The task's pairs, prefetched into LDS: pair id, activation table, the
+// table's activation sum, and the epilogue's per-pair reductions.
+struct EgPairs {
+  int pair[kEgPairs];
+  const uint8_t* tab[kEgPairs];
+  uint32_t asum[kEgPairs];
+  int red_nl[kEgPairs];
+  unsigned red_sum[kEgPairs];
+  int nl;
+};
+
+// Block shape: RG row groups x (4 / RG) pair groups of waves.  Wave w is
+// row group w % RG (64 weight rows: gate rows 0-31 and up rows 32-63 of its
+// 32 h-rows for gate/up, two 32-row tiles for down) and pair group w / RG
+// (NTW tiles of 32 pairs).  A pass covers NP = 32 * NTW * (4 / RG) pairs;
+// D stages in the LDS ring.  LDS layout of one stage:
+//   W  64 * RG weight rows x 64 bytes, 16-byte chunk c of row r in slot
+//      c ^ wswz(r);
+//   B  NP pair rows x ROWB bytes, unit u of pair row r in slot u ^ swz(r).
+__device__ __forceinline__ int wswz(int r) { return (r >> 1) & 3; }
+
+template <bool Q4, int RG, int NTW, int D, int NW = kEgWaves>
+struct EgCfg {
+  static constexpr int W = NW;                                   // waves per block
+  static constexpr int PG = NW / RG;
+  static constexpr int NP = 32 * NTW * PG;
+  static constexpr int W_BYTES = 64 * RG * 64;
+  static constexpr int B_BYTES = NP * EgStage<Q4>::ROWB;
+  static constexpr int STAGE = W_BYTES + B_BYTES;
+  static constexpr int NIW = W_BYTES / 1024;                     // W load instructions (4 * RG)
+  static constexpr int NIB = B_BYTES / 1024;                     // B load instructions
+  static constexpr int PERW = NIW / NW;                          // per wave
+  static constexpr int PERB = (NIB + NW - 1) / NW;               // per wave
+  static constexpr int Q = PERW + PERB;                          // loads per wave per stage
+  static constexpr size_t BYTES = (size_t)D * STAGE;
+  static_assert(NW % RG == 0 && NIW % NW == 0, "block shape");
+  static_assert(NP <= kEgPairs, "pairs of a pass");
+};
+
+// One 16-byte-per-lane global -> LDS load: lane i's 16 bytes from src land at
+// LDS address lds + 16 i.  Issued from inline asm so that the compiler's
+// wait-count bookkeeping, which does not place these loads correctly among
+// the register loads, never sees them: every wait for them is explicit
+// (stage_sync), and the compiler's own vmcnt waits only grow stricter.
+// M0 is reserved to the compiler, which uses it in these kernels for nothing
+// else (checked in the generated code), so setting it here is safe.
+__device__ __forceinline__ void lds_load16(const void* src, uint8_t* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(la)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// This lane's load sources of a pass, at column 0: its weight chunks (LDS
+// row 16 * ins + lane / 4, slot lane % 4, for the wave's instructions ins =
+// wave + 4k) and its B units (limb plane l of pair row ins * RPI + lane /
+// UNITS, slot lane % UNITS).  wrow(r) is the weight row behind LDS row r.
+template <bool Q4, class C>
+struct EgSrc {
+  const uint8_t* w[C::PERW];
+  const uint8_t* b[C::PERB];
+};
+
+template <bool Q4, class C, class WRow>
+__device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const EgPairs& sp,
+                                           int pbase, int n, int K, int l) {
+  using SG = EgStage<Q4>;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int k = 0; k < C::PERW; ++k) {
+    const int r = 16 * (wave + C::W * k) + lane / 4;
+    src.w[k] = wrow(r) + 16 * ((lane % 4) ^ wswz(r));
+  }
+#pragma unroll
+  for (int k = 0; k < C::PERB; ++k) {
+    const int ins = (wave + C::W * k) % C::NIB;
+    const int row = ins * SG::RPI + lane / SG::UNITS;
+    const int unit = (lane % SG::UNITS) ^ swz<Q4>(row);
+    const int q = min(pbase + row, n - 1);
+    src.b[k] = reinterpret_cast<const uint8_t*>(act_plane(sp.tab[q], K, l)) + unit * 16;
+  }
+}
+
+// Loads stage st into buffer buf.  Every wave issues Q loads (a wave past
+// the last B instruction repeats one another wave issued: the same bytes to
+// the same place).
+template <bool Q4, class C>
+__device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint8_t* buf) {
+  using SG = EgStage<Q4>;
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int k = 0; k < C::PERW; ++k)
+    lds_load16(src.w[k] + (size_t)st * 64, buf + (wave + C::W * k) * 1024);
+#pragma unroll
+  for (int k = 0; k < C::PERB; ++k) {
+    const int ins = (wave + C::W * k) % C::NIB;
+    lds_load16(src.b[k] + (size_t)st * SG::UNITS * 16, buf + C::W_BYTES + ins * 1024);
+  }
+}
+
+// Waits for this wave's loads of the stage about to be read (N later loads
+// may stay in flight) and its LDS reads, then joins the block: after it the
+// whole stage is in LDS and every wave is done with the buffer that the
+// next loads overwrite.
+template <int N>
+__device__ __forceinline__ void stage_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// This wave's 32 weight bytes of its row-group row 32m + lane % 32 (bytes
+// 32h .. 32h + 31 of the stage chunk: chunks 2h and 2h + 1).
+template <int RG>
+__device__ __forceinline__ WFrag32 w_frag(const uint8_t* wbuf, int m) {
+  const int lane = threadIdx.x % kWave, rg = (threadIdx.x / kWave) % RG, j = lane % 32, h = lane / 32;
+  const int r = 64 * rg + 32 * m + j;
+  const uint8_t* row = wbuf + r * 64;
+  WFrag32 f;
+  f.w[0] = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * h) ^ wswz(r)));
+  f.w[1] = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * h + 1) ^ wswz(r)));
+  return f;
+}
+
+// One stage of a pass: wait for stage st, issue stage st + D - 1 (clamped to
+// the last stage, then rotated) into its ring buffer, then the MFMAs of
+// stage st: acc[m][t] for this wave's pair tiles t.
+template <bool Q4, int RG, int NTW, int D, int NW>
+__device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int st,
+                                         int nst, int rot, uint8_t* lds, v16i (&acc)[2][NTW]) {
+  using SG = EgStage<Q4>;
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  const int lane = threadIdx.x % kWave, pg = (threadIdx.x / kWave) / RG, j = lane % 32, h = lane / 32;
+  stage_sync<(D - 2) * C::Q>();
+  stage_load<Q4, C>(src, (min(st + D - 1, nst - 1) + rot) % nst, lds + ((st + D - 1) % D) * C::STAGE);
+  const uint8_t* buf = lds + (st % D) * C::STAGE;
+  const WFrag32 f0 = w_frag<RG>(buf, 0), f1 = w_frag<RG>(buf, 1);
+  const uint8_t* B = buf + C::W_BYTES + (32 * NTW * pg + j) * SG::ROWB;
+  const int sw = swz<Q4>(j);   // = swz(32t + j) for every tile t
+#pragma unroll
+  for (int s = 0; s < SG::S; ++s) {
+    const v4i a0 = a_op<Q4>(f0, s);
+    const v4i a1 = a_op<Q4>(f1, s);
+    const int slot = (h * SG::S + s) ^ sw;
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      const v4i b = *reinterpret_cast<const v4i*>(B + 32 * t * SG::ROWB + slot * 16);
+      acc[0][t] = mfma32(a0, b, acc[0][t]);
+      acc[1][t] = mfma32(a1, b, acc[1][t]);
+    }
+  }
+}
+
+// acc[m][t] = sum over all K columns of W_m[lane's row] x limb l of pair
+// pbase + 32 (NTW pg + t) + (lane % 32).  Every thread of the block calls
+// this.  On return every load of the pass has landed and every wave is done
+// with the LDS ring.
+template <bool Q4, int RG, int NTW, int D, int NW, class WRow>
+__device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, int pbase, int n,
+                                        int l, uint8_t* lds, v16i (&acc)[2][NTW]) {
+  using SG = EgStage<Q4>;
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  const int nst = K / SG::COLS;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) acc[m][t] = v16i{};
+  EgSrc<Q4, C> src;
+  eg_sources<Q4, C>(src, wrow, sp, pbase, n, K, l);
+  // the stages run in a rotated order, a different one per block (the dots
+  // are exact in any order), so that concurrent blocks read different
+  // column slices of their rows
+  const int rot = (int)(blockIdx.x % (unsigned)nst);
+#pragma unroll
+  for (int p = 0; p < D - 1; ++p) stage_load<Q4, C>(src, (min(p, nst - 1) + rot) % nst, lds + p * C::STAGE);
+  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW>(src, st, nst, rot, lds, acc);
+  // the clamped loads past the last stage land before the ring is reused
+  stage_sync<0>();
+}
+
+// Dots of a pass over all limbs: one pass (nl == 1) or limb passes folded
+// into wrapping uint32 totals.
+template <bool Q4, int RG, int NTW, int D, int NW, class WRow>
+__device__ __forceinline__ void eg_dots(WRow&& wrow, int K, const EgPairs& sp, int pbase, int n,
+                                        int nl, uint8_t* lds, v16u (&dots)[2][NTW]) {
+  v16i acc[2][NTW];
+  eg_pass<Q4, RG, NTW, D, NW>(wrow, K, sp, pbase, n, 0, lds, acc);
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) dots[m][t] = __builtin_bit_cast(v16u, acc[m][t]);
+  for (int l = 1; l < nl; ++l) {
+    eg_pass<Q4, RG, NTW, D, NW>(wrow, K, sp, pbase, n, l, lds, acc);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) dots[m][t] += __builtin_bit_cast(v16u, acc[m][t]) << (8u * l);
+  }
+}
+
+// Where row r of an activation unit table sits in its limb plane.
+template <bool Q4>
+__device__ __forceinline__ int unit_byte(int r) {
+  if constexpr (!Q4) return r;
+  const int i = r % 16;
+  return (r - i) + ((i & 1) ? 8 + i / 2 : i / 2);
+}
+
+struct EgArgs {
+  const uint8_t* w0; const uint8_t* w1;   // gate and up (gate/up) or down (w1 unused)
+  const float* s0; const float* s1;       // their row scales [E][rows]
+  long long rb;                           // weight row bytes
+  int rows;                               // rows per expert (d_ff or D)
+  int K;                                  // logical columns (D or d_ff)
+  int topk;
+  const int* perm;                        // pair ids grouped by expert
+  const int2* tasks;                      // {expert | pairs << 16, first pair}, x < 0 past the end
+  int ntask;                              // entries of tasks
+  const uint8_t* tab;                     // x tables [T] (gate/up) or h tables [pairs] (down)
+  size_t tab_bytes;
+  uint8_t* htab; size_t htab_bytes;       // gate/up: h tables out
+  uint32_t* hpart; int nseg;              // per-segment h headers: written by gate/up, read by down
+  float* y;                               // down: [pairs][D]
+};
+
+// Block -> (task, row tile), so that the row tiles of a task run on one XCD
+// (blocks are dealt to the 8 XCDs in turn) and share its L2.  The grid is
+// nrt * ceil8(ntask) blocks.  Returns false past the last task.
+__device__ __forceinline__ bool eg_block(int ntask, int nrt, int* task, int* rt) {
+  const int lin = blockIdx.x, xcd = lin % 8, k = lin / 8;
+  *task = (k / nrt) * 8 + xcd;
+  *rt = k % nrt;
+  return *task < ntask;
+}
+
+// ---------------------------------------------------------------- gate/up
+
+// SwiGLU epilogue of one pass (:496-501): lane (j, h) of wave (rg, pg) holds,
+// for pair pbase + 32 (NTW pg + t) + j, gate and up dots of rows rb + 32 rg
+// + 8q + 4h + r.  h = (g / (1 + expf(-g))) * u is quantized for down and
+// written into the pair's h table; the rows' limb count and activation sum
+// go to red_nl / red_sum.
+template <bool Q4, int RG, int NTW>
+__device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const v16u (&dots)[2][NTW],
+                                            int pbase, int n, int rb, const float* sg,
+                                            const float* su, const uint64_t* exp_tab) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, j = lane % 32, h = lane / 32;
+  const int rg = wave % RG, pg = wave / RG;
+  const float div = Q4 ? 7.0f : 127.0f;
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) {
+    const int p0 = pbase + 32 * (NTW * pg + t);
+    if (p0 >= n) break;
+    const int i = p0 + j;
+    const bool live = i < n;
+    const int ic = live ? i : n - 1;
+    const uint32_t xs = sp.asum[ic];
+    uint8_t* tabq = a.htab + (size_t)sp.pair[ic] * a.htab_bytes;
+    int nl = 1;
+    uint32_t hs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lr = 32 * rg + 8 * q + 4 * h;    // block row of 4 consecutive
+      const int row0 = rb + lr;
+      uint32_t bytes[4][4];   // [limb][r]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t dg = dots[0][t][4 * q + r], du = dots[1][t][4 * q + r];
+        if (Q4) { dg -= 8u * xs; du -= 8u * xs; }
+        const float gv = qdot_epilogue(dg, div, sg[lr + r]);
+        const float uv = qdot_epilogue(du, div, su[lr + r]);
+        const int32_t hv = f2i_trunc_x86(silu_mul_t(gv, uv, exp_tab) * div);
+        if (row0 + r < a.rows) {
+          const int nn = limbs_needed(hv);
+          nl = nn > nl ? nn : nl;
+          hs += (uint32_t)hv;
+        }
+        uint32_t b[4];
+        split_limbs(hv, b);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) bytes[l][r] = b[l];
+      }
+      if (live && row0 < a.rows) {
+        // rows row0 .. row0 + 3 (row0 % 4 == 0): Q8 4 consecutive bytes; Q4
+        // the even rows are 2 bytes in the unit's first half, the odd rows 2
+        // in its second half
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          uint8_t* plane = reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.rows, l)));
+          if constexpr (!Q4) {
+            *reinterpret_cast<uint32_t*>(plane + row0) =
+                pack4(bytes[l][0], bytes[l][1], bytes[l][2], bytes[l][3]);
+          } else {
+            const int be = unit_byte<true>(row0), bo = unit_byte<true>(row0 + 1);
+            *reinterpret_cast<uint16_t*>(plane + be) = (uint16_t)(bytes[l][0] | (bytes[l][2] << 8));
+            *reinterpret_cast<uint16_t*>(plane + bo) = (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
+          }
+        }
+      }
+      // one group of four rows at a time bounds the epilogue's registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // lanes j and j + 32 hold the same pair
+    const int o = __shfl_xor(nl, 32, kWave);
+    nl = o > nl ? o : nl;
+    hs += (uint32_t)__shfl_xor((int)hs, 32, kWave);
+    if (h == 0 && live) {
+      atomicMax(&sp.red_nl[i], nl);
+      atomicAdd(&sp.red_sum[i], hs);
+    }
+  }
+}
+
+// gate/up + SwiGLU for one row tile (32 RG rows of d_ff) of one task.
+template <bool Q4, int RG, int NTW, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  constexpr int NTH = 64 * NW;
+  constexpr int BR = 32 * RG;   // h-rows per block
+  extern __shared__ u32x4 lds_eg[];
+  __shared__ EgPairs sp;
+  __shared__ float sg[BR], su[BR];
+  __shared__ uint64_t exp_tab[32];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(lds_eg);
+  int ti, rt;
+  if (!eg_block(a.ntask, (a.rows + BR - 1) / BR, &ti, &rt)) return;
+  const int2 task = a.tasks[ti];
+  if (task.x < 0) return;
+  const int e = task.x & 0xFFFF, n = task.x >> 16, first = task.y;
+  if (n > C::NP) return;   // group_kernel splits tasks at NP pairs
+  const int tid = threadIdx.x;
+  const int rb = rt * BR;
+  if (tid < 32) exp_tab[tid] = kExp2Tab[tid];
+  for (int t2 = tid; t2 < BR; t2 += NTH) {
+    const int row = min(rb + t2, a.rows - 1);
+    sg[t2] = a.s0[(size_t)e * a.rows + row];
+    su[t2] = a.s1[(size_t)e * a.rows + row];
+  }
+  if (tid == 0) sp.nl = 1;
+  __syncthreads();
+  int nl = 1;
+  for (int i = tid; i < n; i += NTH) {
+    const int q = a.perm[first + i];
+    const uint8_t* tb = a.tab + (size_t)(q / a.topk) * a.tab_bytes;
+    sp.pair[i] = q;
+    sp.tab[i] = tb;
+    sp.asum[i] = act_asum(tb);
+    sp.red_nl[i] = 1;
+    sp.red_sum[i] = 0;
+    const int v = act_nl(tb);
+    nl = v > nl ? v : nl;
+  }
+  if (nl > 1) atomicMax(&sp.nl, nl);
+  __syncthreads();
+  // LDS row r: row group r / 64, gate (r % 64 < 32) or up, h-row rb + 32 (r
+  // / 64) + r % 32
+  const uint8_t* g0 = a.w0 + (size_t)e * a.rows * a.rb;
+  const uint8_t* u0 = a.w1 + (size_t)e * a.rows * a.rb;
+  auto wrow = [&](int r) {
+    const int row = min(rb + 32 * (r / 64) + r % 32, a.rows - 1);
+    return ((r % 64) < 32 ? g0 : u0) + (size_t)row * a.rb;
+  };
+  const int nlt = sp.nl;
+  if (nlt == 1) {
+    v16u dots[2][NTW];
+    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
+    gate_up_epi<Q4, RG, NTW>(a, sp, dots, 0, n, rb, sg, su, exp_tab);
+  } else {
+    // limb passes over half as many pairs at a time (the totals take the
+    // other half of the accumulator budget)
+    constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
+    constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
+    v16u dots[2][NTM];
+    for (int pb = 0; pb < n; pb += NPM) {
+      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
+      gate_up_epi<Q4, RG, NTM>(a, sp, dots, pb, n, rb, sg, su, exp_tab);
+    }
+  }
+  __syncthreads();
+  // this block's segment of each pair's h header
+  for (int i = tid; i < n; i += NTH) {
+    uint32_t* pp = a.hpart + ((size_t)sp.pair[i] * a.nseg + rt) * 2;
+    pp[0] = (uint32_t)sp.red_nl[i];
+    pp[1] = sp.red_sum[i];
+  }
+}
+
+// ---------------------------------------------------------------- down
+
+// y epilogue of one pass (:502-503): lane (j, h) of wave (rg, pg) holds, for
+// pair pbase + 32 (NTW pg + t) + j, the dots of rows rb + 64 rg + 32m + 8q +
+// 4h + r.
+template <bool Q4, int RG, int NTW>
+__device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, const v16u (&dots)[2][NTW],
+                                         int pbase, int n, int rb, const float* sd) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, j = lane % 32, h = lane / 32;
+  const int rg = wave % RG, pg = wave / RG;
+  const float div = Q4 ? 7.0f : 127.0f;
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) {
+    const int i = pbase + 32 * (NTW * pg + t) + j;
+    if (i >= n) continue;
+    const uint32_t hs = sp.asum[i];
+    float* yq = a.y + (size_t)sp.pair[i] * a.rows;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lr = 64 * rg + 32 * m + 8 * q + 4 * h;
+        if (rb + lr >= a.rows) continue;
+        float yv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          uint32_t d = dots[m][t][4 * q + r];
+          if (Q4) d -= 8u * hs;
+          yv[r] = qdot_epilogue(d, div, sd[lr + r]);
+        }
+        *reinterpret_cast<float4*>(yq + rb + lr) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  }
+}
+
+// down for one row tile (64 RG rows of D) of one task: y per pair.
+template <bool Q4, int RG, int NTW, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  constexpr int NTH = 64 * NW;
+  constexpr int BR = 64 * RG;   // rows per block
+  extern __shared__ u32x4 lds_eg[];
+  __shared__ EgPairs sp;
+  __shared__ float sd[BR];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(lds_eg);
+  int ti, rt;
+  if (!eg_block(a.ntask, (a.rows + BR - 1) / BR, &ti, &rt)) return;
+  const int2 task = a.tasks[ti];
+  if (task.x < 0) return;
+  const int e = task.x & 0xFFFF, n = task.x >> 16, first = task.y;
+  if (n > C::NP) return;   // group_kernel splits tasks at NP pairs
+  const int tid = threadIdx.x;
+  const int rb = rt * BR;
+  for (int r = tid; r < BR; r += NTH) sd[r] = a.s0[(size_t)e * a.rows + min(rb + r, a.rows - 1)];
+  if (tid == 0) sp.nl = 1;
+  for (int i = tid; i < n; i += NTH) {
+    sp.pair[i] = a.perm[first + i];
+    sp.red_nl[i] = 1;
+    sp.red_sum[i] = 0;
+  }
+  __syncthreads();
+  // the pairs' h headers: the sum of the segments' activation sums and the
+  // largest limb count, one (pair, segment) entry per thread
+  for (int k = tid; k < n * a.nseg; k += NTH) {
+    const int i = k / a.nseg, sg = k - i * a.nseg;
+    const uint32_t* pp = a.hpart + ((size_t)sp.pair[i] * a.nseg + sg) * 2;
+    const int v = (int)pp[0];
+    if (v > 1) atomicMax(&sp.red_nl[i], v);
+    atomicAdd(&sp.red_sum[i], pp[1]);
+  }
+  __syncthreads();
+  int nl = 1;
+  for (int i = tid; i < n; i += NTH) {
+    sp.tab[i] = a.tab + (size_t)sp.pair[i] * a.tab_bytes;
+    sp.asum[i] = sp.red_sum[i];
+    nl = sp.red_nl[i] > nl ? sp.red_nl[i] : nl;
+  }
+  if (nl > 1) atomicMax(&sp.nl, nl);
+  __syncthreads();
+  // LDS row r: row rb + r
+  const uint8_t* w0 = a.w0 + (size_t)e * a.rows * a.rb;
+  auto wrow = [&](int r) { return w0 + (size_t)min(rb + r, a.rows - 1) * a.rb; };
+  const int nlt = sp.nl;
+  if (nlt == 1) {
+    v16u dots[2][NTW];
+    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
+    down_epi<Q4, RG, NTW>(a, sp, dots, 0, n, rb, sd);
+  } else {
+    constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
+    constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
+    v16u dots[2][NTM];
+    for (int pb = 0; pb < n; pb += NPM) {
+      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
+      down_epi<Q4, RG, NTM>(a, sp, dots, pb, n, rb, sd);
+    }
+  }
+}
+
+template <class Kern>
+moe_status eg_lds_attr(Kern* fn, size_t lds, const char* what) {
+  static_assert(sizeof(Kern*) > 0, "");
+  return check_hip(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                   what);
+}
+
+// Shapes per tile count (gate/up h-rows x pairs per block): NT = 1 (few
+// pairs per expert): 128 x 32, 3 stages, two blocks per CU; NT = 2: 64 x
+// 64, 4 stages, two blocks per CU; NT = 4: 128 x 128 in eight waves, 4
+// stages, one block per CU (twice the MFMA work per stage of two 64 x 128
+// blocks, which hides more load latency; measured).
+template <bool Q4, int RG, int NTW, int D, int NW>
+moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  static bool attr = false;
+  if (!attr && C::BYTES > 65536) {
+    moe_status st = eg_lds_attr(gate_up_eg_kernel<Q4, RG, NTW, D, NW>, C::BYTES, "expert gate/up LDS attribute");
+    if (!st) st = eg_lds_attr(down_eg_kernel<Q4, RG, NTW, D, NW>, C::BYTES, "expert down LDS attribute");
+    if (st) return st;
+    attr = true;
+  }
+  const unsigned tpad = (unsigned)((ntask + 7) / 8 * 8);
+  const int nseg = (L->dff + 32 * RG - 1) / (32 * RG);
+  EgArgs g{L->gq, L->uq, L->gs, L->us, L->rbg, L->dff, L->D, L->topk, L->perm, L->tasks, ntask,
+           L->xtab, act_table_bytes(L->D), L->htab, act_table_bytes(L->dff), L->hpart, nseg,
+           nullptr};
+  hipLaunchKernelGGL((gate_up_eg_kernel<Q4, RG, NTW, D, NW>), dim3(tpad * (unsigned)nseg), dim3(64 * NW),
+                     C::BYTES, s, g);
+  moe_status st = check_hip(hipGetLastError(), "expert gate/up launch");
+  if (st) return st;
+  EgArgs d{L->dq, nullptr, L->ds, nullptr, L->rbd, L->D, L->dff, L->topk, L->perm, L->tasks, ntask,
+           L->htab, act_table_bytes(L->dff), nullptr, 0, L->hpart, nseg, L->y};
+  hipLaunchKernelGGL((down_eg_kernel<Q4, RG, NTW, D, NW>),
+                     dim3(tpad * (unsigned)((L->D + 64 * RG - 1) / (64 * RG))), dim3(64 * NW), C::BYTES,
+                     s, d);
+  return check_hip(hipGetLastError(), "expert down launch");
+}
+
+template <bool Q4>
+moe_status launch_eg(const LayerDev* L, int nt, int ntask, hipStream_t s) {
+  switch (nt) {
+    case 1: return launch_eg_shape<Q4, 4, 1, 3, 4>(L, ntask, s);
+    case 2: return launch_eg_shape<Q4, 2, 1, 4, 4>(L, ntask, s);
+    case 4: return launch_eg_shape<Q4, 4, 2, 4, 8>(L, ntask, s);
+    default: return set_error(MOE_ERR_ARG, "expert gemm: %d pair tiles", nt);
+  }
+}
+
+}  // namespace
+
+bool expert_gemm_ok(const LayerDev* L) {
+  const int cols = L->dtype == 3 ? 128 : 64;
+  return L->D % cols == 0 && L->dff % cols == 0 && L->rbg % 16 == 0 && L->rbd % 16 == 0;
+}
+
+int expert_gemm_tiles(const LayerDev* L, int T) {
+  const int mean = T * L->topk / (L->E > 0 ? L->E : 1);
+  return mean <= 24 ? 1 : (mean <= 64 ? 2 : 4);
+}
+
+moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s) {
+  if (L->dtype == 3)
+    hipLaunchKernelGGL(pack_units_kernel<true>, dim3((unsigned)T), dim3(256), 0, s, x, L->D, L->xtab,
+                       act_table_bytes(L->D));
+  else
+    hipLaunchKernelGGL(pack_units_kernel<false>, dim3((unsigned)T), dim3(256), 0, s, x, L->D, L->xtab,
+                       act_table_bytes(L->D));
+  return check_hip(hipGetLastError(), "unit table launch");
+}
+
+moe_status launch_expert_gemm(const LayerDev* L, int nt, int ntask, hipStream_t s) {
+  return L->dtype == 3 ? launch_eg<true>(L, nt, ntask, s) : launch_eg<false>(L, nt, ntask, s);
+}
+
+}  // namespace moe

@@ -114,20 +114,21 @@ __constant__ static const uint64_t kExp2Tab[32] = {
 
 // tab: the 32 table entries (kExp2Tab or a copy, e.g. in LDS, which a
 // kernel that evaluates many expf per lane reads with less latency).
+// Branch-free: the polynomial path runs for every x (its table index is
+// ki % 32, in range for any input) and the published special cases are
+// selected afterwards -- NaN and +inf give x + x, x above the overflow
+// threshold +inf, x below the underflow threshold (-inf included) +0 --
+// so that many evaluations per lane schedule together instead of each in
+// its own divergent region.
 __device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   constexpr double kShift = 0x1.8p+52;
   constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
   constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
   constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  const uint32_t ux = __float_as_uint(x);
-  const uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= 0x42bu) {                      // |x| >= 88 or x is NaN/inf
-    if (ux == 0xff800000u) return 0.0f;        // expf(-inf)
-    if (abstop >= 0x7f8u) return x + x;        // +inf or NaN
-    if (x > 0x1.62e42ep6f) return __builtin_inff();
-    if (x < -0x1.9fe368p6f) return 0.0f;
-  }
+  const float special = x != x ? x + x
+                      : x > 0x1.62e42ep6f ? __builtin_inff()
+                      : x < -0x1.9fe368p6f ? 0.0f : -1.0f;
   const double xd = (double)x;
   double kd = __builtin_fma(kInvLn2N, xd, kShift);
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
@@ -141,7 +142,7 @@ __device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
   double y = __builtin_fma(kC2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  return (float)y;
+  return special == -1.0f ? (float)y : special;
 }
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }

@@ -11,9 +11,11 @@ namespace moe {
 
 constexpr int kMaxTopK = 32;
 
-// Pairs of one expert that one block of the weight-stationary grouped
-// kernels takes at most (an expert with more is split over several blocks).
-constexpr int kWsSplitPairs = 256;
+// Pairs of one expert per block of the grouped GEMM kernels (expert_gemm.hip)
+// at most: 32 per pair tile, 1, 2 or 4 tiles.
+constexpr int kEgPairs = 128;
+// The smallest task split (sizes the task list).
+constexpr int kMinSplitPairs = 32;
 
 struct LayerDev {
   int dtype = 2, D = 0, dff = 0, E = 0, topk = 0;
@@ -43,10 +45,8 @@ struct LayerDev {
   int* ecount = nullptr;     // [E]
   int* eoff = nullptr;       // [E]
   int* perm = nullptr;       // [T*topk]
-  int* wsflag = nullptr;     // [2][E] experts left to the streaming gate/up, down kernels
-  int2* tasks = nullptr;     // [T*topk/kWsSplitPairs + E + 1] tasks of the weight-stationary
-                             // kernels: {expert | pairs << 16, first pair in perm}, x = -1 past
-                             // the last
+  int2* tasks = nullptr;     // [T*topk/kMinSplitPairs + E + 1] tasks of the expert kernels:
+                             // {expert | pairs << 16, first pair in perm}, x = -1 past the last
   float* y = nullptr;        // [T*topk][D]
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };
@@ -59,6 +59,15 @@ moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_ou
 bool grouped_ok(const LayerDev* L);
 moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
                                  float* out, int32_t* idx_out, float* p_out);
+
+// The grouped GEMM expert kernels (expert_gemm.hip): x unit tables into
+// L->xtab; gate/up + SwiGLU into L->htab / L->hpart (one segment per row
+// tile of d_ff), then down into L->y, for the tasks group_kernel listed with
+// a split of 32 * nt pairs (nt = expert_gemm_tiles).
+bool expert_gemm_ok(const LayerDev* L);
+int expert_gemm_tiles(const LayerDev* L, int T);
+moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s);
+moe_status launch_expert_gemm(const LayerDev* L, int nt, int ntask, hipStream_t s);
 
 // ---- routing: top-k by the insertion rule, softmax over the selection ----
 
