@@ -423,33 +423,34 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
       }
     }
     __syncthreads();
-    // this block's column slice [c0, c1) (a multiple of 8 columns)
-    const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
-    const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
-    if (a.xn_out)
-      for (int i = c0 + tid; i < c1; i += kRowThreads) a.xn_out[i] = xs[i];
-    if constexpr (PACK != 0) {
-      if (tid == 0) { pack_scratch[0] = 1; pack_scratch[1] = 0; }
-      __syncthreads();
-      int nl;
-      uint32_t sum;
-      pack_act_cols<PACK == 3>(xs, K, c0, c1, a.pack_tabs, tid, kRowThreads, nl, sum);
+  }
+  // this block's column slice [c0, c1) (a multiple of 8 columns) of the
+  // (normalized) row: to xn_out, and packed into the x tables' planes
+  const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
+  const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
+  if (NORM && a.xn_out)
+    for (int i = c0 + tid; i < c1; i += kRowThreads) a.xn_out[i] = xs[i];
+  if constexpr (PACK != 0) {
+    if (tid == 0) { pack_scratch[0] = 1; pack_scratch[1] = 0; }
+    __syncthreads();
+    int nl;
+    uint32_t sum;
+    pack_act_cols<PACK == 3>(xs, K, c0, c1, a.pack_tabs, tid, kRowThreads, nl, sum);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const int on = __shfl_xor(nl, off, kWave);
-        nl = on > nl ? on : nl;
-        sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
-      }
-      if (lane == 0) {
-        atomicMax(&pack_scratch[0], nl);
-        atomicAdd(reinterpret_cast<unsigned*>(&pack_scratch[1]), sum);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t* pp = a.pack_part + (size_t)blockIdx.x * 2;
-        pp[0] = (uint32_t)pack_scratch[0];
-        pp[1] = (uint32_t)pack_scratch[1];
-      }
+    for (int off = 32; off > 0; off >>= 1) {
+      const int on = __shfl_xor(nl, off, kWave);
+      nl = on > nl ? on : nl;
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    }
+    if (lane == 0) {
+      atomicMax(&pack_scratch[0], nl);
+      atomicAdd(reinterpret_cast<unsigned*>(&pack_scratch[1]), sum);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t* pp = a.pack_part + (size_t)blockIdx.x * 2;
+      pp[0] = (uint32_t)pack_scratch[0];
+      pp[1] = (uint32_t)pack_scratch[1];
     }
   }
   // products x[k] * W[n][k], then their sum in column order
@@ -1460,7 +1461,13 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(dense_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), "dense generic launch");
   }
-  if (dense_row_ok(a, vec)) return launch_row<false, 0>(a, s);
+  if (a.pack_dtype && (!a.sel_counter || !a.pack_part || !a.pack_tabs || !dense_row_ok(a, vec)))
+    return set_error(MOE_ERR_ARG, "dense matmul: packing a given row needs the row kernel and the fused selection");
+  if (dense_row_ok(a, vec)) {
+    if (a.pack_dtype == 2) return launch_row<false, 2>(a, s);
+    if (a.pack_dtype == 3) return launch_row<false, 3>(a, s);
+    return launch_row<false, 0>(a, s);
+  }
   if (a.sel_counter) {
     if (!vec) return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs aligned rows");
     return a.M == 1 ? launch_gemv<16, false, 0, kNpOne>(a, s) : launch_gemv<16, false, 0, 1>(a, s);

@@ -484,11 +484,18 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
   if (grouped) return layer_forward_grouped(L, xn, resid, T, out, idx_out, p_out);
   const bool q4 = L->dtype == 3;
   DenseArgs ra{xn, L->D, L->router_w, L->D, L->router_b, nullptr, 0, L->logits, L->E, T, L->E, L->D};
+  // router logits (+ bias), then top-k and gates (in the router launch's
+  // last block for few tokens)
+  const bool fuse_sel = dense_select_ok(T, L->E) && aligned16(L->router_w) &&
+                        (fuse_norm || aligned16(xn));
   if (fuse_norm) {
     // rmsnorm + x tables + router logits in one launch
     ra.norm = 1; ra.norm_w = L->rms2_w; ra.eps = norm_eps;
     ra.xn_out = L->xn; ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
     xn = L->xn;
+  } else if (fuse_sel && T == 1 && dense_row_path(ra)) {
+    // one given row: the router's row kernel packs the x tables too
+    ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
   } else {
     // x tables for the expert GEMVs
     QShape sh;
@@ -496,10 +503,6 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
     QJob one{nullptr, nullptr, xn, nullptr};
     if ((st = check_hip(launch_act_pack(sh, nullptr, one, 1, L->xtab, s), "act pack"))) return st;
   }
-  // router logits (+ bias), then top-k and gates (in the router launch's
-  // last block for few tokens)
-  const bool fuse_sel = dense_select_ok(T, L->E) && aligned16(L->router_w) &&
-                        (fuse_norm || aligned16(xn));
   if (fuse_sel) {
     ra.sel_counter = L->sel_counter; ra.sel_topk = L->topk;
     ra.sel_idx = L->idx; ra.sel_p = L->p; ra.sel_idx_user = idx_out; ra.sel_p_user = p_out;
