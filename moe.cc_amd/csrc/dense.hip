@@ -1376,8 +1376,8 @@ moe_status launch_tile(const DenseArgs& a, hipStream_t s) {
 
 // Producer waves of the few-token GEMV: three for one token (the LDS of four
 // product buffers fits), one otherwise; the wide one-token products (the
-// vocabulary head) keep MOEHIP_HEAD_NP... three as well: their rows stream
-// from HBM and more producers keep more bytes in flight.
+// vocabulary head) keep three as well: their rows stream from HBM and more
+// producers keep more bytes in flight.
 constexpr int kNpOne = 3;
 constexpr int kNpWide = 3;
 

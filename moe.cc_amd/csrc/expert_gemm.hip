@@ -463,8 +463,6 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const 
           }
         }
       }
-      // one group of four rows at a time bounds the epilogue's registers
-      __builtin_amdgcn_sched_barrier(0);
     }
     // lanes j and j + 32 hold the same pair
     const int o = __shfl_xor(nl, 32, kWave);

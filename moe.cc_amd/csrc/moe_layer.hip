@@ -110,7 +110,9 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   const int q = blockIdx.y;
   int e;
   int x_nl = 0;
-  uint32_t x_sum[1] = {0u};
+  // the token's activation sum, handed to the row streaming by address: in
+  // LDS (a local array whose address is taken would live in scratch memory)
+  __shared__ uint32_t x_sum[1];
   if constexpr (SEL) {
     __shared__ __align__(16) uint64_t keys[kTileBlock];
     __shared__ int part[kTileBlock];
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     __syncthreads();
     // (no partials: the table's header was written by its own pack kernel)
     x_nl = a.nxpart > 0 ? xred[0] : 0;
-    x_sum[0] = (uint32_t)xred[1];
+    x_sum[0] = (uint32_t)xred[1];   // every thread stores the same value before reading it
     e = sidx[q];
     if (blockIdx.x == 0 && q == 0) {
       if (tid < kWave)
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
       if (tid == 0 && a.nxpart > 0) {
         uint32_t* hh = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(a.xtab));
         hh[0] = (uint32_t)x_nl;
-        hh[1] = x_sum[0];
+        hh[1] = (uint32_t)xred[1];
       }
     }
   } else {

@@ -235,12 +235,19 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     (3, 17, 64, 1024, 512, False, True, 40.0),   # 2-limb Q4 activations
     (2, 9, 64, 1024, 256, True, True, 400.0),    # 4-limb Q8 activations (and h)
     (3, 70, 8, 512, 256, False, True, 3000.0),   # 4-limb Q4, > 32 pairs per expert
-    # E = top-k: every expert takes every token, > 256 pairs each, so the
-    # weight-stationary kernels split each expert over several blocks
+    # E = top-k: every expert takes every token, > 256 pairs each, so each
+    # expert's pairs split into several tasks (blocks)
     (3, 300, 8, 512, 256, False, True, 1.0),
-    (3, 520, 8, 256, 256, False, True, 40.0),    # split and flagged (2-limb Q4)
+    (3, 520, 8, 256, 256, False, True, 40.0),    # split, 2-limb Q4
     (2, 280, 8, 512, 256, True, True, 0.3),      # split, one-limb Q8
     (3, 2048, 8, 256, 256, False, True, 1.0),    # router with two token chains per lane
+    # the config shape's D = 2048 and d_ff = 768 (16 and 6 stages of the LDS
+    # ring), 16 experts so that 128 pairs per expert on average select the
+    # four-tile, eight-wave blocks (the prefill bench's T = 2048 shape)
+    (3, 256, 16, 2048, 768, False, True, 1.0),
+    # Q8 at D = 2048, d_ff = 768: x ~ N(0, 1) needs two limbs, so every task
+    # runs limb passes folded into one dot (two-tile blocks)
+    (2, 128, 16, 2048, 768, True, True, 1.0),
 ]
 
 
