@@ -2,23 +2,22 @@
 // grouped integer GEMMs on v_mfma_i32_32x32x32_i8 (gfx950), bit-identical to
 // the per-(token, rank) GEMVs of test_model_trace.c:496-503.
 //
-// One block (four waves) takes one task -- up to 32*NT (token, rank) pairs
-// routed to one expert, listed by group_kernel -- and one tile of rows:
-//   gate/up  128 rows of d_ff in both matrices: wave w owns gate and up rows
-//            32w .. 32w + 31, so a lane holds g and u of the same (row, pair)
-//            for the SwiGLU epilogue (:496-501)
-//   down     256 rows of D: wave w owns rows 64w .. 64w + 63
+// A block takes one task -- up to NP (token, rank) pairs routed to one
+// expert, listed by group_kernel -- and one tile of rows.  Its waves form RG
+// row groups x PG pair groups; a wave holds 64 weight rows (gate/up: 32
+// gate and the same 32 up rows, so a lane holds g and u of one (row, pair)
+// for the SwiGLU epilogue (:496-501); down: two 32-row tiles) and NTW pair
+// tiles of 32 (tile t of pair group pg is the task's tile t * PG + pg).
+// Tiles past the task's pairs skip their MFMAs and epilogue.
 // K runs outermost in stages of 64 weight bytes per row (128 Q4 columns or
-// 64 Q8 columns).  Both operands go straight from memory into a four-stage
-// LDS ring with global_load_lds_dwordx4 (three stages ahead, no registers):
-// each wave's own 64 weight rows, and the pairs' activation units (16 bytes
-// of one limb plane), which the four waves share.  Both are XOR-swizzled so
-// that the MFMA operand reads are free of bank conflicts.  One barrier per
-// stage; the wait before it counts this wave's loads.
-// Every unpacked weight operand feeds all NT pair tiles, so the Q4 nibble
-// unpack costs 6 VALU per 2*NT MFMAs, and each weight byte leaves HBM once
-// per task.  NT (1, 2, 4) is chosen per launch from the mean pairs per
-// expert; tiles past a task's pairs repeat its last pair and are dropped.
+// 64 Q8 columns).  Both operands go straight from memory into a D-stage
+// LDS ring with global_load_lds_dwordx4 (D - 1 stages ahead, no
+// registers): the block's weight rows and the pairs' activation units (16
+// bytes of one limb plane), which all waves share.  Both are XOR-swizzled
+// so that the MFMA operand reads are free of bank conflicts.  One barrier
+// per stage; the wait before it counts this wave's loads.
+// Every unpacked weight operand feeds the wave's NTW pair tiles, and each
+// weight byte leaves memory once per task.
 //
 // The integer dots are exact in any order.  A quantized activation a is
 // split into int8 limbs a = sum_l b_l 256^l; a task whose activations need
@@ -175,11 +174,12 @@ struct EgPairs {
   int nl;
 };
 
-// Block shape: RG row groups x (4 / RG) pair groups of waves.  Wave w is
-// row group w % RG (64 weight rows: gate rows 0-31 and up rows 32-63 of its
-// 32 h-rows for gate/up, two 32-row tiles for down) and pair group w / RG
-// (NTW tiles of 32 pairs).  A pass covers NP = 32 * NTW * (4 / RG) pairs;
-// D stages in the LDS ring.  LDS layout of one stage:
+// Block shape: RG row groups x PG = NW / RG pair groups of NW waves.  Wave
+// w is row group w % RG (64 weight rows: gate rows 0-31 and up rows 32-63
+// of its 32 h-rows for gate/up, two 32-row tiles for down) and pair group w
+// / RG (NTW tiles of 32 pairs).  A pass covers NP = 32 * NTW * PG pairs; D
+// stages in the LDS ring.  LDS layout of one stage (pair row r = the pass's
+// pair r):
 //   W  64 * RG weight rows x 64 bytes, 16-byte chunk c of row r in slot
 //      c ^ wswz(r);
 //   B  NP pair rows x ROWB bytes, unit u of pair row r in slot u ^ swz(r).
@@ -251,7 +251,9 @@ __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const
 
 // Loads stage st into buffer buf.  Every wave issues Q loads (a wave past
 // the last B instruction repeats one another wave issued: the same bytes to
-// the same place).
+// the same place).  Pair rows past the task's pairs repeat its last pair
+// (one more read of bytes already in cache; a smaller stand-in load was
+// measured slower).
 template <bool Q4, class C>
 __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint8_t* buf) {
   using SG = EgStage<Q4>;
@@ -290,8 +292,8 @@ __device__ __forceinline__ WFrag32 w_frag(const uint8_t* wbuf, int m) {
 
 // One stage of a pass: wait for stage st, issue stage st + D - 1 (clamped to
 // the last stage, then rotated) into its ring buffer, then the MFMAs of
-// stage st: acc[m][t] for this wave's pair tiles t.
-template <bool Q4, int RG, int NTW, int D, int NW>
+// stage st: acc[m][t] for this wave's live pair tiles t < NL.
+template <bool Q4, int RG, int NTW, int D, int NW, int NL>
 __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int st,
                                          int nst, int rot, uint8_t* lds, v16i (&acc)[2][NTW]) {
   using SG = EgStage<Q4>;
@@ -301,20 +303,44 @@ __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, N
   stage_load<Q4, C>(src, (min(st + D - 1, nst - 1) + rot) % nst, lds + ((st + D - 1) % D) * C::STAGE);
   const uint8_t* buf = lds + (st % D) * C::STAGE;
   const WFrag32 f0 = w_frag<RG>(buf, 0), f1 = w_frag<RG>(buf, 1);
-  const uint8_t* B = buf + C::W_BYTES + (32 * NTW * pg + j) * SG::ROWB;
-  const int sw = swz<Q4>(j);   // = swz(32t + j) for every tile t
+  const uint8_t* B = buf + C::W_BYTES + (32 * pg + j) * SG::ROWB;
+  const int sw = swz<Q4>(j);   // = swz(32 tile + j) for every tile
 #pragma unroll
   for (int s = 0; s < SG::S; ++s) {
     const v4i a0 = a_op<Q4>(f0, s);
     const v4i a1 = a_op<Q4>(f1, s);
     const int slot = (h * SG::S + s) ^ sw;
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) {
-      const v4i b = *reinterpret_cast<const v4i*>(B + 32 * t * SG::ROWB + slot * 16);
+    for (int t = 0; t < NL; ++t) {
+      const v4i b = *reinterpret_cast<const v4i*>(B + 32 * C::PG * t * SG::ROWB + slot * 16);
       acc[0][t] = mfma32(a0, b, acc[0][t]);
       acc[1][t] = mfma32(a1, b, acc[1][t]);
     }
   }
+}
+
+// The stage loop of a wave with NL live tiles; NL is chosen once per pass
+// (live_tiles), so that the MFMA sequence of a stage has no branches.
+template <bool Q4, int RG, int NTW, int D, int NW, int NL>
+__device__ __forceinline__ void eg_loop(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int nst, int rot,
+                                        int ntl, uint8_t* lds, v16i (&acc)[2][NTW]) {
+  if constexpr (NL > 0) {
+    if (ntl < NL) {
+      eg_loop<Q4, RG, NTW, D, NW, NL - 1>(src, nst, rot, ntl, lds, acc);
+      return;
+    }
+  }
+  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW, NL>(src, st, nst, rot, lds, acc);
+}
+
+// Live pair tiles of this wave in a pass over pairs pbase .. n - 1: tiles t
+// with 32 (t PG + pg) < n - pbase.  The same for every lane of the wave.
+template <int PG, int NTW>
+__device__ __forceinline__ int live_tiles(int pbase, int n, int pg) {
+  const int live = n - pbase;   // >= 1
+  const int tiles = (live + 31) / 32;
+  const int t = (tiles - pg + PG - 1) / PG;
+  return __builtin_amdgcn_readfirstlane(min(max(t, 0), NTW));
 }
 
 // acc[m][t] = sum over all K columns of W_m[lane's row] x limb l of pair
@@ -327,6 +353,7 @@ __device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, i
   using SG = EgStage<Q4>;
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   const int nst = K / SG::COLS;
+  const int ntl = live_tiles<C::PG, NTW>(pbase, n, (threadIdx.x / kWave) / RG);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -339,7 +366,7 @@ __device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, i
   const int rot = (int)(blockIdx.x % (unsigned)nst);
 #pragma unroll
   for (int p = 0; p < D - 1; ++p) stage_load<Q4, C>(src, (min(p, nst - 1) + rot) % nst, lds + p * C::STAGE);
-  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW>(src, st, nst, rot, lds, acc);
+  eg_loop<Q4, RG, NTW, D, NW, NTW>(src, nst, rot, ntl, lds, acc);
   // the clamped loads past the last stage land before the ring is reused
   stage_sync<0>();
 }
@@ -402,11 +429,11 @@ __device__ __forceinline__ bool eg_block(int ntask, int nrt, int* task, int* rt)
 // ---------------------------------------------------------------- gate/up
 
 // SwiGLU epilogue of one pass (:496-501): lane (j, h) of wave (rg, pg) holds,
-// for pair pbase + 32 (NTW pg + t) + j, gate and up dots of rows rb + 32 rg
-// + 8q + 4h + r.  h = (g / (1 + expf(-g))) * u is quantized for down and
+// for pair pbase + 32 (t PG + pg) + j, gate and up dots of rows rb + 32 rg +
+// 8q + 4h + r.  h = (g / (1 + expf(-g))) * u is quantized for down and
 // written into the pair's h table; the rows' limb count and activation sum
 // go to red_nl / red_sum.
-template <bool Q4, int RG, int NTW>
+template <bool Q4, int RG, int PG, int NTW>
 __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const v16u (&dots)[2][NTW],
                                             int pbase, int n, int rb, const float* sg,
                                             const float* su, const uint64_t* exp_tab) {
@@ -415,7 +442,7 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const 
   const float div = Q4 ? 7.0f : 127.0f;
 #pragma unroll
   for (int t = 0; t < NTW; ++t) {
-    const int p0 = pbase + 32 * (NTW * pg + t);
+    const int p0 = pbase + 32 * (PG * t + pg);
     if (p0 >= n) break;
     const int i = p0 + j;
     const bool live = i < n;
@@ -436,11 +463,10 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const 
         const float gv = qdot_epilogue(dg, div, sg[lr + r]);
         const float uv = qdot_epilogue(du, div, su[lr + r]);
         const int32_t hv = f2i_trunc_x86(silu_mul_t(gv, uv, exp_tab) * div);
-        if (row0 + r < a.rows) {
-          const int nn = limbs_needed(hv);
-          nl = nn > nl ? nn : nl;
-          hs += (uint32_t)hv;
-        }
+        const bool row_ok = row0 + r < a.rows;
+        const int nn = row_ok ? limbs_needed(hv) : 1;
+        nl = nn > nl ? nn : nl;
+        hs += row_ok ? (uint32_t)hv : 0u;
         uint32_t b[4];
         split_limbs(hv, b);
 #pragma unroll
@@ -528,7 +554,7 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
   if (nlt == 1) {
     v16u dots[2][NTW];
     eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
-    gate_up_epi<Q4, RG, NTW>(a, sp, dots, 0, n, rb, sg, su, exp_tab);
+    gate_up_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb, sg, su, exp_tab);
   } else {
     // limb passes over half as many pairs at a time (the totals take the
     // other half of the accumulator budget)
@@ -537,7 +563,7 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
     v16u dots[2][NTM];
     for (int pb = 0; pb < n; pb += NPM) {
       eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
-      gate_up_epi<Q4, RG, NTM>(a, sp, dots, pb, n, rb, sg, su, exp_tab);
+      gate_up_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sg, su, exp_tab);
     }
   }
   __syncthreads();
@@ -552,9 +578,9 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
 // ---------------------------------------------------------------- down
 
 // y epilogue of one pass (:502-503): lane (j, h) of wave (rg, pg) holds, for
-// pair pbase + 32 (NTW pg + t) + j, the dots of rows rb + 64 rg + 32m + 8q +
+// pair pbase + 32 (t PG + pg) + j, the dots of rows rb + 64 rg + 32m + 8q +
 // 4h + r.
-template <bool Q4, int RG, int NTW>
+template <bool Q4, int RG, int PG, int NTW>
 __device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, const v16u (&dots)[2][NTW],
                                          int pbase, int n, int rb, const float* sd) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, j = lane % 32, h = lane / 32;
@@ -562,7 +588,7 @@ __device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, con
   const float div = Q4 ? 7.0f : 127.0f;
 #pragma unroll
   for (int t = 0; t < NTW; ++t) {
-    const int i = pbase + 32 * (NTW * pg + t) + j;
+    const int i = pbase + 32 * (PG * t + pg) + j;
     if (i >= n) continue;
     const uint32_t hs = sp.asum[i];
     float* yq = a.y + (size_t)sp.pair[i] * a.rows;
@@ -636,14 +662,14 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   if (nlt == 1) {
     v16u dots[2][NTW];
     eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
-    down_epi<Q4, RG, NTW>(a, sp, dots, 0, n, rb, sd);
+    down_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb, sd);
   } else {
     constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
     constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
     v16u dots[2][NTM];
     for (int pb = 0; pb < n; pb += NPM) {
       eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
-      down_epi<Q4, RG, NTM>(a, sp, dots, pb, n, rb, sd);
+      down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sd);
     }
   }
 }
@@ -655,11 +681,12 @@ moe_status eg_lds_attr(Kern* fn, size_t lds, const char* what) {
                    what);
 }
 
-// Shapes per tile count (gate/up h-rows x pairs per block): NT = 1 (few
+// Shapes per tile count (gate/up h-rows x pairs per task): NT = 1 (few
 // pairs per expert): 128 x 32, 3 stages, two blocks per CU; NT = 2: 64 x
-// 64, 4 stages, two blocks per CU; NT = 4: 128 x 128 in eight waves, 4
-// stages, one block per CU (twice the MFMA work per stage of two 64 x 128
-// blocks, which hides more load latency; measured).
+// 64, 4 stages, two blocks per CU; NT = 4: 128 x 256 in eight waves (four
+// tiles each, those past the task's pairs skipped), 3 stages, one block per
+// CU: one task per expert up to 256 pairs, so that an expert's weights
+// are read once even when its pairs outnumber one pass of 128.
 template <bool Q4, int RG, int NTW, int D, int NW>
 moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
   using C = EgCfg<Q4, RG, NTW, D, NW>;
@@ -692,7 +719,7 @@ moe_status launch_eg(const LayerDev* L, int nt, int ntask, hipStream_t s) {
   switch (nt) {
     case 1: return launch_eg_shape<Q4, 4, 1, 3, 4>(L, ntask, s);
     case 2: return launch_eg_shape<Q4, 2, 1, 4, 4>(L, ntask, s);
-    case 4: return launch_eg_shape<Q4, 4, 2, 4, 8>(L, ntask, s);
+    case 4: return launch_eg_shape<Q4, 4, 4, 3, 8>(L, ntask, s);
     default: return set_error(MOE_ERR_ARG, "expert gemm: %d pair tiles", nt);
   }
 }
@@ -708,6 +735,8 @@ int expert_gemm_tiles(const LayerDev* L, int T) {
   const int mean = T * L->topk / (L->E > 0 ? L->E : 1);
   return mean <= 24 ? 1 : (mean <= 64 ? 2 : 4);
 }
+
+int expert_gemm_split(int nt) { return nt == 4 ? 256 : 32 * nt; }
 
 moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s) {
   if (L->dtype == 3)

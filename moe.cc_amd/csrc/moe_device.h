@@ -28,9 +28,9 @@ __device__ __forceinline__ int32_t f2i_trunc_x86(float v) {
 //   represent every int32 modulo 2^32 (all the dot product needs, since the
 //   reference accumulates in wrapping int32).
 __device__ __forceinline__ int limbs_needed(int32_t a) {
-  if (a >= -128 && a <= 127) return 1;
-  if (a >= -32896 && a <= 32639) return 2;
-  return 4;
+  const uint32_t u = (uint32_t)a;
+  const int n2 = u + 32896u < 65536u ? 2 : 4;   // a in [-32896, 32639]
+  return u + 128u < 256u ? 1 : n2;             // a in [-128, 127]
 }
 
 // Splits a into 4 signed bytes (least significant first) with
@@ -115,20 +115,17 @@ __constant__ static const uint64_t kExp2Tab[32] = {
 // tab: the 32 table entries (kExp2Tab or a copy, e.g. in LDS, which a
 // kernel that evaluates many expf per lane reads with less latency).
 // Branch-free: the polynomial path runs for every x (its table index is
-// ki % 32, in range for any input) and the published special cases are
-// selected afterwards -- NaN and +inf give x + x, x above the overflow
-// threshold +inf, x below the underflow threshold (-inf included) +0 --
-// so that many evaluations per lane schedule together instead of each in
-// its own divergent region.
+// ki % 32, in range for any input) and the published special cases replace
+// its result afterwards, one select each -- x above the overflow threshold
+// (+inf included) +inf, x below the underflow threshold (-inf included) +0,
+// NaN x + x -- so that many evaluations per lane schedule together instead
+// of each in its own divergent region.
 __device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   constexpr double kShift = 0x1.8p+52;
   constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
   constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
   constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  const float special = x != x ? x + x
-                      : x > 0x1.62e42ep6f ? __builtin_inff()
-                      : x < -0x1.9fe368p6f ? 0.0f : -1.0f;
   const double xd = (double)x;
   double kd = __builtin_fma(kInvLn2N, xd, kShift);
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
@@ -142,7 +139,10 @@ __device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
   double y = __builtin_fma(kC2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  return special == -1.0f ? (float)y : special;
+  float e = (float)y;
+  e = x > 0x1.62e42ep6f ? __builtin_inff() : e;
+  e = x < -0x1.9fe368p6f ? 0.0f : e;
+  return x != x ? x + x : e;
 }
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }

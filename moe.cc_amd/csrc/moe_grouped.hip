@@ -385,10 +385,10 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   if (st) return st;
   // 3. top-k and gates
   if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
-  // 4. group pairs by expert, tasks of at most 32 * nt pairs
+  // 4. group pairs by expert, tasks of at most one block's pairs
   const int npairs = T * L->topk;
   const int nt = expert_gemm_tiles(L, T);
-  const int split = 32 * nt;
+  const int split = expert_gemm_split(nt);
   const int ntask_max = npairs / split + L->E + 1;
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
                      L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);

@@ -11,9 +11,9 @@ namespace moe {
 
 constexpr int kMaxTopK = 32;
 
-// Pairs of one expert per block of the grouped GEMM kernels (expert_gemm.hip)
-// at most: 32 per pair tile, 1, 2 or 4 tiles.
-constexpr int kEgPairs = 128;
+// Pairs of one task (one expert) of the grouped GEMM kernels
+// (expert_gemm.hip) at most: 32, 64 or 256 by block shape.
+constexpr int kEgPairs = 256;
 // The smallest task split (sizes the task list).
 constexpr int kMinSplitPairs = 32;
 
@@ -63,9 +63,11 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
 // The grouped GEMM expert kernels (expert_gemm.hip): x unit tables into
 // L->xtab; gate/up + SwiGLU into L->htab / L->hpart (one segment per row
 // tile of d_ff), then down into L->y, for the tasks group_kernel listed with
-// a split of 32 * nt pairs (nt = expert_gemm_tiles).
+// a split of expert_gemm_split(nt) pairs (nt = expert_gemm_tiles, the block
+// shape).
 bool expert_gemm_ok(const LayerDev* L);
 int expert_gemm_tiles(const LayerDev* L, int T);
+int expert_gemm_split(int nt);
 moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s);
 moe_status launch_expert_gemm(const LayerDev* L, int nt, int ntask, hipStream_t s);
 
