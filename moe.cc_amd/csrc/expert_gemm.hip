@@ -219,6 +219,11 @@ __device__ __forceinline__ void lds_load16(const void* src, uint8_t* lds) {
 #pragma clang diagnostic pop
 }
 
+// Sixteen zero bytes: the B source of an h-table unit whose segment's values
+// needed fewer limbs than the pass's limb (the gate/up epilogue writes only
+// the planes a segment needs).
+__device__ __align__(16) const uint8_t kEgZero[16] = {};
+
 // This lane's load sources of a pass, at column 0: its weight chunks (LDS
 // row 16 * ins + lane / 4, slot lane % 4, for the wave's instructions ins =
 // wave + 4k) and its B units (limb plane l of pair row ins * RPI + lane /
@@ -227,11 +232,13 @@ template <bool Q4, class C>
 struct EgSrc {
   const uint8_t* w[C::PERW];
   const uint8_t* b[C::PERB];
+  uint32_t segs[C::PERB];   // SEGM passes: segments whose plane holds this B row's limb
+  int col[C::PERB];         // column of this lane's B unit within a stage
 };
 
 template <bool Q4, class C, class WRow>
 __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const EgPairs& sp,
-                                           int pbase, int n, int K, int l) {
+                                           int pbase, int n, int K, int l, const uint32_t* segmask) {
   using SG = EgStage<Q4>;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
@@ -246,6 +253,8 @@ __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const
     const int unit = (lane % SG::UNITS) ^ swz<Q4>(row);
     const int q = min(pbase + row, n - 1);
     src.b[k] = reinterpret_cast<const uint8_t*>(act_plane(sp.tab[q], K, l)) + unit * 16;
+    src.segs[k] = segmask && l > 0 ? segmask[(l - 1) * kEgPairs + q] : ~0u;
+    src.col[k] = unit * 16;
   }
 }
 
@@ -253,8 +262,9 @@ __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const
 // the last B instruction repeats one another wave issued: the same bytes to
 // the same place).  Pair rows past the task's pairs repeat its last pair
 // (one more read of bytes already in cache; a smaller stand-in load was
-// measured slower).
-template <bool Q4, class C>
+// measured slower).  SEGM: a B unit in a segment of BRS columns outside
+// src.segs loads kEgZero.
+template <bool Q4, class C, bool SEGM, int BRS>
 __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint8_t* buf) {
   using SG = EgStage<Q4>;
   const int wave = threadIdx.x / kWave;
@@ -264,7 +274,12 @@ __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint
 #pragma unroll
   for (int k = 0; k < C::PERB; ++k) {
     const int ins = (wave + C::W * k) % C::NIB;
-    lds_load16(src.b[k] + (size_t)st * SG::UNITS * 16, buf + C::W_BYTES + ins * 1024);
+    const uint8_t* b = src.b[k] + (size_t)st * SG::UNITS * 16;
+    if constexpr (SEGM) {
+      const int seg = (st * SG::COLS + src.col[k]) / BRS;
+      b = (src.segs[k] >> seg) & 1u ? b : kEgZero;
+    }
+    lds_load16(b, buf + C::W_BYTES + ins * 1024);
   }
 }
 
@@ -293,14 +308,15 @@ __device__ __forceinline__ WFrag32 w_frag(const uint8_t* wbuf, int m) {
 // One stage of a pass: wait for stage st, issue stage st + D - 1 (clamped to
 // the last stage, then rotated) into its ring buffer, then the MFMAs of
 // stage st: acc[m][t] for this wave's live pair tiles t < NL.
-template <bool Q4, int RG, int NTW, int D, int NW, int NL>
+template <bool Q4, int RG, int NTW, int D, int NW, int NL, bool SEGM>
 __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int st,
                                          int nst, int rot, uint8_t* lds, v16i (&acc)[2][NTW]) {
   using SG = EgStage<Q4>;
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   const int lane = threadIdx.x % kWave, pg = (threadIdx.x / kWave) / RG, j = lane % 32, h = lane / 32;
   stage_sync<(D - 2) * C::Q>();
-  stage_load<Q4, C>(src, (min(st + D - 1, nst - 1) + rot) % nst, lds + ((st + D - 1) % D) * C::STAGE);
+  stage_load<Q4, C, SEGM, 32 * RG>(src, (min(st + D - 1, nst - 1) + rot) % nst,
+                                   lds + ((st + D - 1) % D) * C::STAGE);
   const uint8_t* buf = lds + (st % D) * C::STAGE;
   const WFrag32 f0 = w_frag<RG>(buf, 0), f1 = w_frag<RG>(buf, 1);
   const uint8_t* B = buf + C::W_BYTES + (32 * pg + j) * SG::ROWB;
@@ -321,16 +337,16 @@ __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, N
 
 // The stage loop of a wave with NL live tiles; NL is chosen once per pass
 // (live_tiles), so that the MFMA sequence of a stage has no branches.
-template <bool Q4, int RG, int NTW, int D, int NW, int NL>
+template <bool Q4, int RG, int NTW, int D, int NW, int NL, bool SEGM>
 __device__ __forceinline__ void eg_loop(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int nst, int rot,
                                         int ntl, uint8_t* lds, v16i (&acc)[2][NTW]) {
   if constexpr (NL > 0) {
     if (ntl < NL) {
-      eg_loop<Q4, RG, NTW, D, NW, NL - 1>(src, nst, rot, ntl, lds, acc);
+      eg_loop<Q4, RG, NTW, D, NW, NL - 1, SEGM>(src, nst, rot, ntl, lds, acc);
       return;
     }
   }
-  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW, NL>(src, st, nst, rot, lds, acc);
+  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW, NL, SEGM>(src, st, nst, rot, lds, acc);
 }
 
 // Live pair tiles of this wave in a pass over pairs pbase .. n - 1: tiles t
@@ -347,9 +363,9 @@ __device__ __forceinline__ int live_tiles(int pbase, int n, int pg) {
 // pbase + 32 (NTW pg + t) + (lane % 32).  Every thread of the block calls
 // this.  On return every load of the pass has landed and every wave is done
 // with the LDS ring.
-template <bool Q4, int RG, int NTW, int D, int NW, class WRow>
+template <bool Q4, int RG, int NTW, int D, int NW, bool SEGM, class WRow>
 __device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, int pbase, int n,
-                                        int l, uint8_t* lds, v16i (&acc)[2][NTW]) {
+                                        int l, const uint32_t* segmask, uint8_t* lds, v16i (&acc)[2][NTW]) {
   using SG = EgStage<Q4>;
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   const int nst = K / SG::COLS;
@@ -359,31 +375,38 @@ __device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, i
 #pragma unroll
     for (int t = 0; t < NTW; ++t) acc[m][t] = v16i{};
   EgSrc<Q4, C> src;
-  eg_sources<Q4, C>(src, wrow, sp, pbase, n, K, l);
+  eg_sources<Q4, C>(src, wrow, sp, pbase, n, K, l, segmask);
   // the stages run in a rotated order, a different one per block (the dots
   // are exact in any order), so that concurrent blocks read different
   // column slices of their rows
   const int rot = (int)(blockIdx.x % (unsigned)nst);
 #pragma unroll
-  for (int p = 0; p < D - 1; ++p) stage_load<Q4, C>(src, (min(p, nst - 1) + rot) % nst, lds + p * C::STAGE);
-  eg_loop<Q4, RG, NTW, D, NW, NTW>(src, nst, rot, ntl, lds, acc);
+  for (int p = 0; p < D - 1; ++p)
+    stage_load<Q4, C, SEGM, 32 * RG>(src, (min(p, nst - 1) + rot) % nst, lds + p * C::STAGE);
+  eg_loop<Q4, RG, NTW, D, NW, NTW, SEGM>(src, nst, rot, ntl, lds, acc);
   // the clamped loads past the last stage land before the ring is reused
   stage_sync<0>();
 }
 
 // Dots of a pass over all limbs: one pass (nl == 1) or limb passes folded
-// into wrapping uint32 totals.
+// into wrapping uint32 totals.  segmask (down: [3][kEgPairs] in LDS, else
+// null): bit s of segmask[l - 1][pair] says segment s of the pair's h
+// table holds limb plane l.
 template <bool Q4, int RG, int NTW, int D, int NW, class WRow>
 __device__ __forceinline__ void eg_dots(WRow&& wrow, int K, const EgPairs& sp, int pbase, int n,
-                                        int nl, uint8_t* lds, v16u (&dots)[2][NTW]) {
+                                        int nl, const uint32_t* segmask, uint8_t* lds,
+                                        v16u (&dots)[2][NTW]) {
   v16i acc[2][NTW];
-  eg_pass<Q4, RG, NTW, D, NW>(wrow, K, sp, pbase, n, 0, lds, acc);
+  eg_pass<Q4, RG, NTW, D, NW, false>(wrow, K, sp, pbase, n, 0, nullptr, lds, acc);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int t = 0; t < NTW; ++t) dots[m][t] = __builtin_bit_cast(v16u, acc[m][t]);
   for (int l = 1; l < nl; ++l) {
-    eg_pass<Q4, RG, NTW, D, NW>(wrow, K, sp, pbase, n, l, lds, acc);
+    if (segmask)
+      eg_pass<Q4, RG, NTW, D, NW, true>(wrow, K, sp, pbase, n, l, segmask, lds, acc);
+    else
+      eg_pass<Q4, RG, NTW, D, NW, false>(wrow, K, sp, pbase, n, l, nullptr, lds, acc);
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -430,32 +453,42 @@ __device__ __forceinline__ bool eg_block(int ntask, int nrt, int* task, int* rt)
 
 // SwiGLU epilogue of one pass (:496-501): lane (j, h) of wave (rg, pg) holds,
 // for pair pbase + 32 (t PG + pg) + j, gate and up dots of rows rb + 32 rg +
-// 8q + 4h + r.  h = (g / (1 + expf(-g))) * u is quantized for down and
-// written into the pair's h table; the rows' limb count and activation sum
-// go to red_nl / red_sum.
-template <bool Q4, int RG, int PG, int NTW>
-__device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const v16u (&dots)[2][NTW],
+// 8q + 4h + r.  h = (g / (1 + expf(-g))) * u is quantized for down.  The
+// block's h rows of one pair are BR consecutive bytes of each limb plane of
+// its h table (rb % 16 == 0), so they are assembled in LDS (stg, the free
+// ring of RING bytes) and written 16 bytes a lane, and only the limb planes this
+// segment needs: limb counts and activation sums per pair go to red_nl /
+// red_sum (then to hpart), and down reads zeros for a plane past a
+// segment's count.  `flag` (LDS, 0 on entry) marks a block whose values
+// need more than one limb; it is 0 again on return.
+template <bool Q4, int RG, int PG, int NTW, size_t RING>
+__device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, v16u (&dots)[2][NTW],
                                             int pbase, int n, int rb, const float* sg,
-                                            const float* su, const uint64_t* exp_tab) {
+                                            const float* su, const uint64_t* exp_tab, uint8_t* stg,
+                                            int* flag) {
+  constexpr int BR = 32 * RG;          // h rows of the block
+  constexpr int SROW = BR + 4;         // staging row of a pair (odd dword count: no bank conflicts)
+  constexpr int NPP = 32 * PG * NTW;   // pairs of the pass
+  constexpr int PLANE = NPP * SROW;
+  constexpr int NTH = 64 * RG * PG;
+  constexpr int PR = RING / PLANE < 4 ? RING / PLANE : 4;   // staged planes per round
+  static_assert(PR >= 1, "one staged plane fits in the LDS ring");
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, j = lane % 32, h = lane / 32;
   const int rg = wave % RG, pg = wave / RG;
   const float div = Q4 ? 7.0f : 127.0f;
+  const int ntl = live_tiles<PG, NTW>(pbase, n, pg);
+  // 1. h values (in place of the gate dots), limb counts and sums per pair
+  int multi = 0;
 #pragma unroll
   for (int t = 0; t < NTW; ++t) {
-    const int p0 = pbase + 32 * (PG * t + pg);
-    if (p0 >= n) break;
-    const int i = p0 + j;
-    const bool live = i < n;
-    const int ic = live ? i : n - 1;
-    const uint32_t xs = sp.asum[ic];
-    uint8_t* tabq = a.htab + (size_t)sp.pair[ic] * a.htab_bytes;
+    if (t >= ntl) break;
+    const int i = pbase + 32 * (PG * t + pg) + j;
+    const uint32_t xs = sp.asum[min(i, n - 1)];
     int nl = 1;
     uint32_t hs = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int lr = 32 * rg + 8 * q + 4 * h;    // block row of 4 consecutive
-      const int row0 = rb + lr;
-      uint32_t bytes[4][4];   // [limb][r]
+      const int lr = 32 * rg + 8 * q + 4 * h;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         uint32_t dg = dots[0][t][4 * q + r], du = dots[1][t][4 * q + r];
@@ -463,42 +496,78 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, const 
         const float gv = qdot_epilogue(dg, div, sg[lr + r]);
         const float uv = qdot_epilogue(du, div, su[lr + r]);
         const int32_t hv = f2i_trunc_x86(silu_mul_t(gv, uv, exp_tab) * div);
-        const bool row_ok = row0 + r < a.rows;
+        dots[0][t][4 * q + r] = (uint32_t)hv;
+        const bool row_ok = rb + lr + r < a.rows;
         const int nn = row_ok ? limbs_needed(hv) : 1;
         nl = nn > nl ? nn : nl;
         hs += row_ok ? (uint32_t)hv : 0u;
-        uint32_t b[4];
-        split_limbs(hv, b);
-#pragma unroll
-        for (int l = 0; l < 4; ++l) bytes[l][r] = b[l];
-      }
-      if (live && row0 < a.rows) {
-        // rows row0 .. row0 + 3 (row0 % 4 == 0): Q8 4 consecutive bytes; Q4
-        // the even rows are 2 bytes in the unit's first half, the odd rows 2
-        // in its second half
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-          uint8_t* plane = reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.rows, l)));
-          if constexpr (!Q4) {
-            *reinterpret_cast<uint32_t*>(plane + row0) =
-                pack4(bytes[l][0], bytes[l][1], bytes[l][2], bytes[l][3]);
-          } else {
-            const int be = unit_byte<true>(row0), bo = unit_byte<true>(row0 + 1);
-            *reinterpret_cast<uint16_t*>(plane + be) = (uint16_t)(bytes[l][0] | (bytes[l][2] << 8));
-            *reinterpret_cast<uint16_t*>(plane + bo) = (uint16_t)(bytes[l][1] | (bytes[l][3] << 8));
-          }
-        }
       }
     }
     // lanes j and j + 32 hold the same pair
     const int o = __shfl_xor(nl, 32, kWave);
     nl = o > nl ? o : nl;
     hs += (uint32_t)__shfl_xor((int)hs, 32, kWave);
-    if (h == 0 && live) {
+    if (h == 0 && i < n) {
       atomicMax(&sp.red_nl[i], nl);
       atomicAdd(&sp.red_sum[i], hs);
     }
+    multi |= nl > 1;
   }
+  if (__any(multi) && lane == 0) atomicOr(flag, 1);
+  __syncthreads();
+  const bool bmulti = *flag != 0;
+  // 2-3. limb planes in rounds of PR planes (one round unless the block
+  // needs several limbs and the ring holds fewer than four planes): bytes
+  // into the staging rows (every row of a live pair is written), then
+  // 16-byte pieces of the planes each pair's segment needs
+  const int nlw = bmulti ? 4 : 1;
+  constexpr int NCH = BR / 16;
+  const int live = min(n - pbase, NPP);
+  for (int l0 = 0; l0 < nlw; l0 += PR) {
+    const int nr = min(PR, nlw - l0);
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      if (t >= ntl) break;
+      uint8_t* row = stg + (32 * (PG * t + pg) + j) * SROW;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lr = 32 * rg + 8 * q + 4 * h;
+        uint32_t b[4][4];   // [r][limb]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) split_limbs((int32_t)dots[0][t][4 * q + r], b[r]);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          // rows lr .. lr + 3 (lr % 4 == 0): Q8 4 consecutive bytes; Q4 the
+          // even rows 2 bytes in the unit's first half, the odd rows 2 in its
+          // second
+          if (l < l0 || l >= l0 + nr) continue;
+          uint8_t* pl = row + (l - l0) * PLANE;
+          if constexpr (!Q4) {
+            *reinterpret_cast<uint32_t*>(pl + lr) = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+          } else {
+            *reinterpret_cast<uint16_t*>(pl + unit_byte<true>(lr)) = (uint16_t)(b[0][l] | (b[2][l] << 8));
+            *reinterpret_cast<uint16_t*>(pl + unit_byte<true>(lr + 1)) = (uint16_t)(b[1][l] | (b[3][l] << 8));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int total = live * NCH * nr;
+    for (int k = threadIdx.x; k < total; k += NTH) {
+      const int kl = k / (live * NCH), rem = k - kl * live * NCH, p = rem / NCH, c = rem - p * NCH;
+      const int i = pbase + p, l = l0 + kl;
+      if (l < sp.red_nl[i] && rb + 16 * c < a.rows) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(stg + kl * PLANE + p * SROW + 16 * c);
+        u32x4 v;
+        v[0] = src[0]; v[1] = src[1]; v[2] = src[2]; v[3] = src[3];
+        uint8_t* tabq = a.htab + (size_t)sp.pair[i] * a.htab_bytes;
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(const_cast<uint32_t*>(act_plane(tabq, a.rows, l))) +
+                                  rb + 16 * c) = v;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *flag = 0;
 }
 
 // gate/up + SwiGLU for one row tile (32 RG rows of d_ff) of one task.
@@ -511,6 +580,7 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
   __shared__ EgPairs sp;
   __shared__ float sg[BR], su[BR];
   __shared__ uint64_t exp_tab[32];
+  __shared__ int multi_flag;
   uint8_t* lds = reinterpret_cast<uint8_t*>(lds_eg);
   int ti, rt;
   if (!eg_block(a.ntask, (a.rows + BR - 1) / BR, &ti, &rt)) return;
@@ -526,7 +596,10 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
     sg[t2] = a.s0[(size_t)e * a.rows + row];
     su[t2] = a.s1[(size_t)e * a.rows + row];
   }
-  if (tid == 0) sp.nl = 1;
+  if (tid == 0) {
+    sp.nl = 1;
+    multi_flag = 0;
+  }
   __syncthreads();
   int nl = 1;
   for (int i = tid; i < n; i += NTH) {
@@ -553,8 +626,8 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
   const int nlt = sp.nl;
   if (nlt == 1) {
     v16u dots[2][NTW];
-    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
-    gate_up_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb, sg, su, exp_tab);
+    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, nullptr, lds, dots);
+    gate_up_epi<Q4, RG, C::PG, NTW, C::BYTES>(a, sp, dots, 0, n, rb, sg, su, exp_tab, lds, &multi_flag);
   } else {
     // limb passes over half as many pairs at a time (the totals take the
     // other half of the accumulator budget)
@@ -562,8 +635,8 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
     constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
     v16u dots[2][NTM];
     for (int pb = 0; pb < n; pb += NPM) {
-      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
-      gate_up_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sg, su, exp_tab);
+      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, nullptr, lds, dots);
+      gate_up_epi<Q4, RG, C::PG, NTM, C::BYTES>(a, sp, dots, pb, n, rb, sg, su, exp_tab, lds, &multi_flag);
     }
   }
   __syncthreads();
@@ -620,6 +693,7 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   extern __shared__ u32x4 lds_eg[];
   __shared__ EgPairs sp;
   __shared__ float sd[BR];
+  __shared__ uint32_t segmask[3 * kEgPairs];
   uint8_t* lds = reinterpret_cast<uint8_t*>(lds_eg);
   int ti, rt;
   if (!eg_block(a.ntask, (a.rows + BR - 1) / BR, &ti, &rt)) return;
@@ -635,6 +709,7 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
     sp.pair[i] = a.perm[first + i];
     sp.red_nl[i] = 1;
     sp.red_sum[i] = 0;
+    segmask[i] = segmask[kEgPairs + i] = segmask[2 * kEgPairs + i] = 0u;
   }
   __syncthreads();
   // the pairs' h headers: the sum of the segments' activation sums and the
@@ -643,7 +718,10 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
     const int i = k / a.nseg, sg = k - i * a.nseg;
     const uint32_t* pp = a.hpart + ((size_t)sp.pair[i] * a.nseg + sg) * 2;
     const int v = (int)pp[0];
-    if (v > 1) atomicMax(&sp.red_nl[i], v);
+    if (v > 1) {
+      atomicMax(&sp.red_nl[i], v);
+      for (int l = 1; l < v; ++l) atomicOr(&segmask[(l - 1) * kEgPairs + i], 1u << sg);
+    }
     atomicAdd(&sp.red_sum[i], pp[1]);
   }
   __syncthreads();
@@ -661,14 +739,14 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   const int nlt = sp.nl;
   if (nlt == 1) {
     v16u dots[2][NTW];
-    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, lds, dots);
+    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, segmask, lds, dots);
     down_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb, sd);
   } else {
     constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
     constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
     v16u dots[2][NTM];
     for (int pb = 0; pb < n; pb += NPM) {
-      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, lds, dots);
+      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, segmask, lds, dots);
       down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sd);
     }
   }
@@ -728,7 +806,9 @@ moe_status launch_eg(const LayerDev* L, int nt, int ntask, hipStream_t s) {
 
 bool expert_gemm_ok(const LayerDev* L) {
   const int cols = L->dtype == 3 ? 128 : 64;
-  return L->D % cols == 0 && L->dff % cols == 0 && L->rbg % 16 == 0 && L->rbd % 16 == 0;
+  // d_ff <= 2048: at most 32 gate/up segments of 64 rows (down's limb masks)
+  return L->D % cols == 0 && L->dff % cols == 0 && L->dff <= 2048 && L->rbg % 16 == 0 &&
+         L->rbd % 16 == 0;
 }
 
 int expert_gemm_tiles(const LayerDev* L, int T) {

@@ -272,6 +272,37 @@ def test_grouped_vs_oracle(moehip, dtype, T, E, D, dff, bias, resid, scale):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("dtype,T", [(3, 24), (3, 96), (3, 256), (2, 24), (2, 96), (2, 256)])
+def test_grouped_mixed_limb_segments(moehip, dtype, T):
+    """h rows 0-63 of every expert scaled up (gate and up row scales x 1000):
+    those h values need 2 (Q4) or 4 (Q8) limbs, the other rows one, so the
+    gate/up blocks write different limb planes per row segment and down's
+    limb passes read zeros for the segments that wrote fewer.  A first call
+    on 1000x larger activations (h of every row needs 2 or 4 limbs) leaves
+    the upper h planes nonzero, so that a plane read where it was not
+    written this call shows.  16 experts: T = 24 / 96
+    / 256 select the 1-, 2- and 4-tile block shapes."""
+    E, D, dff = 16, 512, 768
+    seed = 8800 + dtype * 10 + T
+    print("mixed-limb case", dtype, T, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    ex.gs[:, :64] *= 1000.0
+    ex.us[:, :64] *= 1000.0
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    layer = make_layer(moehip, dtype, ex, rw)
+    layer.set_grouped_min_tokens(1)
+    big = np.ascontiguousarray(xn * np.float32(1000.0))
+    want_big, _, _, _ = O.moe_block(big, xn, rw, None, ex)
+    got_big, _, _ = layer.forward(big, xn)
+    np.testing.assert_array_equal(bits(got_big), bits(want_big))
+    got, idx, p = layer.forward(xn, xn)
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_grouped_and_decode_agree_ties_nan(moehip):
     """Both paths on the same layer and tokens: tied and NaN router logits."""
     dtype, T, E, D, dff = 2, 12, 32, 256, 128
