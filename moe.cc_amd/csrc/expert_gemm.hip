@@ -232,6 +232,7 @@ template <bool Q4, class C>
 struct EgSrc {
   const uint8_t* w[C::PERW];
   const uint8_t* b[C::PERB];
+  int nb;                   // B loads this wave issues per stage (its instructions holding a live pair row)
   uint32_t segs[C::PERB];   // SEGM passes: segments whose plane holds this B row's limb
   int col[C::PERB];         // column of this lane's B unit within a stage
 };
@@ -256,14 +257,26 @@ __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const
     src.segs[k] = segmask && l > 0 ? segmask[(l - 1) * kEgPairs + q] : ~0u;
     src.col[k] = unit * 16;
   }
+  // B instructions past the pass's pairs are not issued (shapes of more
+  // than 128 pairs, where a pass is often half full; the smaller shapes
+  // measured faster with every wave issuing PERB): instruction ins holds
+  // pair rows ins * RPI ..; this wave issues ins = wave + W k
+  if constexpr (C::NP > 128) {
+    const int live = min(n - pbase, C::NP);
+    const int nins = (live + SG::RPI - 1) / SG::RPI;
+    src.nb = __builtin_amdgcn_readfirstlane(min(max((nins - wave + C::W - 1) / C::W, 0), C::PERB));
+  } else {
+    src.nb = C::PERB;
+  }
 }
 
-// Loads stage st into buffer buf.  Every wave issues Q loads (a wave past
-// the last B instruction repeats one another wave issued: the same bytes to
-// the same place).  Pair rows past the task's pairs repeat its last pair
-// (one more read of bytes already in cache; a smaller stand-in load was
-// measured slower).  SEGM: a B unit in a segment of BRS columns outside
-// src.segs loads kEgZero.
+// Loads stage st into buffer buf: this wave's PERW weight loads and src.nb
+// B loads (a wave past the last B instruction repeats one another wave
+// issued: the same bytes to the same place).  Pair rows past the pass's
+// pairs inside an issued instruction repeat its last pair; the LDS rows of
+// instructions not issued keep stale bytes, which only tiles' rows past the
+// pairs read (their results are dropped).  SEGM: a B unit in a segment of
+// BRS columns outside src.segs loads kEgZero.
 template <bool Q4, class C, bool SEGM, int BRS>
 __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint8_t* buf) {
   using SG = EgStage<Q4>;
@@ -273,6 +286,7 @@ __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint
     lds_load16(src.w[k] + (size_t)st * 64, buf + (wave + C::W * k) * 1024);
 #pragma unroll
   for (int k = 0; k < C::PERB; ++k) {
+    if (C::NP > 128 && k >= src.nb) break;
     const int ins = (wave + C::W * k) % C::NIB;
     const uint8_t* b = src.b[k] + (size_t)st * SG::UNITS * 16;
     if constexpr (SEGM) {
@@ -290,6 +304,18 @@ __device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint
 template <int N>
 __device__ __forceinline__ void stage_sync() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// stage_sync with N = (D - 2) q, q this wave's loads per stage (uniform).
+template <int D, int QMAX>
+__device__ __forceinline__ void stage_sync_q(int q) {
+  if constexpr (QMAX > 0) {
+    if (q < QMAX) {
+      stage_sync_q<D, QMAX - 1>(q);
+      return;
+    }
+  }
+  stage_sync<(D - 2) * QMAX>();
 }
 
 // This wave's 32 weight bytes of its row-group row 32m + lane % 32 (bytes
@@ -314,7 +340,10 @@ __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, N
   using SG = EgStage<Q4>;
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   const int lane = threadIdx.x % kWave, pg = (threadIdx.x / kWave) / RG, j = lane % 32, h = lane / 32;
-  stage_sync<(D - 2) * C::Q>();
+  if constexpr (C::NP > 128)
+    stage_sync_q<D, C::Q>(C::PERW + src.nb);
+  else
+    stage_sync<(D - 2) * C::Q>();
   stage_load<Q4, C, SEGM, 32 * RG>(src, (min(st + D - 1, nst - 1) + rot) % nst,
                                    lds + ((st + D - 1) % D) * C::STAGE);
   const uint8_t* buf = lds + (st % D) * C::STAGE;
@@ -511,7 +540,7 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, v16u (
       atomicMax(&sp.red_nl[i], nl);
       atomicAdd(&sp.red_sum[i], hs);
     }
-    multi |= nl > 1;
+    multi |= i < n && nl > 1;   // rows of pairs past the pass hold stale values
   }
   if (__any(multi) && lane == 0) atomicOr(flag, 1);
   __syncthreads();
