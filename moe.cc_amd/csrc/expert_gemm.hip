@@ -278,12 +278,12 @@ __device__ __forceinline__ void eg_sources(EgSrc<Q4, C>& src, WRow&& wrow, const
 // pairs read (their results are dropped).  SEGM: a B unit in a segment of
 // BRS columns outside src.segs loads kEgZero.
 template <bool Q4, class C, bool SEGM, int BRS>
-__device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, uint8_t* buf) {
+__device__ __forceinline__ void stage_load(const EgSrc<Q4, C>& src, int st, size_t woff, uint8_t* buf) {
   using SG = EgStage<Q4>;
   const int wave = threadIdx.x / kWave;
 #pragma unroll
   for (int k = 0; k < C::PERW; ++k)
-    lds_load16(src.w[k] + (size_t)st * 64, buf + (wave + C::W * k) * 1024);
+    lds_load16(src.w[k] + woff + (size_t)st * 64, buf + (wave + C::W * k) * 1024);
 #pragma unroll
   for (int k = 0; k < C::PERB; ++k) {
     if (C::NP > 128 && k >= src.nb) break;
@@ -331,12 +331,14 @@ __device__ __forceinline__ WFrag32 w_frag(const uint8_t* wbuf, int m) {
   return f;
 }
 
-// One stage of a pass: wait for stage st, issue stage st + D - 1 (clamped to
-// the last stage, then rotated) into its ring buffer, then the MFMAs of
-// stage st: acc[m][t] for this wave's live pair tiles t < NL.
+// One step of the stage ring: wait for the stage in buffer cbuf, issue the
+// loads of K stage lst (weights woff bytes further) into buffer lbuf, then
+// the MFMAs of buffer cbuf: acc[m][t] for this wave's live pair tiles t <
+// NL.
 template <bool Q4, int RG, int NTW, int D, int NW, int NL, bool SEGM>
-__device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int st,
-                                         int nst, int rot, uint8_t* lds, v16i (&acc)[2][NTW]) {
+__device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int lst,
+                                         size_t woff, int lbuf, int cbuf, uint8_t* lds,
+                                         v16i (&acc)[2][NTW]) {
   using SG = EgStage<Q4>;
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   const int lane = threadIdx.x % kWave, pg = (threadIdx.x / kWave) / RG, j = lane % 32, h = lane / 32;
@@ -344,9 +346,8 @@ __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, N
     stage_sync_q<D, C::Q>(C::PERW + src.nb);
   else
     stage_sync<(D - 2) * C::Q>();
-  stage_load<Q4, C, SEGM, 32 * RG>(src, (min(st + D - 1, nst - 1) + rot) % nst,
-                                   lds + ((st + D - 1) % D) * C::STAGE);
-  const uint8_t* buf = lds + (st % D) * C::STAGE;
+  stage_load<Q4, C, SEGM, 32 * RG>(src, lst, woff, lds + lbuf * C::STAGE);
+  const uint8_t* buf = lds + cbuf * C::STAGE;
   const WFrag32 f0 = w_frag<RG>(buf, 0), f1 = w_frag<RG>(buf, 1);
   const uint8_t* B = buf + C::W_BYTES + (32 * pg + j) * SG::ROWB;
   const int sw = swz<Q4>(j);   // = swz(32 tile + j) for every tile
@@ -375,7 +376,50 @@ __device__ __forceinline__ void eg_loop(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW
       return;
     }
   }
-  for (int st = 0; st < nst; ++st) eg_stage<Q4, RG, NTW, D, NW, NL, SEGM>(src, st, nst, rot, lds, acc);
+  for (int st = 0; st < nst; ++st)
+    eg_stage<Q4, RG, NTW, D, NW, NL, SEGM>(src, (min(st + D - 1, nst - 1) + rot) % nst, 0,
+                                           (st + D - 1) % D, st % D, lds, acc);
+}
+
+// The ring run on across R consecutive row tiles (weights wstep bytes
+// apart): step g is K stage g % nst of row tile g / nst, so the first loads
+// of a tile are issued during the last stages of the one before.  After a
+// tile's last stage epi(r, acc) takes its dots (epi must leave the ring
+// alone) and the accumulators restart.  One limb (no segment masks).
+template <bool Q4, int RG, int NTW, int D, int NW, int NL, class Epi>
+__device__ __forceinline__ void eg_loop_rows(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, NW>>& src, int nst,
+                                             int rot, int R, size_t wstep, int ntl, uint8_t* lds, Epi& epi) {
+  if constexpr (NL > 0) {
+    if (ntl < NL) {
+      eg_loop_rows<Q4, RG, NTW, D, NW, NL - 1>(src, nst, rot, R, wstep, ntl, lds, epi);
+      return;
+    }
+  }
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  v16i acc[2][NTW];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) acc[m][t] = v16i{};
+  const int total = nst * R;
+  for (int p = 0; p < D - 1; ++p) {
+    const int gl = min(p, total - 1);
+    stage_load<Q4, C, false, 32 * RG>(src, (gl % nst + rot) % nst, (size_t)(gl / nst) * wstep,
+                                      lds + p * C::STAGE);
+  }
+  for (int g = 0; g < total; ++g) {
+    const int gl = min(g + D - 1, total - 1);
+    eg_stage<Q4, RG, NTW, D, NW, NL, false>(src, (gl % nst + rot) % nst, (size_t)(gl / nst) * wstep,
+                                            (g + D - 1) % D, g % D, lds, acc);
+    if (g % nst == nst - 1) {
+      epi(g / nst, acc);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) acc[m][t] = v16i{};
+    }
+  }
+  stage_sync<0>();
 }
 
 // Live pair tiles of this wave in a pass over pairs pbase .. n - 1: tiles t
@@ -411,7 +455,7 @@ __device__ __forceinline__ void eg_pass(WRow&& wrow, int K, const EgPairs& sp, i
   const int rot = (int)(blockIdx.x % (unsigned)nst);
 #pragma unroll
   for (int p = 0; p < D - 1; ++p)
-    stage_load<Q4, C, SEGM, 32 * RG>(src, (min(p, nst - 1) + rot) % nst, lds + p * C::STAGE);
+    stage_load<Q4, C, SEGM, 32 * RG>(src, (min(p, nst - 1) + rot) % nst, 0, lds + p * C::STAGE);
   eg_loop<Q4, RG, NTW, D, NW, NTW, SEGM>(src, nst, rot, ntl, lds, acc);
   // the clamped loads past the last stage land before the ring is reused
   stage_sync<0>();
@@ -443,6 +487,21 @@ __device__ __forceinline__ void eg_dots(WRow&& wrow, int K, const EgPairs& sp, i
   }
 }
 
+// One-limb dots of R consecutive row tiles (weights wstep bytes apart) over
+// all n pairs of the task, epi(r, acc) after each tile (eg_loop_rows).
+template <bool Q4, int RG, int NTW, int D, int NW, class WRow, class Epi>
+__device__ __forceinline__ void eg_rows(WRow&& wrow, int K, const EgPairs& sp, int n, int R, size_t wstep,
+                                        uint8_t* lds, Epi&& epi) {
+  using SG = EgStage<Q4>;
+  using C = EgCfg<Q4, RG, NTW, D, NW>;
+  const int nst = K / SG::COLS;
+  const int ntl = live_tiles<C::PG, NTW>(0, n, (threadIdx.x / kWave) / RG);
+  EgSrc<Q4, C> src;
+  eg_sources<Q4, C>(src, wrow, sp, 0, n, K, 0, nullptr);
+  const int rot = (int)(blockIdx.x % (unsigned)nst);
+  eg_loop_rows<Q4, RG, NTW, D, NW, NTW>(src, nst, rot, R, wstep, ntl, lds, epi);
+}
+
 // Where row r of an activation unit table sits in its limb plane.
 template <bool Q4>
 __device__ __forceinline__ int unit_byte(int r) {
@@ -466,6 +525,7 @@ struct EgArgs {
   uint8_t* htab; size_t htab_bytes;       // gate/up: h tables out
   uint32_t* hpart; int nseg;              // per-segment h headers: written by gate/up, read by down
   float* y;                               // down: [pairs][D]
+  int rtpb;                               // down: row tiles per block (rows % tile == 0 when > 1)
 };
 
 // Block -> (task, row tile), so that the row tiles of a task run on one XCD
@@ -713,26 +773,32 @@ __device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, con
   }
 }
 
-// down for one row tile (64 RG rows of D) of one task: y per pair.
+// Row tiles of down per block at most.
+constexpr int kDownRowTiles = 4;
+
+// down for a.rtpb consecutive row tiles (64 RG rows of D each) of one task:
+// y per pair.  The tiles share the block's pair prologue and its load ring.
 template <bool Q4, int RG, int NTW, int D, int NW>
 __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   constexpr int NTH = 64 * NW;
-  constexpr int BR = 64 * RG;   // rows per block
+  constexpr int BR = 64 * RG;   // rows per tile
   extern __shared__ u32x4 lds_eg[];
   __shared__ EgPairs sp;
-  __shared__ float sd[BR];
+  __shared__ float sd[kDownRowTiles * BR];
   __shared__ uint32_t segmask[3 * kEgPairs];
   uint8_t* lds = reinterpret_cast<uint8_t*>(lds_eg);
-  int ti, rt;
-  if (!eg_block(a.ntask, (a.rows + BR - 1) / BR, &ti, &rt)) return;
+  const int nrt = (a.rows + BR - 1) / BR;
+  int ti, rg;
+  if (!eg_block(a.ntask, (nrt + a.rtpb - 1) / a.rtpb, &ti, &rg)) return;
   const int2 task = a.tasks[ti];
   if (task.x < 0) return;
   const int e = task.x & 0xFFFF, n = task.x >> 16, first = task.y;
   if (n > C::NP) return;   // group_kernel splits tasks at NP pairs
   const int tid = threadIdx.x;
-  const int rb = rt * BR;
-  for (int r = tid; r < BR; r += NTH) sd[r] = a.s0[(size_t)e * a.rows + min(rb + r, a.rows - 1)];
+  const int rt0 = rg * a.rtpb, R = min(a.rtpb, nrt - rt0);
+  const int rb0 = rt0 * BR;
+  for (int r = tid; r < R * BR; r += NTH) sd[r] = a.s0[(size_t)e * a.rows + min(rb0 + r, a.rows - 1)];
   if (tid == 0) sp.nl = 1;
   for (int i = tid; i < n; i += NTH) {
     sp.pair[i] = a.perm[first + i];
@@ -762,21 +828,31 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   }
   if (nl > 1) atomicMax(&sp.nl, nl);
   __syncthreads();
-  // LDS row r: row rb + r
+  // LDS row r of tile t: row rb0 + t BR + r
   const uint8_t* w0 = a.w0 + (size_t)e * a.rows * a.rb;
-  auto wrow = [&](int r) { return w0 + (size_t)min(rb + r, a.rows - 1) * a.rb; };
   const int nlt = sp.nl;
   if (nlt == 1) {
-    v16u dots[2][NTW];
-    eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, segmask, lds, dots);
-    down_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb, sd);
+    auto wrow = [&](int r) { return w0 + (size_t)min(rb0 + r, a.rows - 1) * a.rb; };
+    auto epi = [&](int t, v16i (&acc)[2][NTW]) {
+      v16u dots[2][NTW];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q = 0; q < NTW; ++q) dots[m][q] = __builtin_bit_cast(v16u, acc[m][q]);
+      down_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb0 + t * BR, sd + t * BR);
+    };
+    eg_rows<Q4, RG, NTW, D, NW>(wrow, a.K, sp, n, R, (size_t)BR * a.rb, lds, epi);
   } else {
     constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
     constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
     v16u dots[2][NTM];
-    for (int pb = 0; pb < n; pb += NPM) {
-      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, segmask, lds, dots);
-      down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sd);
+    for (int t = 0; t < R; ++t) {
+      const int rb = rb0 + t * BR;
+      auto wrow = [&](int r) { return w0 + (size_t)min(rb + r, a.rows - 1) * a.rb; };
+      for (int pb = 0; pb < n; pb += NPM) {
+        eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, segmask, lds, dots);
+        down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sd + t * BR);
+      }
     }
   }
 }
@@ -793,9 +869,12 @@ moe_status eg_lds_attr(Kern* fn, size_t lds, const char* what) {
 // 64, 4 stages, two blocks per CU; NT = 4: 128 x 256 in eight waves (four
 // tiles each, those past the task's pairs skipped), 3 stages, one block per
 // CU: one task per expert up to 256 pairs, so that an expert's weights
-// are read once even when its pairs outnumber one pass of 128.
-template <bool Q4, int RG, int NTW, int D, int NW>
+// are read once even when its pairs outnumber one pass of 128.  RTPB: row
+// tiles of down per block (measured: 1 and 2 alike for NT = 1, 4 best for
+// NT = 2, 2 best for NT = 4).
+template <bool Q4, int RG, int NTW, int D, int NW, int RTPB>
 moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
+  static_assert(RTPB >= 1 && RTPB <= kDownRowTiles, "down row tiles per block");
   using C = EgCfg<Q4, RG, NTW, D, NW>;
   static bool attr = false;
   if (!attr && C::BYTES > 65536) {
@@ -808,25 +887,28 @@ moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
   const int nseg = (L->dff + 32 * RG - 1) / (32 * RG);
   EgArgs g{L->gq, L->uq, L->gs, L->us, L->rbg, L->dff, L->D, L->topk, L->perm, L->tasks, ntask,
            L->xtab, act_table_bytes(L->D), L->htab, act_table_bytes(L->dff), L->hpart, nseg,
-           nullptr};
+           nullptr, 1};
   hipLaunchKernelGGL((gate_up_eg_kernel<Q4, RG, NTW, D, NW>), dim3(tpad * (unsigned)nseg), dim3(64 * NW),
                      C::BYTES, s, g);
   moe_status st = check_hip(hipGetLastError(), "expert gate/up launch");
   if (st) return st;
+  // down: row tiles per block (kDownRowTiles at most; one for a partial
+  // last tile, whose rows the continued ring would overrun)
+  const int nrt = (L->D + 64 * RG - 1) / (64 * RG);
+  const int rtpb = L->D % (64 * RG) == 0 ? min(RTPB, nrt) : 1;
   EgArgs d{L->dq, nullptr, L->ds, nullptr, L->rbd, L->D, L->dff, L->topk, L->perm, L->tasks, ntask,
-           L->htab, act_table_bytes(L->dff), nullptr, 0, L->hpart, nseg, L->y};
+           L->htab, act_table_bytes(L->dff), nullptr, 0, L->hpart, nseg, L->y, rtpb};
   hipLaunchKernelGGL((down_eg_kernel<Q4, RG, NTW, D, NW>),
-                     dim3(tpad * (unsigned)((L->D + 64 * RG - 1) / (64 * RG))), dim3(64 * NW), C::BYTES,
-                     s, d);
+                     dim3(tpad * (unsigned)((nrt + rtpb - 1) / rtpb)), dim3(64 * NW), C::BYTES, s, d);
   return check_hip(hipGetLastError(), "expert down launch");
 }
 
 template <bool Q4>
 moe_status launch_eg(const LayerDev* L, int nt, int ntask, hipStream_t s) {
   switch (nt) {
-    case 1: return launch_eg_shape<Q4, 4, 1, 3, 4>(L, ntask, s);
-    case 2: return launch_eg_shape<Q4, 2, 1, 4, 4>(L, ntask, s);
-    case 4: return launch_eg_shape<Q4, 4, 4, 3, 8>(L, ntask, s);
+    case 1: return launch_eg_shape<Q4, 4, 1, 3, 4, 1>(L, ntask, s);
+    case 2: return launch_eg_shape<Q4, 2, 1, 4, 4, 4>(L, ntask, s);
+    case 4: return launch_eg_shape<Q4, 4, 4, 3, 8, 2>(L, ntask, s);
     default: return set_error(MOE_ERR_ARG, "expert gemm: %d pair tiles", nt);
   }
 }

@@ -248,6 +248,10 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     # Q8 at D = 2048, d_ff = 768: x ~ N(0, 1) needs two limbs, so every task
     # runs limb passes folded into one dot (two-tile blocks)
     (2, 128, 16, 2048, 768, True, True, 1.0),
+    # D = 384: three down row tiles of 128 in one block (two-tile shape), a
+    # partial last tile of 256 rows (four-tile shape, one tile per block)
+    (3, 96, 16, 384, 256, False, True, 1.0),
+    (3, 256, 16, 384, 256, False, True, 1.0),
 ]
 
 
