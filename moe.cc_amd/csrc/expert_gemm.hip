@@ -573,8 +573,11 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, v16u (
     if (t >= ntl) break;
     const int i = pbase + 32 * (PG * t + pg) + j;
     const uint32_t xs = sp.asum[min(i, n - 1)];
-    int nl = 1;
+    // the rows' value range (limbs_needed is monotone in |value|; a row
+    // past the matrix counts as 0) and wrapping sum
+    int32_t lo = 0, hi = 0;
     uint32_t hs = 0;
+    const int rows_left = a.rows - rb - 32 * rg - 4 * h;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int lr = 32 * rg + 8 * q + 4 * h;
@@ -586,12 +589,13 @@ __device__ __forceinline__ void gate_up_epi(const EgArgs& a, EgPairs& sp, v16u (
         const float uv = qdot_epilogue(du, div, su[lr + r]);
         const int32_t hv = f2i_trunc_x86(silu_mul_t(gv, uv, exp_tab) * div);
         dots[0][t][4 * q + r] = (uint32_t)hv;
-        const bool row_ok = rb + lr + r < a.rows;
-        const int nn = row_ok ? limbs_needed(hv) : 1;
-        nl = nn > nl ? nn : nl;
-        hs += row_ok ? (uint32_t)hv : 0u;
+        const int32_t hc = 8 * q + r < rows_left ? hv : 0;
+        lo = hc < lo ? hc : lo;
+        hi = hc > hi ? hc : hi;
+        hs += (uint32_t)hc;
       }
     }
+    int nl = max(limbs_needed(lo), limbs_needed(hi));
     // lanes j and j + 32 hold the same pair
     const int o = __shfl_xor(nl, 32, kWave);
     nl = o > nl ? o : nl;

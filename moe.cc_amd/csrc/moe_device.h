@@ -20,7 +20,9 @@ constexpr int kWave = 64;
 // conversion instruction saturates instead, so the out-of-range case is
 // handled explicitly.  Used for kernels.c:66 and kernels.c:115-116.
 __device__ __forceinline__ int32_t f2i_trunc_x86(float v) {
-  return (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;
+  // |v| < 2^31 is the in-range test (one compare); -2^31 itself and NaN fall
+  // outside it and give INT32_MIN, as the x86 conversion does
+  return __builtin_fabsf(v) < 2147483648.0f ? (int32_t)v : INT32_MIN;
 }
 
 // Number of signed int8 limbs needed so that sum_l limb_l * 256^l == a:
