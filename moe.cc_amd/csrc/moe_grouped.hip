@@ -33,6 +33,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGroupThreads = 1024;
+// Pairs up to which one block groups them (group_kernel); above, the
+// two-launch count / scatter over at most kGroupBlocks blocks.
+constexpr int kGroupOneBlockPairs = 4096;
+constexpr int kGroupBatch = 8;   // pair ids per thread in flight in group_kernel
 constexpr int kSelectWaves = 4;
 
 // ---------------------------------------------------------------- router
@@ -244,6 +248,22 @@ __device__ __forceinline__ int group_excl_scan(int v, int* wsum, int* total) {
   return base + x - v;
 }
 
+// Thread e's expert (c pairs from pair start on, c == 0 past E) in runs of
+// at most split pairs: {e | pairs << 16, first pair}, then {-1, 0} up to
+// ntask_max.  Every thread of the block calls this.
+__device__ __forceinline__ void write_tasks(int c, int start, int* wsum, int2* __restrict__ tasks,
+                                            int ntask_max, int split) {
+  const int tid = threadIdx.x;
+  const int nsplit = (c + split - 1) / split;
+  int ntasks;
+  const int t0 = group_excl_scan(nsplit, wsum, &ntasks);
+  for (int k = 0; k < nsplit; ++k) {
+    const int p0 = k * split, n = min(split, c - p0);
+    tasks[t0 + k] = make_int2(tid | (n << 16), start + p0);
+  }
+  for (int i = ntasks + tid; i < ntask_max; i += kGroupThreads) tasks[i] = make_int2(-1, 0);
+}
+
 // One block: count the pairs of each expert, exclusive prefix sum, then
 // scatter the pair ids.  The order of pairs within an expert does not
 // affect any result (every pair's outputs are computed independently).
@@ -259,12 +279,23 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int* __restr
                                                               int ntask_max, int split) {
   __shared__ int cnt[kGroupThreads];
   __shared__ int wsum[kGroupThreads / kWave];
+  // each thread's pair ids are read kGroupBatch at a time, all loads in
+  // flight together (one load then its atomic per pair serialised the
+  // loop on memory latency)
+  constexpr int G = kGroupBatch;
   const int tid = threadIdx.x;
   cnt[tid] = 0;
   __syncthreads();
-  for (int q = tid; q < npairs; q += kGroupThreads) {
-    const int e = idx[q];
-    if (e >= 0) atomicAdd(&cnt[e], 1);
+  for (int base = 0; base < npairs; base += G * kGroupThreads) {
+    int e[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int q = base + g * kGroupThreads + tid;
+      e[g] = q < npairs ? idx[q] : -1;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (e[g] >= 0) atomicAdd(&cnt[e[g]], 1);
   }
   __syncthreads();
   const int c = cnt[tid];   // zero past E
@@ -274,21 +305,87 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int* __restr
     ecount[tid] = c;
     eoff[tid] = start;
   }
-  if (tasks) {
-    const int nsplit = (c + split - 1) / split;
-    int ntasks;
-    const int t0 = group_excl_scan(nsplit, wsum, &ntasks);
-    for (int k = 0; k < nsplit; ++k) {
-      const int p0 = k * split, n = min(split, c - p0);
-      tasks[t0 + k] = make_int2(tid | (n << 16), start + p0);
-    }
-    for (int i = ntasks + tid; i < ntask_max; i += kGroupThreads) tasks[i] = make_int2(-1, 0);
-  }
+  if (tasks) write_tasks(c, start, wsum, tasks, ntask_max, split);
   cnt[tid] = start;   // cursor
   __syncthreads();
-  for (int q = tid; q < npairs; q += kGroupThreads) {
+  for (int base = 0; base < npairs; base += G * kGroupThreads) {
+    int e[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int q = base + g * kGroupThreads + tid;
+      e[g] = q < npairs ? idx[q] : -1;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (e[g] >= 0) perm[atomicAdd(&cnt[e[g]], 1)] = base + g * kGroupThreads + tid;
+  }
+}
+
+// The same grouping over many pairs in two launches of nb blocks, block b
+// taking pairs b*per .. (b+1)*per - 1 (one atomic per pair on a single
+// block's LDS was the cost of group_kernel): group_count_kernel writes each
+// block's pair counts per expert to hist[b][E]; group_scatter_kernel gives
+// block b the cursor start(e) + sum over b' < b of hist[b'][e] and
+// scatters its pairs; block 0 also writes ecount, eoff and the tasks.
+__global__ __launch_bounds__(kGroupThreads) void group_count_kernel(const int* __restrict__ idx, int npairs,
+                                                                    int E, int per, int* __restrict__ hist) {
+  __shared__ int cnt[kGroupThreads];
+  const int tid = threadIdx.x;
+  cnt[tid] = 0;
+  __syncthreads();
+  const int q0 = blockIdx.x * per, q1 = min(q0 + per, npairs);
+  for (int q = q0 + tid; q < q1; q += kGroupThreads) {
     const int e = idx[q];
-    if (e >= 0) perm[atomicAdd(&cnt[e], 1)] = q;
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid < E) hist[(size_t)blockIdx.x * E + tid] = cnt[tid];
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
+    const int* __restrict__ idx, int npairs, int E, int per, const int* __restrict__ hist, int nb,
+    int* __restrict__ ecount, int* __restrict__ eoff, int* __restrict__ perm, int2* __restrict__ tasks,
+    int ntask_max, int split) {
+  __shared__ int cur[kGroupThreads];
+  __shared__ int red[2][kGroupThreads];
+  __shared__ int wsum[kGroupThreads / kWave];
+  const int tid = threadIdx.x, b = blockIdx.x;
+  // expert totals and this block's prefix: G threads per expert read the nb
+  // block counts together, then one thread per expert adds their parts
+  const int G = kGroupThreads / E, e = tid % E, g = tid / E;
+  int c = 0, pre = 0;
+  if (g < G) {
+#pragma unroll 8
+    for (int k = g; k < nb; k += G) {
+      const int v = hist[(size_t)k * E + e];
+      pre += k < b ? v : 0;
+      c += v;
+    }
+  }
+  red[0][tid] = c;
+  red[1][tid] = pre;
+  __syncthreads();
+  c = pre = 0;
+  if (tid < E)
+    for (int k = 0; k < G; ++k) {
+      c += red[0][k * E + tid];
+      pre += red[1][k * E + tid];
+    }
+  int total;
+  const int start = group_excl_scan(c, wsum, &total);
+  if (b == 0) {
+    if (tid < E) {
+      ecount[tid] = c;
+      eoff[tid] = start;
+    }
+    write_tasks(c, start, wsum, tasks, ntask_max, split);
+  }
+  cur[tid] = start + pre;
+  __syncthreads();
+  const int q0 = b * per, q1 = min(q0 + per, npairs);
+  for (int q = q0 + tid; q < q1; q += kGroupThreads) {
+    const int e = idx[q];
+    if (e >= 0) perm[atomicAdd(&cur[e], 1)] = q;
   }
 }
 
@@ -390,8 +487,18 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   const int nt = expert_gemm_tiles(L, T);
   const int split = expert_gemm_split(nt);
   const int ntask_max = npairs / split + L->E + 1;
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
-                     L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
+  if (npairs <= kGroupOneBlockPairs) {
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
+                       L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
+  } else {
+    const int nb = std::min(kGroupBlocks, (npairs + 255) / 256);
+    const int per = (npairs + nb - 1) / nb;
+    hipLaunchKernelGGL(group_count_kernel, dim3((unsigned)nb), dim3(kGroupThreads), 0, s, L->idx, npairs,
+                       L->E, per, L->ghist);
+    if ((st = check_hip(hipGetLastError(), "group count launch"))) return st;
+    hipLaunchKernelGGL(group_scatter_kernel, dim3((unsigned)nb), dim3(kGroupThreads), 0, s, L->idx, npairs,
+                       L->E, per, L->ghist, nb, L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
+  }
   if ((st = check_hip(hipGetLastError(), "group launch"))) return st;
   if (overlap && (st = check_hip(hipStreamWaitEvent(s, join_event(), 0), "join wait"))) return st;
   // 5-6. gate/up + SwiGLU, down: grouped GEMMs on the 32x32x32 int8 MFMA

@@ -16,6 +16,8 @@ constexpr int kMaxTopK = 32;
 constexpr int kEgPairs = 256;
 // The smallest task split (sizes the task list).
 constexpr int kMinSplitPairs = 32;
+// Blocks of the two-launch pair grouping at most (sizes L->ghist).
+constexpr int kGroupBlocks = 64;
 
 struct LayerDev {
   int dtype = 2, D = 0, dff = 0, E = 0, topk = 0;
@@ -48,6 +50,7 @@ struct LayerDev {
   int2* tasks = nullptr;     // [T*topk/kMinSplitPairs + E + 1] tasks of the expert kernels:
                              // {expert | pairs << 16, first pair in perm}, x = -1 past the last
   float* y = nullptr;        // [T*topk][D]
+  int* ghist = nullptr;      // [kGroupBlocks][E] pairs per expert of each grouping block
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };
 

@@ -320,7 +320,7 @@ struct ScratchBuf {
   size_t bytes = 0;
 };
 struct SharedScratch {
-  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, tasks;
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, tasks, ghist;
   unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
 };
 SharedScratch g_scratch;
@@ -362,13 +362,15 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   if (grouped_ok(L) &&
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
        (st = grow(S.perm, np * 4, &synced)) || (st = grow(S.y, np * L->D * 4, &synced)) ||
-       (st = grow(S.tasks, (np / kMinSplitPairs + L->E + 1) * 8, &synced))))
+       (st = grow(S.tasks, (np / kMinSplitPairs + L->E + 1) * 8, &synced)) ||
+       (st = grow(S.ghist, (size_t)kGroupBlocks * L->E * 4, &synced))))
     return st;
   L->logits = (float*)S.logits.p; L->idx = (int*)S.idx.p; L->p = (float*)S.p.p;
   L->xtab = (uint8_t*)S.xtab.p; L->htab = (uint8_t*)S.htab.p; L->h = (float*)S.h.p;
   L->xn = (float*)S.xn.p; L->hpart = (uint32_t*)S.hpart.p; L->xpart = (uint32_t*)S.xpart.p;
   L->ecount = (int*)S.ecount.p; L->eoff = (int*)S.eoff.p; L->perm = (int*)S.perm.p;
   L->tasks = (int2*)S.tasks.p;
+  L->ghist = (int*)S.ghist.p;
   if (!S.sel_counter) {
     if ((st = dev_alloc(&S.sel_counter, 1))) return st;
     if ((st = check_hip(hipMemsetAsync(S.sel_counter, 0, 4, stream()), "counter init"))) return st;
@@ -796,7 +798,7 @@ moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, cons
   L->xn = (float*)(base + o.xn);
   L->hpart = (uint32_t*)(base + o.hpart);
   L->xpart = (uint32_t*)(base + o.xpart);
-  L->ecount = L->eoff = L->perm = nullptr;
+  L->ecount = L->eoff = L->perm = L->ghist = nullptr;
   L->tasks = nullptr;
   L->y = nullptr;
   L->capT = T;
