@@ -351,16 +351,38 @@ __device__ __forceinline__ void eg_stage(const EgSrc<Q4, EgCfg<Q4, RG, NTW, D, N
   const WFrag32 f0 = w_frag<RG>(buf, 0), f1 = w_frag<RG>(buf, 1);
   const uint8_t* B = buf + C::W_BYTES + (32 * pg + j) * SG::ROWB;
   const int sw = swz<Q4>(j);   // = swz(32 tile + j) for every tile
+  if constexpr (NL <= 2) {
+    // every B fragment of the stage requested before the first MFMA, so
+    // that the reads' latencies overlap (the registers fit up to 2 tiles)
+    v4i bf[SG::S][NL > 0 ? NL : 1];
 #pragma unroll
-  for (int s = 0; s < SG::S; ++s) {
-    const v4i a0 = a_op<Q4>(f0, s);
-    const v4i a1 = a_op<Q4>(f1, s);
-    const int slot = (h * SG::S + s) ^ sw;
+    for (int s = 0; s < SG::S; ++s)
 #pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const v4i b = *reinterpret_cast<const v4i*>(B + 32 * C::PG * t * SG::ROWB + slot * 16);
-      acc[0][t] = mfma32(a0, b, acc[0][t]);
-      acc[1][t] = mfma32(a1, b, acc[1][t]);
+      for (int t = 0; t < NL; ++t)
+        bf[s][t] = *reinterpret_cast<const v4i*>(B + 32 * C::PG * t * SG::ROWB + ((h * SG::S + s) ^ sw) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < SG::S; ++s) {
+      const v4i a0 = a_op<Q4>(f0, s);
+      const v4i a1 = a_op<Q4>(f1, s);
+#pragma unroll
+      for (int t = 0; t < NL; ++t) {
+        acc[0][t] = mfma32(a0, bf[s][t], acc[0][t]);
+        acc[1][t] = mfma32(a1, bf[s][t], acc[1][t]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < SG::S; ++s) {
+      const v4i a0 = a_op<Q4>(f0, s);
+      const v4i a1 = a_op<Q4>(f1, s);
+      const int slot = (h * SG::S + s) ^ sw;
+#pragma unroll
+      for (int t = 0; t < NL; ++t) {
+        const v4i b = *reinterpret_cast<const v4i*>(B + 32 * C::PG * t * SG::ROWB + slot * 16);
+        acc[0][t] = mfma32(a0, b, acc[0][t]);
+        acc[1][t] = mfma32(a1, b, acc[1][t]);
+      }
     }
   }
 }
