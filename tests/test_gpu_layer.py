@@ -307,6 +307,30 @@ def test_grouped_mixed_limb_segments(moehip, dtype, T):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def test_grouped_config_shape_T2048(moehip):
+    """The prefill bench's layer shape (configs[3]: Q4, E = 128, D = 2048,
+    d_ff = 768, top-8) at T = 2048: two router chains per lane, x tables
+    packed on the side stream, one 256-pair task per expert, the two-launch
+    grouping, two down row tiles per block -- bit for bit against the
+    oracle (its threaded build: 77 G multiply-adds)."""
+    dtype, T, E, D, dff = 3, 2048, 128, 2048, 768
+    seed = 9900
+    print("config-shape case T=2048", flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    xr = O.normal(T * D, seed + 13, 0.0, 1.0).reshape(T, D)
+    with O.threaded():
+        want, widx, wp, wlog = O.moe_block(xn, xr, rw, None, ex)
+    layer = make_layer(moehip, dtype, ex, rw)
+    got, idx, p = layer.forward(xn, xr)
+    dbg = layer.debug(T)
+    np.testing.assert_array_equal(bits(dbg["logits"]), bits(wlog))
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_grouped_and_decode_agree_ties_nan(moehip):
     """Both paths on the same layer and tokens: tied and NaN router logits."""
     dtype, T, E, D, dff = 2, 12, 32, 256, 128
