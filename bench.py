@@ -177,8 +177,11 @@ def run_gemv(args, dtype, shapes, workload):
         count = int(np.ceil(args.pool_gib * (1 << 30) / (N * rb)))
         log(f"[bench] building pool {N}x{K} dtype {dtype}: {count} matrices")
         pools.append(Pool(dtype, N, K, count, seed=1000 * (i + 1)))
-    # per step and shape: pack (event a -> b), then the GEMV launch (b -> c);
-    # the roofline is taken on the GEMV launch alone, the step value on both
+    # a step: for each shape, pack then the GEMV launch.  The K timed steps
+    # carry events only at their ends (an event pair inside the loop costs
+    # ~5 us of device time); a second pass of K steps brackets each pack
+    # (event a -> b) and each GEMV launch (b -> c) for the per-kernel
+    # figures -- the roofline is taken on the GEMV launch alone.
     evs = {i: [(M.Event(), M.Event(), M.Event()) for _ in range(args.steps)]
            for i in range(len(pools))}
     for _ in range(args.warmup):
@@ -190,6 +193,14 @@ def run_gemv(args, dtype, shapes, workload):
     wall0 = time.perf_counter()
     t_start.record()
     for s in range(args.steps):
+        for p in pools:
+            p.pack()
+            p.launch()
+    t_end.record()
+    M.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_ms(t_end)
+    for s in range(args.steps):
         for i, p in enumerate(pools):
             a, b, c = evs[i][s]
             a.record()
@@ -197,10 +208,7 @@ def run_gemv(args, dtype, shapes, workload):
             b.record()
             p.launch()
             c.record()
-    t_end.record()
     M.synchronize()
-    wall = time.perf_counter() - wall0
-    total_ms = t_start.elapsed_ms(t_end)
     per_kernel = []
     for i, p in enumerate(pools):
         ms = [b.elapsed_ms(c) for a, b, c in evs[i]]
@@ -353,6 +361,16 @@ def run_decode(dtype, Ts, n_layers, steps, warmup):
             lay.forward_dev(xs.ptr + (i % n_in) * T * D * 4, xs.ptr + (i % n_in) * T * D * 4, T,
                             out.ptr)
         M.synchronize()
+        # back to back (events only at the ends), then each layer between
+        # its own pair of events (a pair costs device time of its own)
+        s0, s1 = M.Event(), M.Event()
+        s0.record()
+        for i in range(steps):
+            x = xs.ptr + (i % n_in) * T * D * 4
+            pool.layers[i % n_layers].forward_dev(x, x, T, out.ptr, idx.ptr + i * T * 8 * 4)
+        s1.record()
+        M.synchronize()
+        stream_ms = s0.elapsed_ms(s1) / steps
         ev = [(M.Event(), M.Event()) for _ in range(steps)]
         t0, t1 = M.Event(), M.Event()
         t0.record()
@@ -373,6 +391,7 @@ def run_decode(dtype, Ts, n_layers, steps, warmup):
         res.append({"T": T, "layers_in_pool": n_layers, "steps": steps,
                     "us_per_layer_median": round(med * 1e3, 2),
                     "us_per_layer_mean": round(total_ms / steps * 1e3, 2),
+                    "us_per_layer_back_to_back": round(stream_ms * 1e3, 2),
                     "tokens_per_s_one_layer": round(T / (med * 1e-3), 1),
                     "distinct_experts_avg": U, "algorithmic_bytes": int(algo),
                     "GBs": round(algo / (med * 1e-3) / 1e9, 1),
@@ -400,6 +419,13 @@ def run_prefill(dtype, Ts, n_layers, steps, warmup):
         for i in range(max(warmup, n_layers)):
             pool.layers[i % n_layers].forward_dev(xn.ptr, x.ptr, T, out.ptr)
         M.synchronize()
+        s0, s1 = M.Event(), M.Event()
+        s0.record()
+        for i in range(steps):
+            pool.layers[i % n_layers].forward_dev(xn.ptr, x.ptr, T, out.ptr, idx.ptr)
+        s1.record()
+        M.synchronize()
+        stream_ms = s0.elapsed_ms(s1) / steps
         ev = [(M.Event(), M.Event()) for _ in range(steps)]
         t0, t1 = M.Event(), M.Event()
         t0.record()
@@ -418,6 +444,7 @@ def run_prefill(dtype, Ts, n_layers, steps, warmup):
         res.append({"T": T, "layers_in_pool": n_layers, "steps": steps,
                     "us_per_layer_median": round(med * 1e3, 2),
                     "us_per_layer_mean": round(t0.elapsed_ms(t1) / steps * 1e3, 2),
+                    "us_per_layer_back_to_back": round(stream_ms * 1e3, 2),
                     "tokens_per_s_one_layer": round(T / (med * 1e-3), 1),
                     "distinct_experts_last_step": U, "algorithmic_bytes": int(algo),
                     "GBs": round(algo / (med * 1e-3) / 1e9, 1),

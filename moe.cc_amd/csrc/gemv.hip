@@ -27,6 +27,9 @@ namespace {
 
 constexpr int kBlock = kTileBlock;
 constexpr int kWaves = kTileWaves;
+// LDS for the fused kernel's activation tables at most (four token slots of
+// K = 2048 take 32.8 KiB; larger products pack into a workspace first).
+constexpr size_t kFusedTableLds = 40 * 1024;
 
 struct TiledArgs {
   QShape sh;
@@ -127,6 +130,97 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
   gemv_write_outputs(ybuf, kYRows, job.C, a.sh.ldc, mbase, ntok, r0, r1);
 }
 
+// One activation row into an LDS table (the layout act_pack writes): a
+// first pass over x for the limb count and sum (block reduction), a second
+// that writes the planes those values need -- all four when `all_planes`
+// (a block of several rows reads as many planes as its largest count).
+// Whole block; barriers.
+template <bool Q4>
+__device__ void pack_act_row_lds(const float* __restrict__ x, int K, uint8_t* tab, int* scratch,
+                                 bool all_planes) {
+  const float mult = Q4 ? 7.0f : 127.0f;
+  constexpr int V = Q4 ? 8 : 4;
+  const size_t plane = (((size_t)K + 15) / 16) * 16;
+  uint32_t* p0 = reinterpret_cast<uint32_t*>(tab + 16);
+  const int nd = (K + V - 1) / V;
+  if (threadIdx.x == 0) { scratch[0] = 1; scratch[1] = 0; }
+  __syncthreads();
+  int32_t lo = 0, hi = 0;
+  uint32_t part = 0;
+  for (int d = threadIdx.x; d < nd; d += blockDim.x)
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int k = V * d + i;
+      const int32_t v = k < K ? f2i_trunc_x86(x[k] * mult) : 0;
+      lo = v < lo ? v : lo;
+      hi = v > hi ? v : hi;
+      part += (uint32_t)v;
+    }
+  block_max_sum(max(limbs_needed(lo), limbs_needed(hi)), part, scratch);
+  __syncthreads();
+  const int nl = scratch[0];
+  const int nw = all_planes ? 4 : nl;
+  if (threadIdx.x == 0) {
+    reinterpret_cast<int*>(tab)[0] = nl;
+    reinterpret_cast<uint32_t*>(tab)[1] = (uint32_t)scratch[1];
+  }
+  for (int d = threadIdx.x; d < nd; d += blockDim.x) {
+    uint32_t b[V][4];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int k = V * d + i;
+      split_limbs(k < K ? f2i_trunc_x86(x[k] * mult) : 0, b[i]);
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      if (l >= nw) break;
+      uint32_t* pl = p0 + (size_t)l * (plane / 4);
+      if constexpr (!Q4) {
+        pl[d] = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+      } else {
+        const int KW = (K + 7) / 8;
+        pl[d] = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
+        pl[KW + d] = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
+      }
+    }
+  }
+}
+
+// qgemv_tiled with the activation tables built by each block in its own LDS
+// (dynamic, ntok tables of tab_bytes) from the fp32 rows: one launch for a
+// product instead of act_pack + qgemv_tiled.  x (K floats) is re-read from
+// cache by every block; only the planes the values need are written.
+template <bool Q4, class G, int MT>
+__global__ __launch_bounds__(kBlock) void qgemv_fused(TiledArgs a) {
+  extern __shared__ u32x4 lds_tabs[];
+  __shared__ int scratch[2];
+  const int job_id = blockIdx.x / a.blocks_per_job;
+  const int r0 = (blockIdx.x % a.blocks_per_job) * a.rows_per_block;
+  const int r1 = r0 + a.rows_per_block < a.sh.N ? r0 + a.rows_per_block : a.sh.N;
+  const QJob job = get_job(a, job_id);
+  const int mbase = blockIdx.y * MT;
+  const int ntok = a.sh.M - mbase < MT ? a.sh.M - mbase : MT;
+  uint8_t* lt = reinterpret_cast<uint8_t*>(lds_tabs);
+  for (int t = 0; t < ntok; ++t) {
+    pack_act_row_lds<Q4>(job.A + (size_t)(mbase + t) * a.sh.lda, a.sh.K, lt + (size_t)t * a.tab_bytes,
+                         scratch, ntok > 1);
+    __syncthreads();
+  }
+  const uint8_t* tabs[MT];
+  const float* xs[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int tt = t < ntok ? t : ntok - 1;
+    tabs[t] = lt + (size_t)tt * a.tab_bytes;
+    xs[t] = job.A + (size_t)(mbase + tt) * a.sh.lda;
+  }
+  const uint8_t* W[1] = {job.W};
+  __shared__ float ybuf[MT * kYRows];
+  GemvEpiMaker mk{job.S, ybuf, kYRows, a.sh.M, mbase, r0, Q4 ? 7.0f : 127.0f};
+  stream_tokens<Q4, G, 1, MT>(W, a.sh.rs, a.sh.K, tabs, xs, ntok, r0, r1, mk);
+  gemv_write_outputs(ybuf, kYRows, job.C, a.sh.ldc, mbase, ntok, r0, r1);
+}
+
 template <bool Q4>
 __global__ __launch_bounds__(kBlock) void qgemv_generic(QShape sh, const QJob* __restrict__ jobs,
                                                         QJob one, int blocks_per_job) {
@@ -174,14 +268,15 @@ using TiledFn = void (*)(TiledArgs);
 
 struct Variant {
   TiledFn fn;
-  int wr;      // rows per wave group
+  TiledFn fused;   // the same with the activation tables built in LDS
+  int wr;          // rows per wave group
   int mt;
   const char* name;
 };
 
 template <bool Q4, class G, int MT>
 Variant make_variant(const char* name) {
-  return Variant{qgemv_tiled<Q4, G, MT>, G::WR, MT, name};
+  return Variant{qgemv_tiled<Q4, G, MT>, qgemv_fused<Q4, G, MT>, G::WR, MT, name};
 }
 
 // Row byte counts with a tiled geometry: LPR lanes x P dwordx4 x 16 bytes.
@@ -259,8 +354,9 @@ hipError_t launch_act_pack(const QShape& sh, const QJob* jobs_dev, const QJob& o
   return hipGetLastError();
 }
 
-hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
-                               const uint8_t* tabs, int shared_tabs, hipStream_t stream) {
+// tabs == nullptr: the fused kernel (tables in LDS, lds bytes per block).
+static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                        const uint8_t* tabs, int shared_tabs, size_t lds, hipStream_t stream) {
   Variant v;
   if (!select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) return hipErrorInvalidValue;
   // rows per block: a multiple of (waves x rows per wave group), large
@@ -286,8 +382,17 @@ hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJo
   a.rows_per_block = (int)rpb;
   a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
   dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
-  hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
+  if (tabs)
+    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
+  else
+    hipLaunchKernelGGL(v.fused, grid, dim3(kBlock), lds, stream, a);
   return hipGetLastError();
+}
+
+hipError_t launch_qgemv_tables(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                               const uint8_t* tabs, int shared_tabs, hipStream_t stream) {
+  if (!tabs) return hipErrorInvalidValue;
+  return launch_tiled(sh, jobs_dev, one, njobs, tabs, shared_tabs, 0, stream);
 }
 
 size_t act_table_size(int K) { return act_table_bytes(K); }
@@ -305,6 +410,13 @@ hipError_t launch_qgemv(const QShape& sh, const QJob* jobs_dev, const QJob& one,
   // batched entry point guarantee 16-byte aligned packed rows (capi.cpp).
   if (qgemv_tiled_ok(sh, jobs_dev ? nullptr : one.W)) {
     const size_t tb = act_table_bytes(sh.K);
+    // one product whose token slots' tables fit in LDS: one fused launch
+    // (for many products packing once first is faster: measured 175 against
+    // 189 us for 1366 batch-1 GEMVs of [2048 x 768])
+    const int slots = sh.M == 1 ? 1 : (sh.M == 2 ? 2 : 4);   // select_tiled's token slots per block
+    const size_t lds = tb * (size_t)(sh.M < slots ? sh.M : slots);
+    if (njobs == 1 && lds <= kFusedTableLds)
+      return launch_tiled(sh, jobs_dev, one, njobs, nullptr, 0, lds, stream);
     hipError_t e = ensure_ws(tb * (size_t)njobs * (size_t)sh.M);
     if (e != hipSuccess) return e;
     e = launch_act_pack(sh, jobs_dev, one, njobs, g_ws, stream);
