@@ -352,11 +352,11 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   }
 }
 
-// One token, few rows (the router): one block per output row.  The token
-// row is staged in LDS (normalized first when NORM, the sum of squares by
-// block_seq_sum), the products x[k] * W[n][k] are formed into LDS and summed
-// in order by block_seq_sum, so a row costs about K / 8 dependent adds
-// instead of K.  With PACK each block packs its column slice of the
+// Few tokens, few rows (the router): one block per (output row, token); with
+// NORM or PACK one token.  The token row is staged in LDS (normalized first
+// when NORM, the sum of squares by block_seq_sum), the products x[k] *
+// W[n][k] are formed into LDS and summed in order by block_seq_sum, so a row
+// costs about K / 8 dependent adds instead of K.  With PACK each block packs its column slice of the
 // normalized row into the activation tables (row_finish_kernel writes the
 // header and, with a fused selection, picks the experts).
 // 512 threads: two waves per SIMD.  A wave issues a VALU instruction about
@@ -368,7 +368,7 @@ constexpr int kRowMaxK = 8192;
 template <bool NORM, int PACK>
 __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   extern __shared__ float4 rl4[];
-  const int K = a.K, k4 = K / 4, n = blockIdx.x;
+  const int K = a.K, k4 = K / 4, n = blockIdx.x, m = blockIdx.y;
   float* xs = reinterpret_cast<float*>(rl4);   // [K] the token row
   float* pv = xs + K;                          // [K] squares, then products, then keys
   float4* xs4 = rl4;
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   // the token row (and norm weights) into registers first, then the weight
   // row (a wave's loads complete in order: the LDS staging waits only for
   // the token row)
-  const float4* x4 = reinterpret_cast<const float4*>(a.A);
+  const float4* x4 = reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda);
   const float4* nw4g = reinterpret_cast<const float4*>(a.norm_w);
   float4 xv[WV], nv[WV];
 #pragma unroll
@@ -464,18 +464,19 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   }
   __syncthreads();
   const float acc = block_seq_sum<kRowThreads>(pv, K, seq);
-  if (tid == 0) a.C[n] = dense_epilogue(a, 0, n, acc);
+  if (tid == 0) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
 }
 
 // After dense_row_kernel (a kernel boundary instead of a fence in each of
 // its blocks): the activation table's header from the slices' partials and
-// the token's expert selection.  One wave.
-__global__ __launch_bounds__(kWave) void row_finish_kernel(DenseArgs a) {
-  __shared__ uint64_t keys[1024];
-  __shared__ int sidx[kMaxTopK];
-  __shared__ float sval[kMaxTopK], sexp[kMaxTopK];
-  const int lane = threadIdx.x;
-  if (a.pack_dtype) {
+// each token's expert selection, one wave per token (M <= 4).
+constexpr int kRowFinishWaves = 4;
+__global__ __launch_bounds__(kRowFinishWaves * kWave) void row_finish_kernel(DenseArgs a) {
+  __shared__ uint64_t keys[kRowFinishWaves][1024];
+  __shared__ int sidx[kRowFinishWaves][kMaxTopK];
+  __shared__ float sval[kRowFinishWaves][kMaxTopK], sexp[kRowFinishWaves][kMaxTopK];
+  const int lane = threadIdx.x % kWave, m = threadIdx.x / kWave;
+  if (a.pack_dtype && m == 0) {
     uint32_t nl = 1, sum = 0;
     for (int b = lane; b < a.N; b += kWave) {
       const uint32_t* pp = a.pack_part + (size_t)b * 2;
@@ -494,8 +495,11 @@ __global__ __launch_bounds__(kWave) void row_finish_kernel(DenseArgs a) {
       hh[1] = sum;
     }
   }
-  select_token_any(a.C, a.N, a.sel_topk, keys, sidx, sval, sexp, a.sel_idx, a.sel_p, a.sel_idx_user,
-                   a.sel_p_user);
+  if (m >= a.M) return;
+  const size_t o = (size_t)m * a.sel_topk;
+  select_token_any(a.C + (size_t)m * a.ldc, a.N, a.sel_topk, keys[m], sidx[m], sval[m], sexp[m],
+                   a.sel_idx + o, a.sel_p + o, a.sel_idx_user ? a.sel_idx_user + o : nullptr,
+                   a.sel_p_user ? a.sel_p_user + o : nullptr);
 }
 
 // Many tokens: a block computes a tile of 16*CT tokens x 16*CE rows; thread
@@ -1401,8 +1405,10 @@ bool dense_amax_ok(const DenseArgs& a) {
 int dense_amax_rows(int) { return 16; }
 
 // One token against few rows: the row kernel.
+// Row kernel: one token, or up to 4 without the fused rmsnorm and packing.
 bool dense_row_ok(const DenseArgs& a, bool vec) {
-  return a.M == 1 && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
+  const bool rows = a.M == 1 || (a.M <= 4 && !a.norm && !a.pack_dtype);
+  return rows && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
 }
 
 bool dense_row_path(const DenseArgs& a) {
@@ -1416,10 +1422,11 @@ moe_status launch_row(const DenseArgs& a, hipStream_t s) {
   const size_t lds = (size_t)2 * a.K * 4;
   moe_status st = set_lds(dense_row_kernel<NORM, PACK>, lds, "row kernel LDS attribute");
   if (st) return st;
-  hipLaunchKernelGGL((dense_row_kernel<NORM, PACK>), dim3((unsigned)a.N), dim3(kRowThreads), lds, s, a);
+  hipLaunchKernelGGL((dense_row_kernel<NORM, PACK>), dim3((unsigned)a.N, (unsigned)a.M), dim3(kRowThreads), lds,
+                     s, a);
   if ((st = check_hip(hipGetLastError(), "dense row launch"))) return st;
   if (!a.sel_counter || a.sel_defer) return MOE_OK;
-  hipLaunchKernelGGL(row_finish_kernel, dim3(1), dim3(kWave), 0, s, a);
+  hipLaunchKernelGGL(row_finish_kernel, dim3(1), dim3(kWave * a.M), 0, s, a);
   return check_hip(hipGetLastError(), "row finish launch");
 }
 
