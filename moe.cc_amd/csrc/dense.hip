@@ -467,6 +467,47 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   if (tid == 0) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
 }
 
+// 5-16 tokens, few rows: a block per (output row, four tokens), its 512
+// threads four groups of 128 side by side, each the row kernel on its own
+// token -- products x[k] * W[n][k] into its LDS slice, summed in order by
+// group_seq_sum (four candidate chains per thread).  No norm, no packing.
+constexpr int kRowGroups = 4;
+constexpr int kRowGroupThreads = kRowThreads / kRowGroups;
+constexpr int kRowsMaxK = 4096;
+
+__global__ __launch_bounds__(kRowThreads) void dense_rows4_kernel(DenseArgs a) {
+  extern __shared__ float4 rg4[];   // [kRowGroups][K] products
+  __shared__ SeqSumScratch seq[kRowGroups];
+  const int K = a.K, k4 = K / 4, n = blockIdx.x;
+  const int g = threadIdx.x / kRowGroupThreads, gt = threadIdx.x % kRowGroupThreads;
+  const int mg = blockIdx.y * kRowGroups + g;   // this group's token (past M: a repeat, not written)
+  const int m = min(mg, a.M - 1);
+  float4* pv4 = rg4 + (size_t)g * k4;
+  const float4* x4 = reinterpret_cast<const float4*>(a.A + (size_t)m * a.lda);
+  const float4* w4 = reinterpret_cast<const float4*>(a.W + (size_t)n * a.ldw);
+  constexpr int WV = kRowsMaxK / 4 / kRowGroupThreads;
+  float4 xv[WV], wv[WV];
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = gt + kRowGroupThreads * u;
+    xv[u] = i < k4 ? x4[i] : zero4();
+  }
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = gt + kRowGroupThreads * u;
+    wv[u] = i < k4 ? w4[i] : zero4();
+  }
+#pragma unroll
+  for (int u = 0; u < WV; ++u) {
+    const int i = gt + kRowGroupThreads * u;
+    if (i < k4)
+      pv4[i] = make_float4(xv[u].x * wv[u].x, xv[u].y * wv[u].y, xv[u].z * wv[u].z, xv[u].w * wv[u].w);
+  }
+  __syncthreads();
+  const float acc = group_seq_sum<kRowGroupThreads>(reinterpret_cast<const float*>(pv4), K, seq[g], gt);
+  if (gt == 0 && mg < a.M) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
+}
+
 // After dense_row_kernel (a kernel boundary instead of a fence in each of
 // its blocks): the activation table's header from the slices' partials and
 // each token's expert selection, one wave per token (M <= 4).
@@ -1411,6 +1452,11 @@ bool dense_row_ok(const DenseArgs& a, bool vec) {
   return rows && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
 }
 
+bool dense_rows4_ok(const DenseArgs& a, bool vec) {
+  return a.M > 4 && a.M <= 16 && !a.norm && !a.pack_dtype && !a.sel_counter && !a.amax_part &&
+         a.N <= 1024 && vec && a.K <= kRowsMaxK;
+}
+
 bool dense_row_path(const DenseArgs& a) {
   const bool vec = a.K > 0 && a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) &&
                    al16(a.W);
@@ -1474,6 +1520,14 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     if (a.pack_dtype == 2) return launch_row<false, 2>(a, s);
     if (a.pack_dtype == 3) return launch_row<false, 3>(a, s);
     return launch_row<false, 0>(a, s);
+  }
+  if (dense_rows4_ok(a, vec)) {
+    const size_t lds = (size_t)kRowGroups * a.K * 4;
+    moe_status st = set_lds(dense_rows4_kernel, lds, "rows kernel LDS attribute");
+    if (st) return st;
+    hipLaunchKernelGGL(dense_rows4_kernel, dim3((unsigned)a.N, (unsigned)((a.M + kRowGroups - 1) / kRowGroups)),
+                       dim3(kRowThreads), lds, s, a);
+    return check_hip(hipGetLastError(), "dense rows launch");
   }
   if (a.sel_counter) {
     if (!vec) return set_error(MOE_ERR_ARG, "dense matmul: fused selection needs aligned rows");

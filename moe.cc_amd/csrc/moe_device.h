@@ -239,12 +239,17 @@ __device__ __forceinline__ double group_sum_f64(double v) {
 
 // Every thread of the block (NT threads: 32 to 512, a power of two) must
 // call this; p (LDS) holds the n values; returns s to every thread.
+// group_seq_sum: the same over a group of NT threads (whole waves; gtid in
+// [0, NT) its thread number) when the block runs several groups side by
+// side, each on its own values and scratch; every thread of the block calls
+// it (block barriers inside).
 template <int NT>
-__device__ __forceinline__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
+__device__ __forceinline__ float group_seq_sum(const float* p, int n, SeqSumScratch& sc, int gtid) {
   constexpr int S = kSeqSegs, C = NT / S, CPT = kSeqCands / C;
   static_assert(C >= 4 && C <= 64 && (C & (C - 1)) == 0 && CPT >= 1 && C * CPT == kSeqCands,
                 "threads per segment");
-  const int tid = threadIdx.x, j = tid / C, i = tid % C;
+  static_assert(NT % kWave == 0, "whole waves");
+  const int tid = gtid, j = tid / C, i = tid % C;
   const int L = ((n + S - 1) / S + 3) & ~3;   // segments start on float4 boundaries
   const int k0 = min(n, j * L), k1 = min(n, k0 + L);
   const float4* p4 = reinterpret_cast<const float4*>(p);   // p is 16-byte aligned
@@ -344,6 +349,11 @@ __device__ __forceinline__ float block_seq_sum(const float* p, int n, SeqSumScra
   }
   __syncthreads();
   return sc.result;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_seq_sum(const float* p, int n, SeqSumScratch& sc) {
+  return group_seq_sum<NT>(p, n, sc, (int)threadIdx.x);
 }
 
 // test_model_trace.c:233 then :500: h = (g / (1 + expf(-g))) * u

@@ -37,12 +37,15 @@ def f32_dev(moehip, A, W):
 
 
 # (M, N, K): one-wave GEMV with 16 / 32 / 64 rows per wave (chunk tails,
-# rows past N), the LDS tile kernel at both tile sizes (token and row tails;
+# rows past N), the row kernels (a block per row and token up to 4 tokens;
+# four 128-thread token groups per block for 5-16 tokens, a partial last
+# group), the LDS tile kernel at both tile sizes (token and row tails;
 # 64 x 64 tiles from 1024 blocks: the last shape), and the unaligned
 # fallback (K % 4 != 0)
 F32_SHAPES = [(1, 37, 2048), (1, 5120, 2048), (3, 100, 4100), (4, 2048, 4096), (2, 33000, 64),
-              (1, 70000, 68), (5, 77, 300), (40, 130, 2048), (300, 96, 260), (2, 10, 7),
-              (7, 13, 1001), (1, 1, 4), (1030, 4100, 260)]
+              (1, 70000, 68), (5, 77, 300), (9, 128, 2048), (16, 1024, 4096), (13, 3, 64),
+              (40, 130, 2048), (300, 96, 260), (2, 10, 7), (7, 13, 1001), (1, 1, 4),
+              (1030, 4100, 260)]
 
 
 @pytest.mark.parametrize("M,N,K", F32_SHAPES)
