@@ -57,7 +57,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef unsigned int v16u __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kEgWaves = 4;   // waves per block unless a shape says otherwise
+constexpr int kEgWaves = 4;   // waves per block unless a shape says otherwise (the 256-pair shape: 8)
 
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);

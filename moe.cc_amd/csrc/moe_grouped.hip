@@ -3,7 +3,8 @@
 //
 // The reference runs three GEMVs per (token, rank) pair and re-reads the
 // expert for every pair.  Here every expert's rows are read once per task
-// (up to 128 of its pairs) for all the pairs routed to it:
+// (up to 32, 64 or 256 of its pairs, by block shape) for all the pairs
+// routed to it:
 //   pack        x_norm rows -> int8 limb unit tables (expert_gemm.hip)
 //   router      logits[t,e] = sum_k x[t,k] * Wr[e,k], k ascending, one
 //               sequential fp32 chain per (token, expert); x staged in LDS,
@@ -11,9 +12,10 @@
 //               :213-227)
 //   select      one wave per token: top-k by the insertion rule and the
 //               softmax gates (:480-487)
-//   group       one block: pairs per expert, offsets, pair ids grouped by
-//               expert (a histogram and a permutation of the top-k table),
-//               and the task list of the expert kernels
+//   group       pairs per expert, offsets, pair ids grouped by expert (a
+//               histogram and a permutation of the top-k table) and the
+//               task list of the expert kernels: one block, or above 4096
+//               pairs a count and a scatter launch over up to 64 blocks
 //   gate_up     grouped int8 MFMA GEMM, SwiGLU epilogue (:496-501), h packed
 //               into the pairs' unit tables (expert_gemm.hip)
 //   down        grouped int8 MFMA GEMM, y per pair (:502-503)
