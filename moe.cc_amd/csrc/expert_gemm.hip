@@ -739,18 +739,22 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
     return ((r % 64) < 32 ? g0 : u0) + (size_t)row * a.rb;
   };
   const int nlt = sp.nl;
-  if (nlt == 1) {
+  // half the tiles and one more ring stage (DH) when they fit the same LDS:
+  // the 256-pair shape's tasks of at most 128 pairs, and its limb passes
+  constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
+  constexpr int DH = EgCfg<Q4, RG, NTM, D + 1, NW>::BYTES <= C::BYTES && C::NP > 128 ? D + 1 : D;
+  if (nlt == 1 && (DH == D || n > EgCfg<Q4, RG, NTM, DH, NW>::NP)) {
     v16u dots[2][NTW];
     eg_dots<Q4, RG, NTW, D, NW>(wrow, a.K, sp, 0, n, 1, nullptr, lds, dots);
     gate_up_epi<Q4, RG, C::PG, NTW, C::BYTES>(a, sp, dots, 0, n, rb, sg, su, exp_tab, lds, &multi_flag);
   } else {
     // limb passes over half as many pairs at a time (the totals take the
-    // other half of the accumulator budget)
-    constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
-    constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
+    // other half of the accumulator budget); one limb here when the task
+    // fits a half pass
+    constexpr int NPM = EgCfg<Q4, RG, NTM, DH, NW>::NP;
     v16u dots[2][NTM];
     for (int pb = 0; pb < n; pb += NPM) {
-      eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, nullptr, lds, dots);
+      eg_dots<Q4, RG, NTM, DH, NW>(wrow, a.K, sp, pb, n, nlt, nullptr, lds, dots);
       gate_up_epi<Q4, RG, C::PG, NTM, C::BYTES>(a, sp, dots, pb, n, rb, sg, su, exp_tab, lds, &multi_flag);
     }
   }
@@ -857,8 +861,12 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   // LDS row r of tile t: row rb0 + t BR + r
   const uint8_t* w0 = a.w0 + (size_t)e * a.rows * a.rb;
   const int nlt = sp.nl;
-  if (nlt == 1) {
-    auto wrow = [&](int r) { return w0 + (size_t)min(rb0 + r, a.rows - 1) * a.rb; };
+  // half the tiles and one more ring stage (DH) when they fit the same LDS
+  // (as in gate/up)
+  constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
+  constexpr int DH = EgCfg<Q4, RG, NTM, D + 1, NW>::BYTES <= C::BYTES && C::NP > 128 ? D + 1 : D;
+  auto wrow = [&](int r) { return w0 + (size_t)min(rb0 + r, a.rows - 1) * a.rb; };
+  if (nlt == 1 && (DH == D || n > EgCfg<Q4, RG, NTM, DH, NW>::NP)) {
     auto epi = [&](int t, v16i (&acc)[2][NTW]) {
       v16u dots[2][NTW];
 #pragma unroll
@@ -868,15 +876,24 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
       down_epi<Q4, RG, C::PG, NTW>(a, sp, dots, 0, n, rb0 + t * BR, sd + t * BR);
     };
     eg_rows<Q4, RG, NTW, D, NW>(wrow, a.K, sp, n, R, (size_t)BR * a.rb, lds, epi);
+  } else if (nlt == 1) {
+    auto epi = [&](int t, v16i (&acc)[2][NTM]) {
+      v16u dots[2][NTM];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q = 0; q < NTM; ++q) dots[m][q] = __builtin_bit_cast(v16u, acc[m][q]);
+      down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, 0, n, rb0 + t * BR, sd + t * BR);
+    };
+    eg_rows<Q4, RG, NTM, DH, NW>(wrow, a.K, sp, n, R, (size_t)BR * a.rb, lds, epi);
   } else {
-    constexpr int NTM = NTW > 1 ? NTW / 2 : 1;
-    constexpr int NPM = EgCfg<Q4, RG, NTM, D, NW>::NP;
+    constexpr int NPM = EgCfg<Q4, RG, NTM, DH, NW>::NP;
     v16u dots[2][NTM];
     for (int t = 0; t < R; ++t) {
       const int rb = rb0 + t * BR;
-      auto wrow = [&](int r) { return w0 + (size_t)min(rb + r, a.rows - 1) * a.rb; };
+      auto wrow_t = [&](int r) { return w0 + (size_t)min(rb + r, a.rows - 1) * a.rb; };
       for (int pb = 0; pb < n; pb += NPM) {
-        eg_dots<Q4, RG, NTM, D, NW>(wrow, a.K, sp, pb, n, nlt, segmask, lds, dots);
+        eg_dots<Q4, RG, NTM, DH, NW>(wrow_t, a.K, sp, pb, n, nlt, segmask, lds, dots);
         down_epi<Q4, RG, C::PG, NTM>(a, sp, dots, pb, n, rb, sd + t * BR);
       }
     }
