@@ -393,6 +393,46 @@ __global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
 
 // ---------------------------------------------------------------- combine
 
+// combine_kernel for a fixed top-k: the token's ranks, gates and all K y
+// rows requested before the first add (the adds keep the rank order).
+template <int K>
+__global__ __launch_bounds__(256) void combine_k_kernel(const float* __restrict__ y,
+                                                        const int* __restrict__ idx,
+                                                        const float* __restrict__ p,
+                                                        const float* __restrict__ resid,
+                                                        float* __restrict__ out, int D) {
+  const int t = blockIdx.y;
+  const int o = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (o >= D) return;
+  int e[K];
+  float pj[K];
+  float4 yv[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    e[j] = idx[t * K + j];
+    pj[j] = p[t * K + j];
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    yv[j] = *reinterpret_cast<const float4*>(y + (size_t)(t * K + j) * D + o);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (e[j] < 0) continue;
+    const float a0 = pj[j] * yv[j].x, a1 = pj[j] * yv[j].y, a2 = pj[j] * yv[j].z, a3 = pj[j] * yv[j].w;
+    acc.x = acc.x + a0;
+    acc.y = acc.y + a1;
+    acc.z = acc.z + a2;
+    acc.w = acc.w + a3;
+  }
+  const size_t oi = (size_t)t * D + o;
+  if (resid) {
+    const float4 rv = *reinterpret_cast<const float4*>(resid + oi);
+    acc = make_float4(rv.x + acc.x, rv.y + acc.y, rv.z + acc.z, rv.w + acc.w);
+  }
+  *reinterpret_cast<float4*>(out + oi) = acc;
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
                                                       const int* __restrict__ idx,
                                                       const float* __restrict__ p,
@@ -507,8 +547,11 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   if ((st = launch_expert_gemm(L, nt, ntask_max, s))) return st;
   // 7. ordered combine + residual
   dim3 cg((unsigned)((L->D / 4 + 255) / 256), (unsigned)T);
-  hipLaunchKernelGGL(combine_kernel, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D,
-                     L->topk);
+  if (L->topk == 8)
+    hipLaunchKernelGGL(combine_k_kernel<8>, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D);
+  else
+    hipLaunchKernelGGL(combine_kernel, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D,
+                       L->topk);
   return check_hip(hipGetLastError(), "combine launch");
 }
 
