@@ -51,110 +51,161 @@ struct RouterTileArgs {
   int T, D, E;
 };
 
-// Router weights reach every lane by DPP row broadcast: lane l of a wave
-// holds W[e][k0 + l % 16] of a 16-column group (all four rows of the wave
-// the same values), and v_mul_f32_dpp with row_newbcast:i multiplies each
-// lane's own x by W[e][k0 + i].  Only x goes through LDS, one float4 read
-// per four products of each of the lane's CE chains.
+// Router weights reach every lane by DPP row broadcast: within each 16-lane
+// row of a wave all lanes work for one expert, lane l holding W[e][k0 + l %
+// 16] of a 16-column group, and v_mul_f32_dpp with row_newbcast:i
+// multiplies each lane's own x by W[e][k0 + i].
 template <int I>
 __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + I, 0xF, 0xF, false));
 }
 
-template <int CE, int... I>
-__device__ __forceinline__ void router_group(const float (&w)[CE], const float (&xv)[16],
-                                             float (&acc)[CE], std::integer_sequence<int, I...>) {
-  // k ascending: column I of the group, each product and sum rounded alone
-  (
-      [&] {
-#pragma unroll
-        for (int c = 0; c < CE; ++c) {
-          const float p = row_bcast<I>(w[c]) * xv[I];
-          acc[c] = acc[c] + p;
-        }
-      }(),
-      ...);
-}
-
-// Logits of 64 tokens x 4*CE experts per 256-thread block: lane t of every
-// wave owns token t0 + t, wave w experts e0 + CE*w .. + CE - 1, so each lane
-// runs CE sequential chains (k ascending, :213-227).  The block's x rows
-// stream through two LDS buffers of KC columns (the next-but-one chunk in
-// registers while the current one is consumed); each wave's weight groups
-// are loaded one chunk ahead.  D % KC == 0.
 // x is staged as native 4-float vectors: copies of HIP's float4 struct
 // are memcpys that keep a register array in scratch memory.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int CE, int KC>
+// Block of WPB waves = 16 tokens x 4 * CE * WPB experts: lane l of a wave
+// runs the chains of token t0 + l % 16 with the CE experts of its row l /
+// 16, so the four rows of a wave read the same x addresses from LDS (the
+// LDS serves a repeated address once; with one token per lane the x reads
+// bound the kernel).  The 16 x rows stream through two LDS buffers of KC
+// columns, each wave's weight groups are loaded one chunk ahead.
+template <int CE, int KC, int WPB>
 struct RouterShape {
+  static constexpr int NT = 64 * WPB;        // threads
+  static constexpr int TOK = 16;             // tokens per block
   static constexpr int LD = KC + 4;          // padded x row (floats)
   static constexpr int V4 = KC / 4;          // float4 per row chunk
-  static constexpr int NV = 64 * V4 / 256;   // float4 per thread per chunk
+  static constexpr int NV = TOK * V4 / NT;   // float4 per thread per chunk
   static constexpr int NG = KC / 16;         // weight groups per chunk
-  static_assert(64 * V4 % 256 == 0, "chunk must split evenly over the block");
+  static constexpr int EPB = 4 * CE * WPB;   // experts per block
+  static_assert(TOK * V4 % NT == 0, "chunk must split evenly over the block");
 };
 
+// The register state of one lane across a chunk: the x values of the
+// current and the next 16-column group (X[g % 2]), the products of the
+// column in flight (P[j % 2]) and the CE sums.
+template <int CE>
+struct RouterRegs {
+  float X[2][16];
+  float P[2][CE];
+  float acc[CE];
+};
+
+__device__ __forceinline__ void router_read_group(const float* src, float (&xv)[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * q);
+    xv[4 * q] = v[0]; xv[4 * q + 1] = v[1]; xv[4 * q + 2] = v[2]; xv[4 * q + 3] = v[3];
+  }
+}
+
+template <int CE, int I>
+__device__ __forceinline__ void router_mul(const float (&w)[CE], float xv, float (&p)[CE]) {
+#pragma unroll
+  for (int c = 0; c < CE; ++c) p[c] = row_bcast<I>(w[c]) * xv;
+}
+
+// The KC columns of a chunk in a fixed software-pipelined order: the
+// products of column j + 1 are issued before the sums of column j, so that
+// each add waits only on the previous add of its chain, never on its own
+// product; the next group's x is read from LDS at the start of a group and
+// the staged next chunk is written to LDS halfway through (the compiler's
+// scheduler would put every product right before its add: one dependent
+// stall and one DPP hazard wait per column).  k ascending in every chain.
+template <int CE, int KC, int WPB, int H, int... J>
+__device__ __forceinline__ void router_cols(RouterRegs<CE>& r,
+                                            const float (&wg)[2][RouterShape<CE, KC, WPB>::NG][CE],
+                                            const float* B,
+                                            const f32x4 (&rg)[RouterShape<CE, KC, WPB>::NV],
+                                            const int (&dst)[RouterShape<CE, KC, WPB>::NV], float* nbuf,
+                                            std::integer_sequence<int, J...>) {
+  using RS = RouterShape<CE, KC, WPB>;
+  (
+      [&] {
+        constexpr int g = J / 16, i = J % 16;
+        if constexpr (i == 0 && g + 1 < RS::NG) router_read_group(B + 16 * (g + 1), r.X[(g + 1) & 1]);
+        if constexpr (J == KC / 2) {
+#pragma unroll
+          for (int v = 0; v < RS::NV; ++v) *reinterpret_cast<f32x4*>(nbuf + dst[v]) = rg[v];
+        }
+        if constexpr (J + 1 < KC) {
+          constexpr int g1 = (J + 1) / 16, i1 = (J + 1) % 16;
+          router_mul<CE, i1>(wg[H][g1], r.X[g1 & 1][i1], r.P[(J + 1) & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < CE; ++c) r.acc[c] = r.acc[c] + r.P[J & 1][c];
+        __builtin_amdgcn_sched_barrier(0);
+      }(),
+      ...);
+}
+
 // Chunk cc of the router loop, weight slot H (= cc % 2): the next chunk's
-// weights into slot H ^ 1, the products and sums of this chunk from LDS
-// buffer cc % 2, then the staged chunk cc + 1 into the other buffer and the
-// loads of chunk cc + 2.
-template <int CE, int KC, int H>
+// weights into slot H ^ 1, the KC columns of this chunk from LDS buffer
+// cc % 2 (the staged chunk cc + 1 written into the other buffer on the
+// way), then the loads of chunk cc + 2 and the block barrier.
+template <int CE, int KC, int WPB, int H>
 __device__ __forceinline__ void router_chunk(
-    const f32x4* const (&srcp)[RouterShape<CE, KC>::NV], const int (&dst)[RouterShape<CE, KC>::NV],
-    const float* const (&wrow)[CE], f32x4 (&rg)[RouterShape<CE, KC>::NV],
-    float (&wg)[2][RouterShape<CE, KC>::NG][CE], float (&acc)[CE], const float* xr, float* buf,
-    int cc, int nc) {
-  using RS = RouterShape<CE, KC>;
+    const f32x4* const (&srcp)[RouterShape<CE, KC, WPB>::NV],
+    const int (&dst)[RouterShape<CE, KC, WPB>::NV], const float* const (&wrow)[CE],
+    f32x4 (&rg)[RouterShape<CE, KC, WPB>::NV], float (&wg)[2][RouterShape<CE, KC, WPB>::NG][CE],
+    RouterRegs<CE>& r, const float* xr, float* buf, int cc, int nc) {
+  using RS = RouterShape<CE, KC, WPB>;
+  constexpr int BS = RS::TOK * RS::LD;
   const int nx = min(cc + 1, nc - 1);
 #pragma unroll
   for (int g = 0; g < RS::NG; ++g)
 #pragma unroll
     for (int c = 0; c < CE; ++c) wg[H ^ 1][g][c] = wrow[c][(size_t)nx * KC + 16 * g];
-  const float* B = xr + (cc & 1) * 64 * RS::LD;
-#pragma unroll
-  for (int g = 0; g < RS::NG; ++g) {
-    float xv[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(B + 16 * g + 4 * q);
-      xv[4 * q] = v[0]; xv[4 * q + 1] = v[1]; xv[4 * q + 2] = v[2]; xv[4 * q + 3] = v[3];
-    }
-    router_group<CE>(wg[H][g], xv, acc, std::make_integer_sequence<int, 16>{});
-  }
-  float* b = buf + ((cc + 1) & 1) * 64 * RS::LD;
-#pragma unroll
-  for (int v = 0; v < RS::NV; ++v) *reinterpret_cast<f32x4*>(b + dst[v]) = rg[v];
+  const float* B = xr + (cc & 1) * BS;
+  router_read_group(B, r.X[0]);
+  router_mul<CE, 0>(wg[H][0], r.X[0][0], r.P[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  router_cols<CE, KC, WPB, H>(r, wg, B, rg, dst, buf + ((cc + 1) & 1) * BS,
+                              std::make_integer_sequence<int, KC>{});
   const size_t o = (size_t)min(cc + 2, nc - 1) * RS::V4;
 #pragma unroll
   for (int v = 0; v < RS::NV; ++v) rg[v] = srcp[v][o];
   __syncthreads();
 }
 
-// Logits of 64 tokens x 4*CE experts per 256-thread block: lane t of every
-// wave owns token t0 + t, wave w experts e0 + CE*w .. + CE - 1, so each lane
-// runs CE sequential chains (k ascending, :213-227).  The block's x rows
-// stream through two LDS buffers of KC columns (the next-but-one chunk in
-// registers while the current one is consumed); each wave's weight groups
-// are loaded one chunk ahead.  D % KC == 0.
-template <int CE, int KC>
-__global__ __launch_bounds__(256) void router_bcast_kernel(RouterTileArgs a) {
-  using RS = RouterShape<CE, KC>;
+// Logits of 16 tokens x EPB experts per block (k ascending, :213-227).
+// Blocks of one token group share an XCD (block id mod 8), so that its x
+// rows come from that XCD's L2 after the first read: blocks 0 .. 8 * NEG *
+// (NTG / 8) - 1 map to (token group xcd + 8 * (slot / NEG), expert group
+// slot % NEG) with xcd = id % 8, slot = id / 8; the rest (NTG % 8 token
+// groups) in row order.  D % KC == 0.
+template <int CE, int KC, int WPB>
+__global__ __launch_bounds__(64 * WPB) void router_bcast_kernel(RouterTileArgs a) {
+  using RS = RouterShape<CE, KC, WPB>;
   extern __shared__ float4 lds4[];
-  float* buf = reinterpret_cast<float*>(lds4);   // [2][64][LD]
+  float* buf = reinterpret_cast<float*>(lds4);   // [2][16][LD]
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int t0 = blockIdx.y * 64;
-  const int eb = blockIdx.x * 4 * CE + wave * CE;
+  const int neg = (a.E + RS::EPB - 1) / RS::EPB;
+  const int ntg8 = ((a.T + RS::TOK - 1) / RS::TOK) & ~7;
+  const int id = blockIdx.x;
+  int tg, eg;
+  if (id < ntg8 * neg) {
+    const int slot = id / 8;
+    tg = id % 8 + 8 * (slot / neg);
+    eg = slot % neg;
+  } else {
+    tg = ntg8 + (id - ntg8 * neg) / neg;
+    eg = (id - ntg8 * neg) % neg;
+  }
+  const int t0 = tg * RS::TOK;
+  const int eb = eg * RS::EPB + wave * 4 * CE + (lane / 16) * CE;
   const int D = a.D, nc = D / KC;
   const f32x4* srcp[RS::NV];
   int dst[RS::NV];
   const float* wrow[CE];
   f32x4 rg[RS::NV];
   float wg[2][RS::NG][CE];
-  float acc[CE];
+  RouterRegs<CE> r;
 #pragma unroll
   for (int v = 0; v < RS::NV; ++v) {
-    const int i = tid + 256 * v;
+    const int i = tid + RS::NT * v;
     const int row = i / RS::V4, c4 = i % RS::V4;
     srcp[v] = reinterpret_cast<const f32x4*>(a.x + (size_t)min(t0 + row, a.T - 1) * D) + c4;
     dst[v] = row * RS::LD + 4 * c4;
@@ -162,7 +213,7 @@ __global__ __launch_bounds__(256) void router_bcast_kernel(RouterTileArgs a) {
 #pragma unroll
   for (int c = 0; c < CE; ++c) {
     wrow[c] = a.W + (size_t)min(eb + c, a.E - 1) * D + lane % 16;
-    acc[c] = 0.0f;
+    r.acc[c] = 0.0f;
   }
   // loads and stores are unconditional (chunk index clamped; a store past
   // the last chunk fills the idle buffer) so the staging stays in registers
@@ -178,19 +229,19 @@ __global__ __launch_bounds__(256) void router_bcast_kernel(RouterTileArgs a) {
 #pragma unroll
   for (int v = 0; v < RS::NV; ++v) rg[v] = srcp[v][o1];
   __syncthreads();
-  const float* xr = buf + lane * RS::LD;
+  const float* xr = buf + (lane % 16) * RS::LD;
   // two chunks per iteration, so that each weight slot is a fixed register set
   for (int cc = 0;;) {
-    router_chunk<CE, KC, 0>(srcp, dst, wrow, rg, wg, acc, xr, buf, cc, nc);
+    router_chunk<CE, KC, WPB, 0>(srcp, dst, wrow, rg, wg, r, xr, buf, cc, nc);
     if (++cc >= nc) break;
-    router_chunk<CE, KC, 1>(srcp, dst, wrow, rg, wg, acc, xr, buf, cc, nc);
+    router_chunk<CE, KC, WPB, 1>(srcp, dst, wrow, rg, wg, r, xr, buf, cc, nc);
     if (++cc >= nc) break;
   }
-  const int t = t0 + lane;
+  const int t = t0 + lane % 16;
 #pragma unroll
   for (int c = 0; c < CE; ++c) {
     const int e = eb + c;
-    if (t < a.T && e < a.E) a.logits[(size_t)t * a.E + e] = a.b ? acc[c] + a.b[e] : acc[c];
+    if (t < a.T && e < a.E) a.logits[(size_t)t * a.E + e] = a.b ? r.acc[c] + a.b[e] : r.acc[c];
   }
 }
 
@@ -463,21 +514,28 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 bool is16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
-template <int CE, int KC>
+template <int CE, int KC, int WPB>
 moe_status launch_router_bcast(const RouterTileArgs& a, hipStream_t s) {
-  constexpr size_t lds = 2 * (size_t)64 * (KC + 4) * 4;
-  static bool attr_set = false;
-  if (lds > 65536 && !attr_set) {
-    moe_status st = check_hip(hipFuncSetAttribute((const void*)router_bcast_kernel<CE, KC>,
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  (int)lds),
-                              "router LDS attribute");
-    if (st) return st;
-    attr_set = true;
-  }
-  dim3 grid((unsigned)((a.E + 4 * CE - 1) / (4 * CE)), (unsigned)((a.T + 63) / 64));
-  hipLaunchKernelGGL((router_bcast_kernel<CE, KC>), grid, dim3(256), lds, s, a);
+  using RS = RouterShape<CE, KC, WPB>;
+  constexpr size_t lds = 2 * (size_t)RS::TOK * RS::LD * 4;
+  static_assert(lds <= 65536, "router LDS");
+  const unsigned blocks = (unsigned)(((a.T + RS::TOK - 1) / RS::TOK) * ((a.E + RS::EPB - 1) / RS::EPB));
+  hipLaunchKernelGGL((router_bcast_kernel<CE, KC, WPB>), dim3(blocks), dim3(RS::NT), lds, s, a);
   return check_hip(hipGetLastError(), "router launch");
+}
+
+// Waves per router block: eight from 1024 tokens, four from 256, two below
+// (measured at E = 128, D = 2048), fewer where the block would hold more
+// experts than the layer.
+moe_status launch_router(const RouterTileArgs& a, hipStream_t s) {
+  int wpb = a.T >= 1024 ? 8 : a.T >= 256 ? 4 : 2;
+  while (wpb > 1 && 4 * wpb > a.E) wpb /= 2;
+  switch (wpb) {
+    case 8: return launch_router_bcast<1, 128, 8>(a, s);
+    case 4: return launch_router_bcast<1, 128, 4>(a, s);
+    case 2: return launch_router_bcast<1, 128, 2>(a, s);
+    default: return launch_router_bcast<1, 128, 1>(a, s);
+  }
 }
 
 }  // namespace
@@ -517,11 +575,9 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   } else if ((st = launch_pack_units(L, xn, T, s))) {
     return st;
   }
-  // 2. router logits: one token chain per lane below 1024 tokens (fewer
-  // waves than SIMDs there, so chain latency decides), two from 1024
+  // 2. router logits, one sequential chain per lane
   RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E};
-  st = T >= 1024 ? launch_router_bcast<2, 128>(ra, s) : launch_router_bcast<1, 128>(ra, s);
-  if (st) return st;
+  if ((st = launch_router(ra, s))) return st;
   // 3. top-k and gates
   if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
   // 4. group pairs by expert, tasks of at most one block's pairs
