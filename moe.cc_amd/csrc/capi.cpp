@@ -27,8 +27,6 @@ std::mutex g_mu;
 bool g_ready = false;
 int g_device = -1;
 hipStream_t g_stream = nullptr;
-hipStream_t g_side = nullptr;
-hipEvent_t g_fork = nullptr, g_join = nullptr;
 
 struct CacheKey {
   const void* host;
@@ -77,9 +75,6 @@ moe_status ensure_init() {
 }
 
 hipStream_t stream() { return g_stream; }
-hipStream_t side_stream() { return g_side; }
-hipEvent_t fork_event() { return g_fork; }
-hipEvent_t join_event() { return g_join; }
 
 namespace {
 
@@ -172,12 +167,6 @@ moe_status moe_init(int device) {
   st = check_hip(hipSetDevice(device), "hipSetDevice");
   if (st) return st;
   st = check_hip(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
-  if (st) return st;
-  st = check_hip(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "hipStreamCreate");
-  if (st) return st;
-  st = check_hip(hipEventCreateWithFlags(&g_fork, hipEventDisableTiming), "hipEventCreate");
-  if (st) return st;
-  st = check_hip(hipEventCreateWithFlags(&g_join, hipEventDisableTiming), "hipEventCreate");
   if (st) return st;
   g_device = device;
   g_ready = true;

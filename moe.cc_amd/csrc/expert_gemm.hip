@@ -39,8 +39,8 @@
 // offsets of moe_qtile.h's act tables, but each limb plane is a sequence of
 // 16-byte units, unit u = columns 16u .. 16u + 15: Q8 in column order, Q4
 // the 8 even columns then the 8 odd ones (the order a packed weight dword's
-// low nibbles, then high nibbles, take).  pack_units_kernel writes the x
-// tables, the gate/up epilogue the h tables.
+// low nibbles, then high nibbles, take).  The router blocks write the x
+// tables (pack_unit16, moe_grouped.hip), the gate/up epilogue the h tables.
 #include <utility>
 
 #include "moe_device.h"
@@ -106,59 +106,6 @@ __device__ __forceinline__ v4i a_op(const WFrag32& f, int s) {
     r[0] = (int)w[0]; r[1] = (int)w[1]; r[2] = (int)w[2]; r[3] = (int)w[3];
   }
   return r;
-}
-
-// ---------------------------------------------------------------- x tables
-
-// One block per row: x -> quantized a = trunc(x * 7 or 127) (kernels.c:115
-// / :66) -> 4 limb planes of 16-byte units, header {limbs needed, sum a}.
-// K % 16 == 0.
-template <bool Q4>
-__global__ __launch_bounds__(256) void pack_units_kernel(const float* __restrict__ x, int K,
-                                                         uint8_t* __restrict__ tabs, size_t tab_bytes) {
-  __shared__ int scratch[2];
-  const float mult = Q4 ? 7.0f : 127.0f;
-  const float* xr = x + (size_t)blockIdx.x * K;
-  uint8_t* tab = tabs + (size_t)blockIdx.x * tab_bytes;
-  if (threadIdx.x == 0) { scratch[0] = 1; scratch[1] = 0; }
-  __syncthreads();
-  int nl = 1;
-  uint32_t part = 0;
-  for (int u = threadIdx.x; u < K / 16; u += blockDim.x) {
-    int32_t a[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 v = reinterpret_cast<const f32x4*>(xr + 16 * u)[q];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[4 * q + i] = f2i_trunc_x86(v[i] * mult);
-    }
-    uint32_t b[16][4];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int n = limbs_needed(a[i]);
-      nl = n > nl ? n : nl;
-      part += (uint32_t)a[i];
-      split_limbs(a[i], b[i]);
-    }
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      u32x4 o;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        // Q4: dwords 0-1 the even columns, 2-3 the odd ones
-        const int c0 = Q4 ? (d < 2 ? 8 * d : 8 * (d - 2) + 1) : 4 * d;
-        const int st = Q4 ? 2 : 1;
-        o[d] = pack4(b[c0][l], b[c0 + st][l], b[c0 + 2 * st][l], b[c0 + 3 * st][l]);
-      }
-      *reinterpret_cast<u32x4*>(const_cast<uint32_t*>(act_plane(tab, K, l)) + 4 * u) = o;
-    }
-  }
-  block_max_sum(nl, part, scratch);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    reinterpret_cast<int*>(tab)[0] = scratch[0];
-    reinterpret_cast<uint32_t*>(tab)[1] = (uint32_t)scratch[1];
-  }
 }
 
 // ---------------------------------------------------------------- passes
@@ -971,16 +918,6 @@ int expert_gemm_tiles(const LayerDev* L, int T) {
 }
 
 int expert_gemm_split(int nt) { return nt == 4 ? 256 : 32 * nt; }
-
-moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s) {
-  if (L->dtype == 3)
-    hipLaunchKernelGGL(pack_units_kernel<true>, dim3((unsigned)T), dim3(256), 0, s, x, L->D, L->xtab,
-                       act_table_bytes(L->D));
-  else
-    hipLaunchKernelGGL(pack_units_kernel<false>, dim3((unsigned)T), dim3(256), 0, s, x, L->D, L->xtab,
-                       act_table_bytes(L->D));
-  return check_hip(hipGetLastError(), "unit table launch");
-}
 
 moe_status launch_expert_gemm(const LayerDev* L, int nt, int ntask, hipStream_t s) {
   return L->dtype == 3 ? launch_eg<true>(L, nt, ntask, s) : launch_eg<false>(L, nt, ntask, s);

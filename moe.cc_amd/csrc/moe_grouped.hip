@@ -5,13 +5,13 @@
 // expert for every pair.  Here every expert's rows are read once per task
 // (up to 32, 64 or 256 of its pairs, by block shape) for all the pairs
 // routed to it:
-//   pack        x_norm rows -> int8 limb unit tables (expert_gemm.hip)
 //   router      logits[t,e] = sum_k x[t,k] * Wr[e,k], k ascending, one
 //               sequential fp32 chain per (token, expert); x staged in LDS,
 //               the weights broadcast from registers by DPP (:465-468 ->
-//               :213-227)
+//               :213-227); the same blocks then pack the x_norm rows into
+//               the int8 limb unit tables of the expert kernels
 //   select      one wave per token: top-k by the insertion rule and the
-//               softmax gates (:480-487)
+//               softmax gates (:480-487); the x tables' headers
 //   group       pairs per expert, offsets, pair ids grouped by expert (a
 //               histogram and a permutation of the top-k table) and the
 //               task list of the expert kernels: one block, or above 4096
@@ -49,6 +49,10 @@ struct RouterTileArgs {
   const float* b;      // [E] or null
   float* logits;       // [T][E]
   int T, D, E;
+  uint8_t* tabs;       // [T] x unit tables (tab_bytes each), packed by the same blocks
+  size_t tab_bytes;
+  int q4;              // tables for Q4 experts (else Q8)
+  uint2* part;         // [token groups][expert groups][16] partial table headers {nl, sum}
 };
 
 // Router weights reach every lane by DPP row broadcast: within each 16-lane
@@ -170,6 +174,54 @@ __device__ __forceinline__ void router_chunk(
   __syncthreads();
 }
 
+// The x unit tables of a token group, packed by its router blocks (the x
+// rows are in L2 from the router loop; a separate pack launch cost more):
+// block eg packs units [eg U / neg, (eg + 1) U / neg) of each of the 16
+// tokens (U = D / 16), thread i the units of token i % 16.  The limb counts
+// (max) and activation sums (wrapping add) reduce per block into
+// part[tg][eg]; select_kernel combines a token's partials into its table
+// header (both reductions are order-free; no fence between blocks needed).
+template <int NT>
+__device__ __forceinline__ void router_pack(const RouterTileArgs& a, int t0, int tg, int eg, int neg) {
+  __shared__ int pk_nl[16];
+  __shared__ unsigned pk_sum[16];
+  const int tid = threadIdx.x, lane = tid % kWave;
+  if (tid < 16) { pk_nl[tid] = 1; pk_sum[tid] = 0; }
+  __syncthreads();
+  const int U = a.D / 16, u0 = eg * U / neg, nu = (eg + 1) * U / neg - u0;
+  const int tok = tid % 16, t = t0 + tok;
+  int nl = 1;
+  uint32_t sum = 0;
+  if (t < a.T) {
+    const float* xr = a.x + (size_t)t * a.D;
+    uint8_t* tab = a.tabs + (size_t)t * a.tab_bytes;
+    for (int k = tid / 16; k < nu; k += NT / 16) {
+      const int u = u0 + k;
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 w = reinterpret_cast<const f32x4*>(xr + 16 * u)[q];
+        v[4 * q] = w[0]; v[4 * q + 1] = w[1]; v[4 * q + 2] = w[2]; v[4 * q + 3] = w[3];
+      }
+      if (a.q4) pack_unit16<true>(v, tab, a.D, u, nl, sum);
+      else pack_unit16<false>(v, tab, a.D, u, nl, sum);
+    }
+  }
+  // lanes l, l + 16, l + 32, l + 48 hold the same token
+#pragma unroll
+  for (int off = 16; off < kWave; off *= 2) {
+    const int o = __shfl_xor(nl, off, kWave);
+    nl = o > nl ? o : nl;
+    sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+  }
+  if (lane < 16) {
+    atomicMax(&pk_nl[tok], nl);
+    atomicAdd(&pk_sum[tok], sum);
+  }
+  __syncthreads();
+  if (tid < 16) a.part[((size_t)tg * neg + eg) * 16 + tid] = make_uint2((unsigned)pk_nl[tid], pk_sum[tid]);
+}
+
 // Logits of 16 tokens x EPB experts per block (k ascending, :213-227).
 // Blocks of one token group share an XCD (block id mod 8), so that its x
 // rows come from that XCD's L2 after the first read: blocks 0 .. 8 * NEG *
@@ -243,6 +295,7 @@ __global__ __launch_bounds__(64 * WPB) void router_bcast_kernel(RouterTileArgs a
     const int e = eb + c;
     if (t < a.T && e < a.E) a.logits[(size_t)t * a.E + e] = a.b ? r.acc[c] + a.b[e] : r.acc[c];
   }
+  router_pack<RS::NT>(a, t0, tg, eg, neg);
 }
 
 // ---------------------------------------------------------------- select
@@ -254,6 +307,10 @@ struct SelectArgs {
   float* p;
   int* idx_user;
   float* p_user;
+  const uint2* part;   // the router blocks' partial x-table headers, or null
+  int neg;             // router blocks per token group
+  uint8_t* tabs;       // x unit tables
+  size_t tab_bytes;
 };
 
 __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs a) {
@@ -261,9 +318,31 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs
   __shared__ float sval[kSelectWaves][kMaxTopK];
   __shared__ float sexp[kSelectWaves][kMaxTopK];
   __shared__ ulonglong2 keys2[kSelectWaves][512];   // E <= 1024 keys per wave
-  const int wave = threadIdx.x / kWave;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int t = blockIdx.x * kSelectWaves + wave;
   if (t >= a.T) return;
+  if (a.part) {
+    // the token's x-table header from the router blocks' partials
+    const uint2* pp = a.part + (size_t)(t / 16) * a.neg * 16 + t % 16;
+    int nl = 1;
+    uint32_t sum = 0;
+    for (int q = lane; q < a.neg; q += kWave) {
+      const uint2 v = pp[(size_t)q * 16];
+      nl = (int)v.x > nl ? (int)v.x : nl;
+      sum += v.y;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const int o = __shfl_xor(nl, off, kWave);
+      nl = o > nl ? o : nl;
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    }
+    if (lane == 0) {
+      uint8_t* tab = a.tabs + (size_t)t * a.tab_bytes;
+      reinterpret_cast<int*>(tab)[0] = nl;
+      reinterpret_cast<uint32_t*>(tab)[1] = sum;
+    }
+  }
   const size_t q = (size_t)t * a.topk;
   select_token_any(a.logits + (size_t)t * a.E, a.E, a.topk, reinterpret_cast<uint64_t*>(keys2[wave]),
                    sidx[wave], sval[wave], sexp[wave], a.idx + q, a.p + q,
@@ -527,9 +606,10 @@ moe_status launch_router_bcast(const RouterTileArgs& a, hipStream_t s) {
 // Waves per router block: eight from 1024 tokens, four from 256, two below
 // (measured at E = 128, D = 2048), fewer where the block would hold more
 // experts than the layer.
-moe_status launch_router(const RouterTileArgs& a, hipStream_t s) {
+moe_status launch_router(const RouterTileArgs& a, hipStream_t s, int* neg) {
   int wpb = a.T >= 1024 ? 8 : a.T >= 256 ? 4 : 2;
   while (wpb > 1 && 4 * wpb > a.E) wpb /= 2;
+  *neg = (a.E + 4 * wpb - 1) / (4 * wpb);
   switch (wpb) {
     case 8: return launch_router_bcast<1, 128, 8>(a, s);
     case 4: return launch_router_bcast<1, 128, 4>(a, s);
@@ -540,8 +620,10 @@ moe_status launch_router(const RouterTileArgs& a, hipStream_t s) {
 
 }  // namespace
 
-moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s) {
-  SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out};
+moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s,
+                         const uint2* xpart, int neg) {
+  SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out,
+                xpart, neg, L->xtab, act_table_bytes(L->D)};
   dim3 sg((unsigned)((T + kSelectWaves - 1) / kSelectWaves));
   hipLaunchKernelGGL(select_kernel, sg, dim3(kSelectWaves * kWave), 0, s, sa);
   return check_hip(hipGetLastError(), "select launch");
@@ -552,34 +634,20 @@ bool grouped_ok(const LayerDev* L) {
   return L->D % 128 == 0 && expert_gemm_ok(L) && L->E <= kGroupThreads && is16(L->router_w);
 }
 
-constexpr int kPackOverlapTokens = 1024;
-
 moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resid, int T,
                                  float* out, int32_t* idx_out, float* p_out) {
   hipStream_t s = stream();
   moe_status st;
   if (!is16(xn) || !is16(out) || (resid && !is16(resid)))
     return set_error(MOE_ERR_ARG, "grouped forward: arrays must be 16-byte aligned");
-  // 1. x unit tables; for many tokens on the side stream, where they overlap
-  // the router, the selection and the grouping and are joined before gate/up
-  // (the fork and join cost ~8 us: more than the packing saves below ~1024
-  // tokens, measured)
-  const bool overlap = T >= kPackOverlapTokens;
-  if (overlap) {
-    hipStream_t s2 = side_stream();
-    if ((st = check_hip(hipEventRecord(fork_event(), s), "fork record")) ||
-        (st = check_hip(hipStreamWaitEvent(s2, fork_event(), 0), "fork wait")) ||
-        (st = launch_pack_units(L, xn, T, s2)) ||
-        (st = check_hip(hipEventRecord(join_event(), s2), "join record")))
-      return st;
-  } else if ((st = launch_pack_units(L, xn, T, s))) {
-    return st;
-  }
-  // 2. router logits, one sequential chain per lane
-  RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E};
-  if ((st = launch_router(ra, s))) return st;
-  // 3. top-k and gates
-  if ((st = launch_select(L, T, idx_out, p_out, s))) return st;
+  // 1-2. router logits (one sequential chain per lane) and, in the same
+  // blocks, the x unit tables of the expert kernels
+  RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E,
+                    L->xtab, act_table_bytes(L->D), L->dtype == 3, L->rpart};
+  int neg = 0;
+  if ((st = launch_router(ra, s, &neg))) return st;
+  // 3. top-k and gates; the x tables' headers
+  if ((st = launch_select(L, T, idx_out, p_out, s, L->rpart, neg))) return st;
   // 4. group pairs by expert, tasks of at most one block's pairs
   const int npairs = T * L->topk;
   const int nt = expert_gemm_tiles(L, T);
@@ -598,7 +666,6 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
                        L->E, per, L->ghist, nb, L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
   }
   if ((st = check_hip(hipGetLastError(), "group launch"))) return st;
-  if (overlap && (st = check_hip(hipStreamWaitEvent(s, join_event(), 0), "join wait"))) return st;
   // 5-6. gate/up + SwiGLU, down: grouped GEMMs on the 32x32x32 int8 MFMA
   if ((st = launch_expert_gemm(L, nt, ntask_max, s))) return st;
   // 7. ordered combine + residual

@@ -51,12 +51,16 @@ struct LayerDev {
                              // {expert | pairs << 16, first pair in perm}, x = -1 past the last
   float* y = nullptr;        // [T*topk][D]
   int* ghist = nullptr;      // [kGroupBlocks][E] pairs per expert of each grouping block
+  uint2* rpart = nullptr;    // [T/16 + 1][ceil(E/4)][16] the router blocks' partial x-table headers
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
 };
 
 // Top-k and softmax gates of T tokens from L->logits into L->idx / L->p
 // (and the caller's copies, when given): one wave per token.
-moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s);
+// With xpart set, each token's wave also combines the router blocks'
+// partial x-table headers (neg per token group of 16) into its table.
+moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s,
+                         const uint2* xpart = nullptr, int neg = 0);
 
 // Grouped (expert-major) forward for many tokens; requires grouped_ok(L).
 bool grouped_ok(const LayerDev* L);
@@ -71,7 +75,6 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
 bool expert_gemm_ok(const LayerDev* L);
 int expert_gemm_tiles(const LayerDev* L, int T);
 int expert_gemm_split(int nt);
-moe_status launch_pack_units(const LayerDev* L, const float* x, int T, hipStream_t s);
 moe_status launch_expert_gemm(const LayerDev* L, int nt, int ntask, hipStream_t s);
 
 // ---- routing: top-k by the insertion rule, softmax over the selection ----

@@ -320,7 +320,7 @@ struct ScratchBuf {
   size_t bytes = 0;
 };
 struct SharedScratch {
-  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, tasks, ghist;
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, tasks, ghist, rpart;
   unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
 };
 SharedScratch g_scratch;
@@ -329,10 +329,7 @@ std::mutex g_layer_mu;
 moe_status grow(ScratchBuf& b, size_t need, bool* synced) {
   if (need <= b.bytes) return MOE_OK;
   if (!*synced) {
-    // both streams: the expert-major path packs x tables on the side stream,
-    // and a forward that failed after forking it may not have joined it back
     moe_status st = check_hip(hipStreamSynchronize(stream()), "sync");
-    if (!st) st = check_hip(hipStreamSynchronize(side_stream()), "sync side stream");
     if (st) return st;
     *synced = true;
   }
@@ -363,7 +360,8 @@ moe_status ensure_scratch(LayerDev* L, int T) {
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
        (st = grow(S.perm, np * 4, &synced)) || (st = grow(S.y, np * L->D * 4, &synced)) ||
        (st = grow(S.tasks, (np / kMinSplitPairs + L->E + 1) * 8, &synced)) ||
-       (st = grow(S.ghist, (size_t)kGroupBlocks * L->E * 4, &synced))))
+       (st = grow(S.ghist, (size_t)kGroupBlocks * L->E * 4, &synced)) ||
+       (st = grow(S.rpart, ((size_t)T / 16 + 1) * ((L->E + 3) / 4) * 16 * 8, &synced))))
     return st;
   L->logits = (float*)S.logits.p; L->idx = (int*)S.idx.p; L->p = (float*)S.p.p;
   L->xtab = (uint8_t*)S.xtab.p; L->htab = (uint8_t*)S.htab.p; L->h = (float*)S.h.p;
@@ -371,6 +369,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   L->ecount = (int*)S.ecount.p; L->eoff = (int*)S.eoff.p; L->perm = (int*)S.perm.p;
   L->tasks = (int2*)S.tasks.p;
   L->ghist = (int*)S.ghist.p;
+  L->rpart = (uint2*)S.rpart.p;
   if (!S.sel_counter) {
     if ((st = dev_alloc(&S.sel_counter, 1))) return st;
     if ((st = check_hip(hipMemsetAsync(S.sel_counter, 0, 4, stream()), "counter init"))) return st;
@@ -799,6 +798,7 @@ moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, cons
   L->hpart = (uint32_t*)(base + o.hpart);
   L->xpart = (uint32_t*)(base + o.xpart);
   L->ecount = L->eoff = L->perm = L->ghist = nullptr;
+  L->rpart = nullptr;
   L->tasks = nullptr;
   L->y = nullptr;
   L->capT = T;

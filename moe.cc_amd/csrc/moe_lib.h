@@ -13,10 +13,4 @@ moe_status check_hip(hipError_t e, const char* what);
 moe_status ensure_init();
 // The library's stream.
 hipStream_t stream();
-// A second stream (default priority) for work that overlaps the library
-// stream's, forked from it with fork_event() and joined back with
-// join_event() (both recorded and waited on inside one call).
-hipStream_t side_stream();
-hipEvent_t fork_event();
-hipEvent_t join_event();
 }  // namespace moe

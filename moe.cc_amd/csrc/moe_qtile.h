@@ -57,6 +57,40 @@ __device__ __forceinline__ void block_max_sum(int nl, uint32_t part, int* scratc
   }
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Unit u (columns 16u .. 16u + 15) of an x *unit* table (the expert-major
+// path's layout: the act table's header and plane offsets, each limb plane
+// a sequence of 16-byte units, Q8 in column order, Q4 the 8 even columns
+// then the 8 odd ones): a = trunc(x * 7 or 127) (kernels.c:115 / :66) into
+// the four planes; the limb count and the wrapping sum fold into nl / part.
+template <bool Q4>
+__device__ __forceinline__ void pack_unit16(const float (&x)[16], uint8_t* tab, int K, int u, int& nl,
+                                            uint32_t& part) {
+  const float mult = Q4 ? 7.0f : 127.0f;
+  uint32_t b[16][4];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int32_t a = f2i_trunc_x86(x[i] * mult);
+    const int n = limbs_needed(a);
+    nl = n > nl ? n : nl;
+    part += (uint32_t)a;
+    split_limbs(a, b[i]);
+  }
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    u32x4 o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      // Q4: dwords 0-1 the even columns, 2-3 the odd ones
+      const int c0 = Q4 ? (d < 2 ? 8 * d : 8 * (d - 2) + 1) : 4 * d;
+      const int st = Q4 ? 2 : 1;
+      o[d] = pack4(b[c0][l], b[c0 + st][l], b[c0 + 2 * st][l], b[c0 + 3 * st][l]);
+    }
+    *reinterpret_cast<u32x4*>(const_cast<uint32_t*>(act_plane(tab, K, l)) + 4 * u) = o;
+  }
+}
+
 // Packs one activation row into its table.  Called by a whole block (whole
 // waves); contains barriers.  `scratch` is 2 ints of LDS.
 template <bool Q4>
@@ -175,7 +209,6 @@ struct TileGeom {
   static constexpr int ROW_BYTES = LPR * P * 16;
 };
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Weight rows are streamed once per launch: nontemporal loads keep them from
 // displacing reused data in the caches (measured ~+15% streaming bandwidth).

@@ -240,7 +240,7 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     (3, 300, 8, 512, 256, False, True, 1.0),
     (3, 520, 8, 256, 256, False, True, 40.0),    # split, 2-limb Q4
     (2, 280, 8, 512, 256, True, True, 0.3),      # split, one-limb Q8
-    (3, 2048, 8, 256, 256, False, True, 1.0),    # router with two token chains per lane
+    (3, 2048, 8, 256, 256, False, True, 1.0),    # 2048 tokens, router blocks cut to E = 8 experts
     # the config shape's D = 2048 and d_ff = 768 (16 and 6 stages of the LDS
     # ring), 16 experts so that 128 pairs per expert on average select the
     # four-tile, eight-wave blocks (the prefill bench's T = 2048 shape)
@@ -252,6 +252,9 @@ GROUPED = [  # dtype, T, E, D, d_ff, bias, resid, x scale
     # partial last tile of 256 rows (four-tile shape, one tile per block)
     (3, 96, 16, 384, 256, False, True, 1.0),
     (3, 256, 16, 384, 256, False, True, 1.0),
+    # x tables packed by 16 router blocks per token group, 24 units a token
+    # (uneven shares), two-limb activations, a partial last token group
+    (3, 50, 128, 384, 256, False, True, 40.0),
 ]
 
 
@@ -309,8 +312,8 @@ def test_grouped_mixed_limb_segments(moehip, dtype, T):
 
 def test_grouped_config_shape_T2048(moehip):
     """The prefill bench's layer shape (configs[3]: Q4, E = 128, D = 2048,
-    d_ff = 768, top-8) at T = 2048: two router chains per lane, x tables
-    packed on the side stream, one 256-pair task per expert, the two-launch
+    d_ff = 768, top-8) at T = 2048: eight-wave router blocks, x tables
+    packed by the router blocks, one 256-pair task per expert, the two-launch
     grouping, two down row tiles per block -- bit for bit against the
     oracle (its threaded build: 77 G multiply-adds)."""
     dtype, T, E, D, dff = 3, 2048, 128, 2048, 768
