@@ -353,11 +353,11 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
 }
 
 // Few tokens, few rows (the router): one block per (output row, token); with
-// NORM or PACK one token.  The token row is staged in LDS (normalized first
+// NORM one token.  The token row is staged in LDS (normalized first
 // when NORM, the sum of squares by block_seq_sum), the products x[k] *
 // W[n][k] are formed into LDS and summed in order by block_seq_sum, so a row
-// costs about K / 8 dependent adds instead of K.  With PACK each block packs its column slice of the
-// normalized row into the activation tables (row_finish_kernel writes the
+// costs about K / 8 dependent adds instead of K.  With PACK each block packs its column slice of its
+// token's (normalized) row into that token's activation table (row_finish_kernel writes the
 // header and, with a fused selection, picks the experts).
 // 512 threads: two waves per SIMD.  A wave issues a VALU instruction about
 // every 8 clocks whether or not it depends on the previous one, so the
@@ -435,7 +435,8 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
     __syncthreads();
     int nl;
     uint32_t sum;
-    pack_act_cols<PACK == 3>(xs, K, c0, c1, a.pack_tabs, tid, kRowThreads, nl, sum);
+    pack_act_cols<PACK == 3>(xs, K, c0, c1, a.pack_tabs + (size_t)m * act_table_bytes(K), tid, kRowThreads,
+                             nl, sum);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       const int on = __shfl_xor(nl, off, kWave);
@@ -448,7 +449,7 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
     }
     __syncthreads();
     if (tid == 0) {
-      uint32_t* pp = a.pack_part + (size_t)blockIdx.x * 2;
+      uint32_t* pp = a.pack_part + ((size_t)m * gridDim.x + blockIdx.x) * 2;
       pp[0] = (uint32_t)pack_scratch[0];
       pp[1] = (uint32_t)pack_scratch[1];
     }
@@ -509,18 +510,18 @@ __global__ __launch_bounds__(kRowThreads) void dense_rows4_kernel(DenseArgs a) {
 }
 
 // After dense_row_kernel (a kernel boundary instead of a fence in each of
-// its blocks): the activation table's header from the slices' partials and
-// each token's expert selection, one wave per token (M <= 4).
+// its blocks): each token's activation-table header from its slices'
+// partials and its expert selection, one wave per token (M <= 4).
 constexpr int kRowFinishWaves = 4;
 __global__ __launch_bounds__(kRowFinishWaves * kWave) void row_finish_kernel(DenseArgs a) {
   __shared__ uint64_t keys[kRowFinishWaves][1024];
   __shared__ int sidx[kRowFinishWaves][kMaxTopK];
   __shared__ float sval[kRowFinishWaves][kMaxTopK], sexp[kRowFinishWaves][kMaxTopK];
   const int lane = threadIdx.x % kWave, m = threadIdx.x / kWave;
-  if (a.pack_dtype && m == 0) {
+  if (a.pack_dtype && m < a.M) {
     uint32_t nl = 1, sum = 0;
     for (int b = lane; b < a.N; b += kWave) {
-      const uint32_t* pp = a.pack_part + (size_t)b * 2;
+      const uint32_t* pp = a.pack_part + ((size_t)m * a.N + b) * 2;
       nl = pp[0] > nl ? pp[0] : nl;
       sum += pp[1];
     }
@@ -531,7 +532,7 @@ __global__ __launch_bounds__(kRowFinishWaves * kWave) void row_finish_kernel(Den
       sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
     }
     if (lane == 0) {
-      uint32_t* hh = reinterpret_cast<uint32_t*>(a.pack_tabs);
+      uint32_t* hh = reinterpret_cast<uint32_t*>(a.pack_tabs + (size_t)m * act_table_bytes(a.K));
       hh[0] = nl;
       hh[1] = sum;
     }
@@ -1448,7 +1449,7 @@ int dense_amax_rows(int) { return 16; }
 // One token against few rows: the row kernel.
 // Row kernel: one token, or up to 4 without the fused rmsnorm and packing.
 bool dense_row_ok(const DenseArgs& a, bool vec) {
-  const bool rows = a.M == 1 || (a.M <= 4 && !a.norm && !a.pack_dtype);
+  const bool rows = a.M == 1 || (a.M <= 4 && !a.norm);
   return rows && a.N <= 1024 && vec && a.K <= kRowMaxK && !a.amax_part;
 }
 

@@ -496,8 +496,8 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
     ra.norm = 1; ra.norm_w = L->rms2_w; ra.eps = norm_eps;
     ra.xn_out = L->xn; ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
     xn = L->xn;
-  } else if (fuse_sel && T == 1 && dense_row_path(ra)) {
-    // one given row: the router's row kernel packs the x tables too
+  } else if (fuse_sel && T <= 4 && dense_row_path(ra)) {
+    // up to four given rows: the router's row kernel packs the x tables too
     ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
   } else {
     // x tables for the expert GEMVs
