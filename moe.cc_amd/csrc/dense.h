@@ -27,7 +27,9 @@ struct DenseArgs {
   // tables for the expert GEMVs (pack_dtype 2 / 3, tables of
   // act_table_bytes(K) bytes at pack_tabs; pack_part: scratch of
   // M * gridDim.x * 2 words for the slices' headers, reduced by the last
-  // block).
+  // block).  The 5-16 token rows kernel (dense_rows4_path) packs given rows
+  // without a norm or a fused selection: pack_part then holds N * 16 uint2
+  // {limbs, sum}, slice-major, combined by select_kernel.
   int norm = 0;
   const float* norm_w = nullptr;
   float eps = 0.0f;
@@ -66,6 +68,9 @@ bool dense_select_ok(int M, int N);
 // Whether dense_matmul runs `a` with the one-token row kernel (one block
 // per output row; with packing, pack_part then holds N partial headers).
 bool dense_row_path(const DenseArgs& a);
+// True where dense_matmul runs a (5-16 token, no norm, no fused selection)
+// product on the rows kernel, which can also pack the rows.
+bool dense_rows4_path(const DenseArgs& a);
 
 // x[t] = emb[ids[t]] (ids clamped to [0, V)), T rows of D floats.
 moe_status embed_rows(const int32_t* ids, int T, const float* emb, int V, int D, float* x,

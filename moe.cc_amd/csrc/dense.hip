@@ -471,14 +471,19 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
 // 5-16 tokens, few rows: a block per (output row, four tokens), its 512
 // threads four groups of 128 side by side, each the row kernel on its own
 // token -- products x[k] * W[n][k] into its LDS slice, summed in order by
-// group_seq_sum (four candidate chains per thread).  No norm, no packing.
+// group_seq_sum (four candidate chains per thread).  No norm.  With PACK
+// each group also packs the block's column slice of its token's row into
+// the token's activation table and leaves the slice's partial header at
+// pack_part[slice][token] (uint2 {limbs, sum}; select_kernel combines them).
 constexpr int kRowGroups = 4;
 constexpr int kRowGroupThreads = kRowThreads / kRowGroups;
 constexpr int kRowsMaxK = 4096;
 
+template <int PACK>
 __global__ __launch_bounds__(kRowThreads) void dense_rows4_kernel(DenseArgs a) {
   extern __shared__ float4 rg4[];   // [kRowGroups][K] products
   __shared__ SeqSumScratch seq[kRowGroups];
+  __shared__ int pk[kRowGroups][2];
   const int K = a.K, k4 = K / 4, n = blockIdx.x;
   const int g = threadIdx.x / kRowGroupThreads, gt = threadIdx.x % kRowGroupThreads;
   const int mg = blockIdx.y * kRowGroups + g;   // this group's token (past M: a repeat, not written)
@@ -498,6 +503,28 @@ __global__ __launch_bounds__(kRowThreads) void dense_rows4_kernel(DenseArgs a) {
     const int i = gt + kRowGroupThreads * u;
     wv[u] = i < k4 ? w4[i] : zero4();
   }
+  if constexpr (PACK != 0) {
+    // the block's column slice [c0, c1) (a multiple of 8 columns)
+    const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
+    const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
+    if (gt == 0) { pk[g][0] = 1; pk[g][1] = 0; }
+    int nl = 1;
+    uint32_t sum = 0;
+    if (mg < a.M)
+      pack_act_cols<PACK == 3>(a.A + (size_t)m * a.lda, K, c0, c1, a.pack_tabs + (size_t)m * act_table_bytes(K),
+                               gt, kRowGroupThreads, nl, sum);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int on = __shfl_xor(nl, off, kWave);
+      nl = on > nl ? on : nl;
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    }
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) {
+      atomicMax(&pk[g][0], nl);
+      atomicAdd(reinterpret_cast<unsigned*>(&pk[g][1]), sum);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < WV; ++u) {
     const int i = gt + kRowGroupThreads * u;
@@ -505,6 +532,10 @@ __global__ __launch_bounds__(kRowThreads) void dense_rows4_kernel(DenseArgs a) {
       pv4[i] = make_float4(xv[u].x * wv[u].x, xv[u].y * wv[u].y, xv[u].z * wv[u].z, xv[u].w * wv[u].w);
   }
   __syncthreads();
+  if constexpr (PACK != 0) {
+    if (gt == 0 && mg < a.M)
+      reinterpret_cast<uint2*>(a.pack_part)[(size_t)n * 16 + mg] = make_uint2((unsigned)pk[g][0], (unsigned)pk[g][1]);
+  }
   const float acc = group_seq_sum<kRowGroupThreads>(reinterpret_cast<const float*>(pv4), K, seq[g], gt);
   if (gt == 0 && mg < a.M) a.C[(size_t)m * a.ldc + n] = dense_epilogue(a, m, n, acc);
 }
@@ -1454,8 +1485,14 @@ bool dense_row_ok(const DenseArgs& a, bool vec) {
 }
 
 bool dense_rows4_ok(const DenseArgs& a, bool vec) {
-  return a.M > 4 && a.M <= 16 && !a.norm && !a.pack_dtype && !a.sel_counter && !a.amax_part &&
-         a.N <= 1024 && vec && a.K <= kRowsMaxK;
+  return a.M > 4 && a.M <= 16 && !a.norm && !a.sel_counter && !a.amax_part && a.N <= 1024 && vec &&
+         a.K <= kRowsMaxK;
+}
+
+bool dense_rows4_path(const DenseArgs& a) {
+  const bool vec = a.K > 0 && a.K % 4 == 0 && a.lda % 4 == 0 && a.ldw % 4 == 0 && al16(a.A) &&
+                   al16(a.W);
+  return a.N > 0 && dense_rows4_ok(a, vec);
 }
 
 bool dense_row_path(const DenseArgs& a) {
@@ -1515,8 +1552,10 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(dense_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), "dense generic launch");
   }
-  if (a.pack_dtype && (!a.sel_counter || !a.pack_part || !a.pack_tabs || !dense_row_ok(a, vec)))
-    return set_error(MOE_ERR_ARG, "dense matmul: packing a given row needs the row kernel and the fused selection");
+  if (a.pack_dtype && (!a.pack_part || !a.pack_tabs ||
+                       !((a.sel_counter && dense_row_ok(a, vec)) || dense_rows4_ok(a, vec))))
+    return set_error(MOE_ERR_ARG, "dense matmul: packing given rows needs the row kernel and the fused "
+                                  "selection, or the 5-16 token rows kernel");
   if (dense_row_ok(a, vec)) {
     if (a.pack_dtype == 2) return launch_row<false, 2>(a, s);
     if (a.pack_dtype == 3) return launch_row<false, 3>(a, s);
@@ -1524,10 +1563,18 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   }
   if (dense_rows4_ok(a, vec)) {
     const size_t lds = (size_t)kRowGroups * a.K * 4;
-    moe_status st = set_lds(dense_rows4_kernel, lds, "rows kernel LDS attribute");
-    if (st) return st;
-    hipLaunchKernelGGL(dense_rows4_kernel, dim3((unsigned)a.N, (unsigned)((a.M + kRowGroups - 1) / kRowGroups)),
-                       dim3(kRowThreads), lds, s, a);
+    const dim3 grid((unsigned)a.N, (unsigned)((a.M + kRowGroups - 1) / kRowGroups));
+    moe_status st;
+    if (a.pack_dtype == 2) {
+      if ((st = set_lds(dense_rows4_kernel<2>, lds, "rows kernel LDS attribute"))) return st;
+      hipLaunchKernelGGL(dense_rows4_kernel<2>, grid, dim3(kRowThreads), lds, s, a);
+    } else if (a.pack_dtype == 3) {
+      if ((st = set_lds(dense_rows4_kernel<3>, lds, "rows kernel LDS attribute"))) return st;
+      hipLaunchKernelGGL(dense_rows4_kernel<3>, grid, dim3(kRowThreads), lds, s, a);
+    } else {
+      if ((st = set_lds(dense_rows4_kernel<0>, lds, "rows kernel LDS attribute"))) return st;
+      hipLaunchKernelGGL(dense_rows4_kernel<0>, grid, dim3(kRowThreads), lds, s, a);
+    }
     return check_hip(hipGetLastError(), "dense rows launch");
   }
   if (a.sel_counter) {

@@ -40,8 +40,8 @@ struct LayerDev {
   float* h = nullptr;        // [T*topk][dff] (decode kernels)
   float* xn = nullptr;       // [T][D] normed input (block forward)
   uint32_t* hpart = nullptr; // [T*topk][h segments][2] partial headers of the h tables
-  uint32_t* xpart = nullptr; // [T][router blocks][2] partial headers of the x tables (fused
-                             // rmsnorm + router)
+  uint32_t* xpart = nullptr; // partial headers of the x tables packed by the router: up to 4
+                             // tokens [T][router blocks][2], 5-16 [router blocks][16][2]
   // grouped kernels: pairs per expert, first pair of each expert in `perm`,
   // pair ids (t * topk + j) grouped by expert, expert outputs per pair
   int* ecount = nullptr;     // [E]

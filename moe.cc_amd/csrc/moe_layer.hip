@@ -354,7 +354,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
       (st = grow(S.htab, np * act_table_bytes(L->dff), &synced)) ||
       (st = grow(S.h, np * L->dff * 4, &synced)) || (st = grow(S.xn, (size_t)T * L->D * 4, &synced)) ||
       (st = grow(S.hpart, np * (size_t)((L->dff + 7) / 8) * 8, &synced)) ||
-      (st = grow(S.xpart, (size_t)std::min(T, 4) * (L->E + 16) * 8, &synced)))
+      (st = grow(S.xpart, (size_t)(T > 4 ? 16 : T) * (L->E + 16) * 8, &synced)))
     return st;
   if (grouped_ok(L) &&
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
@@ -499,6 +499,10 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
   } else if (fuse_sel && T <= 4 && dense_row_path(ra)) {
     // up to four given rows: the router's row kernel packs the x tables too
     ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
+  } else if (!fuse_sel && dense_rows4_path(ra)) {
+    // 5-16 given rows: the router's rows kernel packs the x tables too, the
+    // selection kernel writes their headers
+    ra.pack_dtype = L->dtype; ra.pack_tabs = L->xtab; ra.pack_part = L->xpart;
   } else {
     // x tables for the expert GEMVs
     QShape sh;
@@ -515,7 +519,11 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
   const bool sel_gu = fuse_sel && T == 1 && L->E <= kTileBlock && dense_row_path(ra) && !sel_kernel;
   ra.sel_defer = sel_gu ? 1 : 0;
   if ((st = dense_matmul(ra, s))) return st;
-  if (!fuse_sel && (st = launch_select(L, T, idx_out, p_out, s))) return st;
+  const bool rows_pack = !fuse_sel && ra.pack_dtype != 0;
+  if (!fuse_sel && (st = launch_select(L, T, idx_out, p_out, s,
+                                       rows_pack ? reinterpret_cast<const uint2*>(L->xpart) : nullptr,
+                                       rows_pack ? L->E : 0)))
+    return st;
   const int nxpart = ra.pack_dtype ? L->E : 0;
   int nchunks = 0;
   if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out); });
@@ -585,7 +593,7 @@ NoAllocLayout noalloc_layout(const LayerDev* L, int T) {
   o.h = take(np * L->dff * 4);
   o.xn = take((size_t)T * L->D * 4);
   o.hpart = take(np * (size_t)((L->dff + 7) / 8) * 8);
-  o.xpart = take((size_t)std::min(T, 4) * (L->E + 16) * 8);
+  o.xpart = take((size_t)(T > 4 ? 16 : T) * (L->E + 16) * 8);
   o.total = at;
   return o;
 }
