@@ -73,6 +73,24 @@ struct GateUpEpiMaker {
   __device__ GateUpEpi at(int) const { return e; }
 };
 
+// Block -> (row chunk r, item q) of an nr x nq launch (1-D grid) so that
+// all items of one row chunk run on one XCD (blocks are dealt to the 8 XCDs
+// in turn) one after another: pairs or tokens that share an expert then
+// read its rows of that chunk from HBM once and from that XCD's L2 after.
+// Row chunks past the last multiple of 8 go in row order.
+__device__ __forceinline__ void xcd_chunk_item(int nr, int nq, int* r, int* q) {
+  const int L = blockIdx.x, nr8 = nr & ~7;
+  if (L < nr8 * nq) {
+    const int slot = L / 8;
+    *r = (slot / nq) * 8 + L % 8;
+    *q = slot % nq;
+  } else {
+    const int k = L - nr8 * nq;
+    *r = nr8 + k / nq;
+    *q = k % nq;
+  }
+}
+
 struct GateUpArgs {
   const uint8_t* gq; const float* gs; const uint8_t* uq; const float* us;
   long long rb; int D, dff, topk;
@@ -80,6 +98,7 @@ struct GateUpArgs {
   float* h; uint8_t* htab; size_t htab_bytes;
   uint32_t* hpart;      // [pair][chunk][2] partial (limbs, sum) of each row chunk of h
   int nchunks, rows_per_block;
+  int npairs;           // the launch is nchunks x npairs blocks (xcd_chunk_item)
   // SEL (one token, E <= kTileBlock): the selection is made here, from the
   // router logits and the x table's nxpart partial headers; p and the
   // caller's copies (may be null) get the gates
@@ -107,7 +126,8 @@ template <bool Q4, class G, bool SEL>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   extern __shared__ float hb[];   // [rows_per_block]
   __shared__ int red[2];   // limb count, activation sum
-  const int q = blockIdx.y;
+  int rc, q;
+  xcd_chunk_item(a.nchunks, a.npairs, &rc, &q);
   int e;
   int x_nl = 0;
   // the token's activation sum, handed to the row streaming by address: in
@@ -132,7 +152,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     x_nl = a.nxpart > 0 ? xred[0] : 0;
     x_sum[0] = (uint32_t)xred[1];   // every thread stores the same value before reading it
     e = sidx[q];
-    if (blockIdx.x == 0 && q == 0) {
+    if (rc == 0 && q == 0) {
       if (tid < kWave)
         select_gates(a.topk, sidx, sval, sexp, a.idx_w, a.p, a.idx_user, a.p_user);
       if (tid == 0 && a.nxpart > 0) {
@@ -146,7 +166,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   }
   if (e < 0) return;
   const int t = q / a.topk;
-  const int r0 = blockIdx.x * a.rows_per_block;
+  const int r0 = rc * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.dff ? r0 + a.rows_per_block : a.dff;
   const uint8_t* W[2] = {a.gq + (size_t)e * a.dff * a.rb, a.uq + (size_t)e * a.dff * a.rb};
   const uint8_t* tabs[1] = {a.xtab + (size_t)t * a.tab_bytes};
@@ -170,7 +190,7 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   block_max_sum(nl, sum, red);
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + blockIdx.x) * 2;
+    uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + rc) * 2;
     pp[0] = (uint32_t)red[0];
     pp[1] = (uint32_t)red[1];
   }
@@ -181,6 +201,7 @@ struct DownArgs {
   const int* idx; const float* p; const uint8_t* htab; size_t tab_bytes; const float* h;
   const uint32_t* hpart; int nchunks;
   const float* resid; float* out; int rows_per_block;
+  int nrc;   // row chunks: the launch is nrc x T blocks (xcd_chunk_item)
 };
 
 // Epilogue of down: yb[j][row - r0] = Q(h_j Wd_j)  (LDS)
@@ -210,8 +231,9 @@ struct DownEpiMaker {
 template <bool Q4, class G>
 __global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs a) {
   extern __shared__ float yb[];   // [topk][rows_per_block]
-  const int t = blockIdx.y;
-  const int r0 = blockIdx.x * a.rows_per_block;
+  int rc, t;
+  xcd_chunk_item(a.nrc, a.T, &rc, &t);
+  const int r0 = rc * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.D ? r0 + a.rows_per_block : a.D;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   for (int j = wave; j < a.topk; j += kCombineWaves) {
@@ -410,7 +432,8 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
   GateUpArgs a{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk, L->idx,
                L->xtab, act_table_bytes(L->D), xn, L->h, L->htab, act_table_bytes(L->dff),
                L->hpart, nc, (int)rpb};
-  dim3 grid((unsigned)nc, (unsigned)npairs);
+  a.npairs = npairs;
+  dim3 grid((unsigned)(nc * npairs));
   if (sel) {
     a.logits = L->logits; a.xpart = L->xpart; a.nxpart = nxpart; a.E = L->E;
     a.idx_w = L->idx; a.p = L->p; a.idx_user = idx_out; a.p_user = p_out;
@@ -431,7 +454,8 @@ void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, floa
   rpb = std::min<long long>(rpb, 16 * unit);
   DownArgs a{L->dq, L->ds, L->rbd, T, L->D, L->dff, L->topk, L->idx, L->p, L->htab,
              act_table_bytes(L->dff), L->h, L->hpart, nchunks, resid, out, (int)rpb};
-  dim3 grid((unsigned)((L->D + rpb - 1) / rpb), (unsigned)T);
+  a.nrc = (int)((L->D + rpb - 1) / rpb);
+  dim3 grid((unsigned)(a.nrc * T));
   hipLaunchKernelGGL((down_combine_kernel<Q4, G>), grid, dim3(kCombineThreads),
                      (size_t)L->topk * rpb * 4, s, a);
 }
