@@ -1592,12 +1592,14 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   } else if (a.M <= 16) {
     return launch_gemv<4, false, 0, 1>(a, s);
   } else if (a.M >= 256 && (long long)((a.N + 63) / 64) * ((a.M + 63) / 64) >= 1024) {
-    // 64 x 64 tiles only with >= 1024 blocks; below that 32 x 32 tiles keep
-    // more waves on each SIMD (prefill at T = 512: Wo 256 and [Wq;Wk;Wv]
-    // 640 blocks of 64 x 64; the model's 512-token prefill 49.7 -> 43.5 ms)
+    // 64 x 64 tiles only with >= 1024 blocks; below that 32-token x 64-row
+    // tiles keep more waves on each SIMD (prefill at T = 512: Wo 256 and
+    // [Wq;Wk;Wv] 640 blocks of 64 x 64; the model's 512-token prefill 49.7
+    // -> 43.5 ms with 32 x 32 tiles, 41.5 -> 39.8 ms with 32 x 64: eight
+    // chains a thread, each x value read for four rows)
     return launch_tile<4, 4, 32>(a, s);
   } else {
-    return launch_tile<2, 2, 64>(a, s);
+    return launch_tile<2, 4, 64>(a, s);
   }
   return check_hip(hipGetLastError(), "dense gemv launch");
 }
