@@ -896,7 +896,7 @@ moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
 template <bool Q4>
 moe_status launch_eg(const LayerDev* L, int nt, int ntask, hipStream_t s) {
   switch (nt) {
-    case 1: return launch_eg_shape<Q4, 4, 1, 3, 4, 1>(L, ntask, s);
+    case 1: return launch_eg_shape<Q4, 4, 1, 3, 4, 2>(L, ntask, s);
     case 2: return launch_eg_shape<Q4, 2, 1, 4, 4, 4>(L, ntask, s);
     case 4: return launch_eg_shape<Q4, 4, 4, 3, 8, 2>(L, ntask, s);
     default: return set_error(MOE_ERR_ARG, "expert gemm: %d pair tiles", nt);
