@@ -1146,12 +1146,56 @@ __global__ __launch_bounds__(256) void attn_scores_qt_kernel(AttnArgs a) {
   }
 }
 
-// Softmax and weighted V sum of query rows t0 .. t0 + kQt - 1 of head
-// blockIdx.y for dimensions d0 .. d0 + kPvDpb - 1: thread (qi, dd) =
-// (tid / kPvDpb, tid % kPvDpb).  Row qi (n = pos0 + t0 + qi + 1 scores) in
-// LDS; its max by its kPvDpb threads (order-free, a NaN first score wins as
-// in attn_softmax_pv_kernel), e = expf(s - m), the sum chain in thread dd =
-// 0, p = e * (1 / (sum + 1e-9)); then V staged kPvCh positions at a time and
+// Softmax of the score rows of the query-tiled path, in place, once per
+// (query row, head): one wave each, row t of head h (n = pos0 + t + 1
+// scores) staged in LDS; its max by the wave (order-free; a NaN first score
+// wins, as in attn_softmax_pv_kernel), e = expf(s - m), the sum chain in
+// lane 0, p = e * (1 / (sum + 1e-9)) written back over the scores
+// (test_model_trace.c:411-420).  attn_pv_qt_kernel then reads p.
+constexpr int kSmRowWaves = 4;
+
+size_t attn_softmax_rows_lds(int pos0, int T) {
+  return (size_t)kSmRowWaves * (size_t)((pos0 + T + 3) & ~3) * 4;
+}
+
+__global__ __launch_bounds__(kSmRowWaves * kWave) void attn_softmax_rows_kernel(AttnArgs a) {
+  extern __shared__ float smr[];   // [kSmRowWaves][ES]
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int h = blockIdx.x * kSmRowWaves + wave, t = blockIdx.y;
+  if (h >= a.nq) return;   // (no block barriers below)
+  const int ES = (a.pos0 + a.T + 3) & ~3;
+  float* er = smr + (size_t)wave * ES;
+  const int n = a.pos0 + t + 1;
+  float* Srow = a.S + ((size_t)t * a.nq + h) * a.max_seq;
+  float mx = -__builtin_inff();
+  for (int i = lane; i < n; i += kWave) {
+    const float v = Srow[i];
+    er[i] = v;
+    if (v == v && v > mx) mx = v;
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off, kWave);
+    mx = o > mx ? o : mx;
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  const float s0 = er[0];
+  const float m = s0 != s0 ? s0 : mx;
+  for (int i = lane; i < n; i += kWave) er[i] = expf_glibc(er[i] - m);
+  for (int i = n + lane; i < ((n + 3) & ~3); i += kWave) er[i] = 0.0f;
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  float inv = 0.0f;
+  if (lane == 0) inv = 1.0f / (chain_sum(0.0f, er, (n + 3) / 4) + 1e-9f);
+  inv = __shfl(inv, 0, kWave);
+  for (int i = lane; i < n; i += kWave) Srow[i] = er[i] * inv;
+}
+
+// Weighted V sum of query rows t0 .. t0 + kQt - 1 of head blockIdx.y for
+// dimensions d0 .. d0 + kPvDpb - 1: thread (qi, dd) = (tid / kPvDpb, tid %
+// kPvDpb).  Row qi's probabilities (n = pos0 + t0 + qi + 1, from
+// attn_softmax_rows_kernel) in LDS; V staged kPvCh positions at a time and
 // out = (((0 + p_0 v_0) + p_1 v_1) + ...) over the row's positions in order.
 constexpr int kPvDpb = 32;
 constexpr int kPvCh = 128;
@@ -1170,41 +1214,16 @@ __global__ __launch_bounds__(256) void attn_pv_qt_kernel(AttnArgs a) {
   const int ES = (a.pos0 + a.T + 3) & ~3;            // row stride of es
   float* es = lds;                                    // [kQt][ES]
   float* vt = es + (size_t)kQt * ES;                  // [kPvCh][kPvDpb]
-  __shared__ float inv_s[kQt];
   const int nt = min(kQt, a.T - t0);
   const int nmax = a.pos0 + t0 + nt;                  // positions of the last row
   const bool row_live = qi < nt;
   const int n = row_live ? a.pos0 + t0 + qi + 1 : 0;
   const int kvh = h / (a.nq / a.nkv);
   float* er = es + (size_t)qi * ES;
-  // 1. the row's scores, its max, the exponentials
+  // 1. the row's probabilities (attn_softmax_rows_kernel)
   const float* Srow = a.S + ((size_t)(t0 + qi) * a.nq + h) * a.max_seq;
-  float mx = -__builtin_inff();
-  for (int i = dd; i < n; i += kPvDpb) {
-    const float s = Srow[i];
-    er[i] = s;
-    if (s == s && s > mx) mx = s;
-  }
-#pragma unroll
-  for (int off = kPvDpb / 2; off > 0; off >>= 1) {
-    const float o = __shfl_xor(mx, off, kWave);
-    mx = o > mx ? o : mx;
-  }
-  __syncthreads();
-  float m = mx;
-  if (n > 0) {
-    const float s0 = er[0];
-    if (s0 != s0) m = s0;
-  }
-  for (int i = dd; i < n; i += kPvDpb) er[i] = expf_glibc(er[i] - m);
+  for (int i = dd; i < n; i += kPvDpb) er[i] = Srow[i];
   for (int i = n + dd; i < ((n + 3) & ~3); i += kPvDpb) er[i] = 0.0f;
-  __syncthreads();
-  if (dd == 0 && row_live) inv_s[qi] = 1.0f / (chain_sum(0.0f, er, (n + 3) / 4) + 1e-9f);
-  __syncthreads();
-  if (row_live) {
-    const float inv = inv_s[qi];
-    for (int i = dd; i < n; i += kPvDpb) er[i] = er[i] * inv;
-  }
   // 2. the weighted V sums
   const float* vbase = a.vc + (size_t)kvh * a.max_seq * hd + d0;
   const int dl = min(kPvDpb, hd - d0);
@@ -1632,6 +1651,11 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
                        dim3((unsigned)((a.pos0 + a.T + 63) / 64), (unsigned)a.nq, (unsigned)((a.T + kSq - 1) / kSq)),
                        dim3(256), lds_s, s, a);
     if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
+    const size_t lds_m = attn_softmax_rows_lds(a.pos0, a.T);
+    if ((st = set_lds(attn_softmax_rows_kernel, lds_m, "softmax rows LDS attribute"))) return st;
+    hipLaunchKernelGGL(attn_softmax_rows_kernel, dim3((unsigned)((a.nq + kSmRowWaves - 1) / kSmRowWaves), (unsigned)a.T),
+                       dim3(kSmRowWaves * kWave), lds_m, s, a);
+    if ((st = check_hip(hipGetLastError(), "softmax rows launch"))) return st;
     const size_t lds_p = attn_pv_qt_lds(a.pos0, a.T);
     if ((st = set_lds(attn_pv_qt_kernel, lds_p, "softmax/pv LDS attribute"))) return st;
     hipLaunchKernelGGL(attn_pv_qt_kernel, dim3((unsigned)((a.hd + kPvDpb - 1) / kPvDpb), (unsigned)a.nq, qg),
