@@ -168,6 +168,33 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
+def read_stream(pools, steps):
+    """The plain read-only stream over each pool's weights
+    (moe_stream_read_dev: the GEMV's 16-byte nontemporal loads, nothing
+    else), for a pass that no cache holds.  Returns GB/s per pool.  On
+    MI355X it is not an upper bound for the GEMV: the HBM read rate depends
+    on the data and the access order (a constant buffer streams at ~7.1
+    TB/s, these quantized weights at ~6.0, while the GEMV reads them at
+    ~6.5)."""
+    L = M.lib()
+    sink = M.DeviceBuffer(16)
+    rates = []
+    for p in pools:
+        M.check(L.moe_memset(sink.ptr, 0, 16))
+        for _ in range(2):
+            M.check(L.moe_stream_read_dev(p.q.ptr, p.weight_bytes, sink.ptr), "stream read")
+        a, b = M.Event(), M.Event()
+        a.record()
+        for _ in range(steps):
+            M.check(L.moe_stream_read_dev(p.q.ptr, p.weight_bytes, sink.ptr), "stream read")
+        b.record()
+        M.synchronize()
+        ms = a.elapsed_ms(b) / steps
+        rates.append(round(p.weight_bytes / (ms * 1e-3) / 1e9, 1))
+    sink.free()
+    return rates
+
+
 def run_gemv(args, dtype, shapes, workload):
     M.init(0)
     copy_calibration()
@@ -220,6 +247,8 @@ def run_gemv(args, dtype, shapes, workload):
                            "avg_pack_us": round(float(np.mean(pack_ms)) * 1e3, 2),
                            "algorithmic_bytes_per_launch": p.bytes_per_launch,
                            "achieved_GBs": round(p.bytes_per_launch / (avg * 1e-3) / 1e9, 1)})
+    for k, c in zip(per_kernel, read_stream(pools, args.steps)):
+        k["read_stream_GBs"] = c
     bytes_step = sum(p.bytes_per_launch for p in pools)
     ms_step = total_ms / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
@@ -238,7 +267,9 @@ def run_gemv(args, dtype, shapes, workload):
         "roofline": {"bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dom["kernel"]), "kernel": dom["kernel"],
-                     "algorithmic_bytes": dom["algorithmic_bytes_per_launch"]},
+                     "algorithmic_bytes": dom["algorithmic_bytes_per_launch"],
+                     # the plain read-only stream over the same pool (moe_stream_read_dev)
+                     "read_stream_same_pool": dom["read_stream_GBs"]},
         "kernels": per_kernel,
         "wall_s_timed": round(wall, 3),
     }

@@ -180,6 +180,15 @@ moe_status moe_matmul_q_batched_dev(int dtype, const moe_qjob* jobs_dev, int njo
  * are not one of the tiled widths 192..4096 return MOE_ERR_ARG. */
 size_t moe_act_table_bytes(int K);
 moe_status moe_act_pack_dev(int dtype, const float* A, int M, int K, void* tabs);
+/* Measurement helper, no counterpart in the reference: reads `bytes` (a
+ * multiple of 16) at src (16-byte aligned) once with 16-byte nontemporal
+ * loads on the library stream and XORs every 32-bit word into *sink (device
+ * memory, zeroed by the caller).  Its rate over a pool that no cache holds is
+ * the plain read stream reported beside the GEMV roofline (on MI355X the HBM
+ * read rate depends on the data and the access order: a constant buffer
+ * streams faster than quantized weights, which the GEMV itself reads faster
+ * than this stream). */
+moe_status moe_stream_read_dev(const void* src, size_t bytes, uint32_t* sink);
 moe_status moe_matmul_q_prepacked_dev(int dtype, const moe_qjob* jobs_dev, int njobs,
                                       int M, int N, int K, const void* tabs);
 

@@ -392,6 +392,15 @@ static moe_status prepacked_shape(int dtype, int M, int N, int K, const char* wh
   return MOE_OK;
 }
 
+moe_status moe_stream_read_dev(const void* src, size_t bytes, uint32_t* sink) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  if (!src || !sink) return set_error(MOE_ERR_ARG, "stream_read: null pointer");
+  if (((uintptr_t)src % 16) != 0 || bytes % 16 != 0 || ((uintptr_t)sink % 4) != 0)
+    return set_error(MOE_ERR_ARG, "stream_read: src and bytes must be multiples of 16");
+  return check_hip(launch_stream_read(src, bytes, sink, g_stream), "stream_read launch");
+}
+
 moe_status moe_act_pack_dev(int dtype, const float* A, int M, int K, void* tabs) {
   moe_status st = ensure_init();
   if (st) return st;

@@ -263,6 +263,36 @@ __global__ void zero_fill(float* p, size_t n) {
   if (i < n) p[i] = 0.0f;
 }
 
+// Read-only stream of n16 16-byte words: the plain HBM read rate on a pass
+// over data that no cache holds, reported beside the GEMV's.  The blocks
+// sweep the span together, tile t (8 words a thread, eight
+// nontemporal 16-byte loads in flight: the GEMV's load kind) by block t mod
+// the grid, and the words fold into one XOR per wave (so that no load is
+// dead), combined into *sink.
+constexpr int kStreamUnroll = 8;
+__global__ __launch_bounds__(kBlock) void stream_read_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                             uint32_t* sink) {
+  constexpr size_t tile = (size_t)kStreamUnroll * kBlock;
+  const size_t ntiles = n16 / tile;
+  uint32_t acc = 0;
+  for (size_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const u32x4* q = p + t * tile + threadIdx.x;
+    u32x4 v[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) v[u] = __builtin_nontemporal_load(q + u * kBlock);
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  for (size_t i = ntiles * tile + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * kBlock) {
+    const u32x4 v = __builtin_nontemporal_load(p + i);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off, kWave);
+  if (threadIdx.x % kWave == 0 && acc != 0u) atomicXor(sink, acc);
+}
+
 // ---- host-side variant selection ----
 using TiledFn = void (*)(TiledArgs);
 
@@ -439,6 +469,19 @@ hipError_t launch_f32gemv(const float* A, const float* W, float* C, int M, int N
   const unsigned blocks = (unsigned)((total + kBlock - 1) / kBlock);
   hipLaunchKernelGGL(f32gemv_seq, dim3(blocks), dim3(kBlock), 0, stream, A, W, C, M, N, K, lda,
                      ldw, ldc);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream) {
+  const size_t n16 = bytes / 16;
+  if (n16 == 0) return hipSuccess;
+  // four blocks a CU (256 CUs; measured on quantized weights: 6.0 TB/s, 5.6
+  // with eight, 4.3 with sixteen), fewer for small spans
+  const size_t tile = (size_t)kStreamUnroll * kBlock;
+  const size_t want = (n16 + tile - 1) / tile;
+  const unsigned blocks = (unsigned)(want < 1024 ? want : 1024);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                     reinterpret_cast<const u32x4*>(src), n16, sink);
   return hipGetLastError();
 }
 

@@ -45,6 +45,10 @@ size_t act_table_size(int K);
 hipError_t launch_f32gemv(const float* A, const float* W, float* C, int M, int N, int K,
                           int lda, int ldw, int ldc, hipStream_t stream);
 
+// Read-only stream of bytes / 16 16-byte words at src (16-byte aligned), the
+// XOR of all its 32-bit words folded into *sink (the caller zeroes it).
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
+
 // Zero-fill used for unsupported dtypes (kernels.c:172-179).
 hipError_t launch_zero(float* C, size_t n, hipStream_t stream);
 

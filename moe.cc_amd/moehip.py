@@ -66,6 +66,7 @@ _SIGS = {
     "moe_memcpy_d2h": (_I, [_P, _P, _SZ]),
     "moe_memcpy_d2d": (_I, [_P, _P, _SZ]),
     "moe_memset": (_I, [_P, _I, _SZ]),
+    "moe_stream_read_dev": (_I, [_P, _SZ, _P]),
     "moe_event_create": (_I, [ctypes.POINTER(_P)]),
     "moe_event_record": (_I, [_P]),
     "moe_event_elapsed_ms": (_I, [_P, _P, ctypes.POINTER(ctypes.c_float)]),

@@ -180,3 +180,22 @@ def test_prepacked_rejects_untiled_shapes(moehip):
     assert L.moe_matmul_q_prepacked_dev(2, buf.ptr, 1, 1, 4, 100, buf.ptr) != 0
     assert b"tiled" in L.moe_last_error()
     assert L.moe_act_pack_dev(2, buf.ptr, 1, 2048, buf.ptr + 4) != 0  # misaligned tables
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, 3 * (1 << 20) + 48, 64 << 20])
+def test_stream_read_ceiling_kernel(moehip, nbytes):
+    """The plain read-only stream that bench.py times beside the GEMV reads
+    every word once: the XOR of all 32-bit words it folds into the sink
+    equals the host's, for spans that split unevenly over the blocks and
+    threads."""
+    M_ = moehip
+    rng = np.random.default_rng(nbytes)
+    words = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint32)
+    d = M_.DeviceBuffer.from_array(words)
+    sink = M_.DeviceBuffer(16)
+    M_.check(M_.lib().moe_memset(sink.ptr, 0, 16), "memset")
+    M_.check(M_.lib().moe_stream_read_dev(d.ptr, nbytes, sink.ptr), "stream read")
+    got = int(sink.download((4,), np.uint32)[0])
+    assert got == int(np.bitwise_xor.reduce(words))
+    # sizes that are not whole 16-byte words are rejected
+    assert M_.lib().moe_stream_read_dev(d.ptr, nbytes - 4, sink.ptr) != 0
