@@ -66,6 +66,7 @@ __global__ __launch_bounds__(kBlock) void act_pack_kernel(QShape sh, const QJob*
 // output writes, ~1% of the bytes, still cost ~8% of the streaming rate on
 // the box, wherever in the launch they are placed).
 constexpr int kYRows = 512;   // rows per block, at most
+constexpr int kLdsPerCU = 160 * 1024;
 
 struct GemvEpiMaker {
   const float* S;
@@ -412,8 +413,19 @@ static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJo
   a.rows_per_block = (int)rpb;
   a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
   dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
+  // Batch-1 launches from tables cap the blocks a CU holds through dynamic
+  // LDS that the kernel does not use: measured on 1 GiB pools (alternating
+  // runs), fewer resident blocks read HBM faster -- 4 a CU for rows under 1
+  // KB (Q4 down [2048 x 768]: 6.43-6.51 -> 6.53-6.58 TB/s; 3 a CU: 6.25), 3
+  // for longer rows (Q4 gate [768 x 2048]: 6.67-6.72 -> 6.73-6.75, Q8 gate
+  // 6.57-6.63 -> 6.75-6.76).
+  size_t pad = 0;
+  if (tabs && sh.M == 1) {
+    const int cap = sh.rs >= 1024 ? 3 : 4;
+    pad = ((size_t)kLdsPerCU / cap - (size_t)v.mt * kYRows * 4 - 256) / 512 * 512;
+  }
   if (tabs)
-    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), pad, stream, a);
   else
     hipLaunchKernelGGL(v.fused, grid, dim3(kBlock), lds, stream, a);
   return hipGetLastError();
