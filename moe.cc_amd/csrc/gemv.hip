@@ -415,13 +415,14 @@ static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJo
   dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
   // Batch-1 launches from tables cap the blocks a CU holds through dynamic
   // LDS that the kernel does not use: measured on 1 GiB pools (alternating
-  // runs), fewer resident blocks read HBM faster -- 4 a CU for rows under 1
-  // KB (Q4 down [2048 x 768]: 6.43-6.51 -> 6.53-6.58 TB/s; 3 a CU: 6.25), 3
-  // for longer rows (Q4 gate [768 x 2048]: 6.67-6.72 -> 6.73-6.75, Q8 gate
-  // 6.57-6.63 -> 6.75-6.76).
+  // runs), fewer resident blocks read HBM faster -- 5 a CU for rows under 1
+  // KB (Q4 down [2048 x 768]: 6.43-6.51 uncapped, 6.48-6.58 with 4 a CU,
+  // 6.59-6.60 with 5, 6.24-6.27 with 3), 3 for longer rows (Q4 gate [768 x
+  // 2048]: 6.67-6.72 -> 6.71-6.78, Q8 gate 6.57-6.63 -> 6.68-6.76; 2 a CU
+  // alike).
   size_t pad = 0;
   if (tabs && sh.M == 1) {
-    const int cap = sh.rs >= 1024 ? 3 : 4;
+    const int cap = sh.rs >= 1024 ? 3 : 5;
     pad = ((size_t)kLdsPerCU / cap - (size_t)v.mt * kYRows * 4 - 256) / 512 * 512;
   }
   if (tabs)
