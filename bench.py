@@ -49,6 +49,12 @@ def gemv_bytes(dtype: int, N: int, K: int) -> int:
     return wbytes + 4 * N + 4 * K + 4 * N
 
 
+def pool_count(dtype: int, N: int, K: int, pool_gib: float = 1.0) -> int:
+    """Matrices in a GEMV pool of `pool_gib` GiB of packed weights."""
+    rb = K if dtype == 2 else K // 2
+    return int(np.ceil(pool_gib * (1 << 30) / (N * rb)))
+
+
 class Pool:
     """`count` distinct quantized matrices [N x K] in one device allocation,
     plus a shared x and one output row per matrix, and the job table."""
@@ -200,8 +206,7 @@ def run_gemv(args, dtype, shapes, workload):
     copy_calibration()
     pools = []
     for i, (N, K) in enumerate(shapes):
-        rb = K if dtype == 2 else K // 2
-        count = int(np.ceil(args.pool_gib * (1 << 30) / (N * rb)))
+        count = pool_count(dtype, N, K, args.pool_gib)
         log(f"[bench] building pool {N}x{K} dtype {dtype}: {count} matrices")
         pools.append(Pool(dtype, N, K, count, seed=1000 * (i + 1)))
     # a step: for each shape, pack then the GEMV launch.  The K timed steps

@@ -384,6 +384,29 @@ class TinyModel:
             self.layers.append(lw)
         self._build_structs()
 
+    @classmethod
+    def from_weights(cls, D, L, hd, nq, nkv, dff, E, V, dtype, tok_emb, final_norm_w, lm_head,
+                     layers, top_k=8, theta=1e7, eps=1e-6):
+        """A model over given arrays (same attribute layout as __init__
+        builds): `layers` = list of dicts with the QwenLayerWeights names and
+        an "experts" ExpertSet.  For full-width models whose weights are made
+        elsewhere (a seeded generator on the device, downloaded)."""
+        self = cls.__new__(cls)
+        self.D, self.L, self.hd, self.nq, self.nkv, self.dff = D, L, hd, nq, nkv, dff
+        self.E, self.top_k, self.V, self.expert_dtype = E, top_k, V, dtype
+        self.theta, self.eps = float(theta), float(eps)
+        self.cfg = OrcConfig(D, L, hd, nq, nkv, dff, E, top_k, V, 1, self.theta, self.eps)
+        self.tok_emb = np.ascontiguousarray(tok_emb, dtype=np.float32)
+        self.final_norm_w = np.ascontiguousarray(final_norm_w, dtype=np.float32)
+        self.lm_head = None if lm_head is None else np.ascontiguousarray(lm_head, dtype=np.float32)
+        names = ("Wq", "bq", "Wk", "bk", "Wv", "bv", "Wo", "bo", "q_norm", "k_norm", "rms1_w",
+                 "rms2_w", "router_w", "router_b")
+        self.layers = [dict({k: None for k in names}, **lw) for lw in layers]
+        if len(self.layers) != L:
+            raise ValueError("from_weights: layer count differs from L")
+        self._build_structs()
+        return self
+
     def _build_structs(self):
         self._layers = (OrcLayer * self.L)()
         for i, lw in enumerate(self.layers):
