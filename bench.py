@@ -492,6 +492,43 @@ def run_prefill(dtype, Ts, n_layers, steps, warmup):
     return res
 
 
+def run_dropin(calls):
+    """The drop-in matmul_adaptive (host buffers: upload of A, the GEMV,
+    download of C, a stream synchronisation per call) at the reference's
+    call pattern (test_model_trace.c:496-503: one call per expert
+    projection), over 24 distinct Q8 gate matrices [768 x 2048] (the 3
+    projections of 8 experts), in both weight-cache modes: content-verified
+    (the default; every call re-hashes the 1.5 MB of weight bytes) and
+    address-trusted (moe_weight_cache_mode(1)).  Microseconds per call.
+    The bytes are random (the call's cost does not depend on them)."""
+    N, K, n_mats = 768, 2048, 24
+    L = M.lib()
+    rng = np.random.default_rng(6100)
+    mats = []
+    for i in range(n_mats):
+        q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = np.full(N, 1e-3, np.float32)
+        mats.append((q, s, M.QuantizedWeight(q.ctypes.data, s.ctypes.data, N, K, 2)))
+    x = rng.standard_normal(K, dtype=np.float32)
+    y = np.empty(N, np.float32)
+    out = {"shape": f"{N}x{K}", "dtype": "q8", "matrices": n_mats, "calls": calls}
+    for mode, key in ((0, "us_per_call_verified"), (1, "us_per_call_trusted")):
+        M.check(L.moe_weight_cache_mode(mode))
+        for q, s, qw in mats:   # first use uploads
+            L.matmul_adaptive(x.ctypes.data, None, ctypes.byref(qw), y.ctypes.data, 1, N, K)
+        t0 = time.perf_counter()
+        for i in range(calls):
+            qw = mats[i % n_mats][2]
+            L.matmul_adaptive(x.ctypes.data, None, ctypes.byref(qw), y.ctypes.data, 1, N, K)
+        out[key] = round((time.perf_counter() - t0) / calls * 1e6, 1)
+    M.check(L.moe_weight_cache_mode(0))
+    M.check(L.moe_weight_cache_clear())
+    out["hash_share_of_verified_call"] = round(
+        1.0 - out["us_per_call_trusted"] / out["us_per_call_verified"], 3)
+    log(f"[bench] drop-in matmul_adaptive: {out}")
+    return out
+
+
 QWEN3_30B_A3B = dict(D=2048, L=48, hd=128, nq=32, nkv=4, dff=768, E=128, top_k=8, V=151936)
 
 
@@ -634,6 +671,8 @@ def main():
     ap.add_argument("--model-steps", type=int, default=256,
                     help="greedy decode steps of the 48-layer model (configs[4]); 0 to skip")
     ap.add_argument("--model-prompt", type=int, default=512)
+    ap.add_argument("--dropin-calls", type=int, default=480,
+                    help="timed drop-in matmul_adaptive calls per weight-cache mode; 0 to skip")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the expert path on a single MI355X "
@@ -666,6 +705,8 @@ def main():
                 if r["T"] in cpu_T:
                     log(f"[bench] prefill layer cpu baseline T={r['T']} ...")
                     r["cpu_baseline"] = layer_cpu_baseline(3, r["T"], args.cpu_layer_runs)
+    if args.dropin_calls > 0:
+        out["dropin_matmul_adaptive"] = run_dropin(args.dropin_calls)
     if args.model_steps > 0:
         out["model_decode_q4"] = run_model(args)
         if not args.no_cpu:

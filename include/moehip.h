@@ -97,8 +97,10 @@ typedef struct {
  * all host memory.  Results are bit-identical to the reference.  Weights are
  * uploaded on first use and cached by (host address, size); by default each
  * call re-hashes the host bytes and re-uploads them if they changed, so freed
- * and reused host memory is safe.  moe_weight_cache_mode(1) skips the hash
- * for callers whose weights never change (the reference's loader).  Errors
+ * and reused host memory is safe.  moe_weight_cache_mode(1), or the
+ * environment variable MOEHIP_WEIGHT_CACHE_TRUST=1 read at initialisation,
+ * skips the hash for callers whose weights never change (the reference's
+ * loader).  Errors
  * from the GPU runtime abort the process with a message: there is no CPU
  * fallback. */
 void matmul_adaptive(const float* A, const float* W_fp32, const void* W_q_ptr,
@@ -118,6 +120,17 @@ enum {
 /* Initialises the library on `device` (creates its stream).  Called lazily
  * with device 0 by every entry point if not called first. */
 moe_status moe_init(int device);
+/* Ends the library's use of the GPU (the context destroy of this API): waits
+ * for queued work, frees every device buffer the library owns (the weight
+ * cache of matmul_adaptive, its staging buffers, the shared forward scratch)
+ * and destroys the stream.  Layers and models belong to the caller and must
+ * be destroyed first: while any is alive it returns MOE_ERR_ARG and frees
+ * nothing.  A later call of any entry point initialises the library again
+ * (moe_init, or device 0 lazily).  The no-allocation entry point's
+ * file-scope array is not freed (it lives as long as the process).  No
+ * reference counterpart: the reference runs on the host and frees its
+ * buffers at exit (test_model_trace.c:763-769). */
+moe_status moe_shutdown(void);
 const char* moe_last_error(void);
 const char* moe_version(void);
 /* hipStream_t the library queues work on */
@@ -246,11 +259,10 @@ moe_status moe_layer_set_grouped_min_tokens(moe_layer* layer, int min_tokens);
  *   Bit-identical to the reference on the same inputs. */
 moe_status moe_layer_forward(moe_layer* layer, const float* x_norm, const float* x_resid, int T,
                              float* out, int32_t* idx_out, float* p_out);
-/* moe_layer_forward that allocates nothing: no reference counterpart (the
- * reference allocates its temporaries per call, test_model_trace.c:474-476);
- * it is for callers that cannot allocate device memory -- code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same
- * arguments and bit-identical results; always the per-(token, rank) kernels.
+/* moe_layer_forward that allocates nothing.  It has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * bit-identical results; always the per-(token, rank) kernels.
  * Its scratch (logits, selection, packed tables, h) lives in a 4 MiB
  * file-scope device array each GPU holds until the process ends; T is at
  * most 32 tokens and the scratch need at most 4 MiB (about 72 KiB per token

@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -63,6 +64,12 @@ moe_status set_error(moe_status st, const char* fmt, ...) {
   g_err = buf;
   return st;
 }
+
+namespace {
+std::atomic<int> g_live{0};
+}  // namespace
+
+void live_objects(int delta) { g_live.fetch_add(delta); }
 
 moe_status check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return MOE_OK;
@@ -168,6 +175,10 @@ moe_status moe_init(int device) {
   if (st) return st;
   st = check_hip(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
   if (st) return st;
+  // callers that cannot call moe_weight_cache_mode (an unmodified reference
+  // build linked against this library) opt in to address trust here
+  if (const char* v = std::getenv("MOEHIP_WEIGHT_CACHE_TRUST"))
+    if (*v) g_trust_addresses = std::atoi(v) != 0;
   g_device = device;
   g_ready = true;
   return MOE_OK;
@@ -480,6 +491,30 @@ void matmul_adaptive(const float* A, const float* W_fp32, const void* W_q_ptr, f
   st = check_hip(hipMemcpyAsync(C, dC, c_bytes, hipMemcpyDeviceToHost, g_stream), "download C");
   if (!st) st = check_hip(hipStreamSynchronize(g_stream), "matmul_adaptive sync");
   if (st) die("matmul_adaptive");
+}
+
+moe_status moe_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_ready) return MOE_OK;
+  const int live = g_live.load();
+  if (live)
+    return set_error(MOE_ERR_ARG, "moe_shutdown: %d layer(s) or model(s) still alive; destroy them first",
+                     live);
+  moe_status st = check_hip(hipStreamSynchronize(g_stream), "moe_shutdown: sync");
+  for (auto& kv : g_cache) (void)hipFree(kv.second.dev);
+  g_cache.clear();
+  for (void** b : {&g_stage_a, &g_stage_c, reinterpret_cast<void**>(&g_head_part)})
+    if (*b) (void)hipFree(*b);
+  g_stage_a = g_stage_c = nullptr;
+  g_head_part = nullptr;
+  g_stage_a_bytes = g_stage_c_bytes = g_head_part_n = 0;
+  release_gemv_workspace();
+  release_layer_scratch();
+  const moe_status sd = check_hip(hipStreamDestroy(g_stream), "moe_shutdown: hipStreamDestroy");
+  g_stream = nullptr;
+  g_ready = false;
+  g_device = -1;
+  return st ? st : sd;
 }
 
 }  // extern "C"

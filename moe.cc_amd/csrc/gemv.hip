@@ -367,6 +367,12 @@ hipError_t ensure_ws(size_t need) {
 
 }  // namespace
 
+void release_gemv_workspace() {
+  if (g_ws) (void)hipFree(g_ws);
+  g_ws = nullptr;
+  g_ws_bytes = 0;
+}
+
 const char* qgemv_variant_name(const QShape& sh, const void* w_base) {
   Variant v;
   if (select_tiled(sh, w_base, &v)) return v.name;

@@ -52,6 +52,8 @@ struct Buf {
 }  // namespace
 
 struct moe_model {
+  moe_model() { moe::live_objects(1); }
+  ~moe_model() { moe::live_objects(-1); }
   QwenConfig cfg{};
   int max_seq = 0, pos = 0, nqkv = 0, Dq = 0, Dkv = 0;
   float scale = 0.0f;

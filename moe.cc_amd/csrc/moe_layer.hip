@@ -402,6 +402,19 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   return MOE_OK;
 }
 
+void release_scratch_all() {
+  std::lock_guard<std::mutex> lk(g_layer_mu);
+  SharedScratch& S = g_scratch;
+  for (ScratchBuf* b : {&S.logits, &S.idx, &S.p, &S.xtab, &S.htab, &S.h, &S.xn, &S.hpart, &S.xpart,
+                        &S.ecount, &S.eoff, &S.perm, &S.y, &S.tasks, &S.ghist, &S.rpart}) {
+    dfree(b->p);
+    b->p = nullptr;
+    b->bytes = 0;
+  }
+  dfree(S.sel_counter);
+  S.sel_counter = nullptr;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 // Rows-per-block targets (tuning knobs, read once): MOEHIP_GATEUP_BLOCKS and
@@ -660,11 +673,17 @@ moe_status rmsnorm_dev(const float* x, const float* w, float* y, int T, int D, f
   return check_hip(hipGetLastError(), "rmsnorm launch");
 }
 
+void release_layer_scratch() { release_scratch_all(); }
+
 }  // namespace moe
 
 using namespace moe;
 
-struct moe_layer { LayerDev L; };
+struct moe_layer {
+  LayerDev L;
+  moe_layer() { moe::live_objects(1); }
+  ~moe_layer() { moe::live_objects(-1); }
+};
 
 namespace {
 

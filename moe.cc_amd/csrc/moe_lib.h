@@ -13,4 +13,10 @@ moe_status check_hip(hipError_t e, const char* what);
 moe_status ensure_init();
 // The library's stream.
 hipStream_t stream();
+// Layers and models alive (moe_shutdown refuses while any is).
+void live_objects(int delta);
+// Free the library-owned device buffers of one translation unit (the
+// stream has drained; called by moe_shutdown only).
+void release_gemv_workspace();
+void release_layer_scratch();
 }  // namespace moe

@@ -54,6 +54,7 @@ _SZ = ctypes.c_size_t
 _SIGS = {
     "matmul_adaptive": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "moe_init": (_I, [_I]),
+    "moe_shutdown": (_I, []),
     "moe_last_error": (ctypes.c_char_p, []),
     "moe_version": (ctypes.c_char_p, []),
     "moe_get_stream": (_P, []),
@@ -143,6 +144,12 @@ def check(status: int, what: str = "") -> None:
 
 def init(device: int = 0) -> None:
     check(lib().moe_init(device), "moe_init")
+
+
+def shutdown() -> None:
+    """moe_shutdown: frees the library's own device buffers and stream (every
+    layer and model must be closed first); the next call re-initialises."""
+    check(lib().moe_shutdown(), "moe_shutdown")
 
 
 def synchronize() -> None:

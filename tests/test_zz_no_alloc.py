@@ -57,6 +57,7 @@ CASES = [
     (2, 128, 2048, 768, 8, False, (16, 3)),      # configs[2] shape
     (3, 128, 2048, 768, 8, False, (4, 1)),       # Q4 at the config shape, one-token path
     (3, 60, 512, 256, 8, True, (32, 2, 1)),      # the largest T; bias; E not a power of two
+    (2, 128, 2048, 768, 8, False, (32, 17)),     # Q8 at the config shape at the largest T
 ]
 
 
