@@ -201,6 +201,41 @@ def read_stream(pools, steps):
     return rates
 
 
+READ_CAPS = (0, 1, 2, 3, 4, 5, 6, 8)
+
+
+def read_rows(pools, steps):
+    """The GEMV launch's own reads without its arithmetic (moe_rows_read_dev:
+    same blocks, rows per block, lanes per row and loads in flight; weights
+    and scales), over each pool, with the GEMV's blocks-per-CU cap (0) and
+    with 1..8 blocks a CU.  Returns per pool {cap: (GB/s over the weight and
+    scale bytes, us per launch)}; the fastest is the read ceiling of the
+    GEMV's access order."""
+    L = M.lib()
+    sink = M.DeviceBuffer(16)
+    out = []
+    for p in pools:
+        nbytes = p.weight_bytes + 4 * p.N * p.count
+        per_cap = {}
+        for cap in READ_CAPS:
+            M.check(L.moe_memset(sink.ptr, 0, 16))
+            for _ in range(2):
+                M.check(L.moe_rows_read_dev(p.dtype, p.jobs.ptr, p.count, p.N, p.K, cap, sink.ptr),
+                        "rows read")
+            a, b = M.Event(), M.Event()
+            a.record()
+            for _ in range(steps):
+                M.check(L.moe_rows_read_dev(p.dtype, p.jobs.ptr, p.count, p.N, p.K, cap, sink.ptr),
+                        "rows read")
+            b.record()
+            M.synchronize()
+            ms = a.elapsed_ms(b) / steps
+            per_cap[cap] = (round(nbytes / (ms * 1e-3) / 1e9, 1), round(ms * 1e3, 2))
+        out.append(per_cap)
+    sink.free()
+    return out
+
+
 def run_gemv(args, dtype, shapes, workload):
     M.init(0)
     copy_calibration()
@@ -254,6 +289,11 @@ def run_gemv(args, dtype, shapes, workload):
                            "achieved_GBs": round(p.bytes_per_launch / (avg * 1e-3) / 1e9, 1)})
     for k, c in zip(per_kernel, read_stream(pools, args.steps)):
         k["read_stream_GBs"] = c
+    for k, per_cap in zip(per_kernel, read_rows(pools, args.steps)):
+        best = min(per_cap, key=lambda c: per_cap[c][1])
+        k["read_rows_GBs_by_cap"] = {str(c): v[0] for c, v in per_cap.items()}
+        k["read_rows_GBs"], k["read_rows_us"], k["read_rows_best_cap"] = (per_cap[best][0],
+                                                                          per_cap[best][1], best)
     bytes_step = sum(p.bytes_per_launch for p in pools)
     ms_step = total_ms / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
@@ -274,7 +314,14 @@ def run_gemv(args, dtype, shapes, workload):
                      "traffic": measured_traffic(dom["kernel"]), "kernel": dom["kernel"],
                      "algorithmic_bytes": dom["algorithmic_bytes_per_launch"],
                      # the plain read-only stream over the same pool (moe_stream_read_dev)
-                     "read_stream_same_pool": dom["read_stream_GBs"]},
+                     "read_stream_same_pool": dom["read_stream_GBs"],
+                     # the GEMV launch's own reads alone (moe_rows_read_dev, the
+                     # fastest blocks-per-CU cap): the ceiling of its access
+                     # order, and the GEMV's share of it (read-only launch time
+                     # / GEMV launch time, the same weight and scale bytes read)
+                     "read_ceiling_same_order": dom["read_rows_GBs"],
+                     "read_ceiling_blocks_per_cu": dom["read_rows_best_cap"],
+                     "frac_of_read_ceiling": round(dom["read_rows_us"] / dom["avg_launch_us"], 4)},
         "kernels": per_kernel,
         "wall_s_timed": round(wall, 3),
     }

@@ -204,6 +204,19 @@ moe_status moe_act_pack_dev(int dtype, const float* A, int M, int K, void* tabs)
 moe_status moe_stream_read_dev(const void* src, size_t bytes, uint32_t* sink);
 moe_status moe_matmul_q_prepacked_dev(int dtype, const moe_qjob* jobs_dev, int njobs,
                                       int M, int N, int K, const void* tabs);
+/* Measurement helper, no counterpart in the reference: the reads of
+ * moe_matmul_q_prepacked_dev at M = 1 for the same jobs -- the same blocks,
+ * rows per block, lanes per row and loads in flight, every weight row and
+ * scale read once -- with no arithmetic.  blocks_per_cu 0 keeps the GEMV's
+ * own cap on resident blocks a CU; 1..8 caps them at that many instead
+ * (reads without arithmetic between them may stream best at another
+ * occupancy).  Each 32-bit word is
+ * XORed into one of sink[0..3] (16 bytes of device memory, zeroed by the
+ * caller; the XOR of the four is the XOR of every word read; A, C and the
+ * tables are not touched).  Its rate is the read ceiling of the GEMV's own
+ * access order on the same matrices. */
+moe_status moe_rows_read_dev(int dtype, const moe_qjob* jobs_dev, int njobs, int N, int K,
+                             int blocks_per_cu, uint32_t* sink);
 
 /* test_model_trace.c:229-236 and :500 on device arrays of n floats:
  * h = (g / (1 + expf(-g))) * u  (u may be NULL: h = silu(g)).  expf is

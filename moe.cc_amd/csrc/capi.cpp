@@ -440,6 +440,22 @@ moe_status moe_matmul_q_prepacked_dev(int dtype, const moe_qjob* jobs_dev, int n
                    "prepacked qgemv launch");
 }
 
+moe_status moe_rows_read_dev(int dtype, const moe_qjob* jobs_dev, int njobs, int N, int K,
+                             int blocks_per_cu, uint32_t* sink) {
+  moe_status st = ensure_init();
+  if (st) return st;
+  QShape sh;
+  st = prepacked_shape(dtype, 1, N, K, "rows_read", &sh);
+  if (st) return st;
+  if (njobs < 0) return set_error(MOE_ERR_ARG, "rows_read: njobs %d", njobs);
+  if (!sink) return set_error(MOE_ERR_ARG, "rows_read: null sink");
+  if (blocks_per_cu < 0 || blocks_per_cu > 8)
+    return set_error(MOE_ERR_ARG, "rows_read: blocks_per_cu %d (0..8)", blocks_per_cu);
+  if (njobs == 0 || N == 0) return MOE_OK;
+  return check_hip(launch_rows_read(sh, (const QJob*)jobs_dev, njobs, blocks_per_cu, sink, g_stream),
+                   "rows_read launch");
+}
+
 const char* moe_gemv_variant(int dtype, int M, int N, int K) {
   QShape sh;
   sh.dtype = dtype;

@@ -131,6 +131,68 @@ __global__ __launch_bounds__(kBlock) void qgemv_tiled(TiledArgs a) {
   gemv_write_outputs(ybuf, kYRows, job.C, a.sh.ldc, mbase, ntok, r0, r1);
 }
 
+// The reads of a batch-1 tiled launch and nothing else: the same blocks,
+// rows per block, wave walk (row groups wave, wave + 4, ..., two groups of
+// loads in flight), nontemporal 16-byte weight loads, per-row scale loads and
+// LDS-capped blocks per CU as qgemv_tiled<Q4, G, 1>, with the words folded
+// into one XOR per wave instead of the dots.  Its rate is what the GEMV's own
+// access order allows on the same pool.
+template <class G>
+__global__ __launch_bounds__(kBlock) void rows_read_kernel(TiledArgs a, uint32_t* sink) {
+  const int job_id = blockIdx.x / a.blocks_per_job;
+  const int r0 = (blockIdx.x % a.blocks_per_job) * a.rows_per_block;
+  const int r1 = r0 + a.rows_per_block < a.sh.N ? r0 + a.rows_per_block : a.sh.N;
+  const QJob job = get_job(a, job_id);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / G::LPR;
+  const int ngroups = (r1 - r0 + G::WR - 1) / G::WR;
+  constexpr int PF = 2;
+  uint32_t w[PF][G::DW];
+  uint32_t sc[PF];
+  uint32_t acc = 0;
+  auto load = [&](int gi, uint32_t (&d)[G::DW], uint32_t& s) {
+    const int row = r0 + gi * G::WR + g;
+    s = __float_as_uint(job.S[row < r1 ? row : r0]);
+    if (row < r1) {
+      load_row_regs<G>(job.W + (size_t)row * (size_t)a.sh.rs, d);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::DW; ++i) d[i] = 0;
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < PF; ++i)
+    if (wave + i * kWaves < ngroups) load(wave + i * kWaves, w[i], sc[i]);
+  for (int base = 0;; base += PF) {
+    bool done = false;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int gi = wave + (base + i) * kWaves;
+      if (gi >= ngroups) { done = true; break; }
+      // the row's scale once (lane 0 of its lane group), past-the-end rows none
+      if (lane % G::LPR == 0 && r0 + gi * G::WR + g < r1) acc ^= sc[i];
+#pragma unroll
+      for (int j = 0; j < G::DW; ++j) acc ^= w[i][j];
+      const int gn = gi + PF * kWaves;
+      if (gn < ngroups) load(gn, w[i], sc[i]);
+    }
+    if (done) break;
+  }
+  // one atomic a block, on one of the sink's four words (tens of thousands
+  // of atomics on one address would serialise behind the loads)
+  __shared__ uint32_t wx[kWaves];
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off, kWave);
+  if (lane == 0) wx[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) b ^= wx[i];
+    if (b != 0u) atomicXor(sink + (blockIdx.x & 3), b);
+  }
+}
+
 // One activation row into an LDS table (the layout act_pack writes): a
 // first pass over x for the limb count and sum (block reduction), a second
 // that writes the planes those values need -- all four when `all_planes`
@@ -297,9 +359,12 @@ __global__ __launch_bounds__(kBlock) void stream_read_kernel(const u32x4* __rest
 // ---- host-side variant selection ----
 using TiledFn = void (*)(TiledArgs);
 
+using ReadFn = void (*)(TiledArgs, uint32_t*);
+
 struct Variant {
   TiledFn fn;
   TiledFn fused;   // the same with the activation tables built in LDS
+  ReadFn read;     // its reads alone (rows_read_kernel)
   int wr;          // rows per wave group
   int mt;
   const char* name;
@@ -307,7 +372,7 @@ struct Variant {
 
 template <bool Q4, class G, int MT>
 Variant make_variant(const char* name) {
-  return Variant{qgemv_tiled<Q4, G, MT>, qgemv_fused<Q4, G, MT>, G::WR, MT, name};
+  return Variant{qgemv_tiled<Q4, G, MT>, qgemv_fused<Q4, G, MT>, rows_read_kernel<G>, G::WR, MT, name};
 }
 
 // Row byte counts with a tiled geometry: LPR lanes x P dwordx4 x 16 bytes.
@@ -391,11 +456,19 @@ hipError_t launch_act_pack(const QShape& sh, const QJob* jobs_dev, const QJob& o
   return hipGetLastError();
 }
 
-// tabs == nullptr: the fused kernel (tables in LDS, lds bytes per block).
-static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
-                        const uint8_t* tabs, int shared_tabs, size_t lds, hipStream_t stream) {
+// The geometry of a tiled launch: arguments, grid and (batch-1 launches from
+// tables) the dynamic LDS that caps the blocks a CU holds.
+struct TiledPlan {
   Variant v;
-  if (!select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) return hipErrorInvalidValue;
+  TiledArgs a;
+  dim3 grid;
+  size_t pad;
+};
+
+static bool plan_tiled(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                       const uint8_t* tabs, int shared_tabs, TiledPlan* pl) {
+  Variant& v = pl->v;
+  if (!select_tiled(sh, jobs_dev ? nullptr : one.W, &v)) return false;
   // rows per block: a multiple of (waves x rows per wave group), large
   // enough to amortise the activation loads, small enough for >= target
   // blocks (tuning knobs MOEHIP_GEMV_BLOCKS, MOEHIP_GEMV_MAX_GROUPS)
@@ -409,7 +482,7 @@ static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJo
   if (rpb > (long long)max_groups * unit) rpb = (long long)max_groups * unit;
   if (rpb > kYRows) rpb = kYRows / unit * unit;   // the staging buffer's rows
   if (rpb > sh.N) rpb = (sh.N + unit - 1) / unit * unit;
-  TiledArgs a;
+  TiledArgs& a = pl->a;
   a.sh = sh;
   a.jobs = jobs_dev;
   a.one = one;
@@ -418,7 +491,7 @@ static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJo
   a.shared_tabs = shared_tabs;
   a.rows_per_block = (int)rpb;
   a.blocks_per_job = (int)((sh.N + rpb - 1) / rpb);
-  dim3 grid((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
+  pl->grid = dim3((unsigned)((long long)a.blocks_per_job * njobs), (unsigned)((sh.M + v.mt - 1) / v.mt));
   // Batch-1 launches from tables cap the blocks a CU holds through dynamic
   // LDS that the kernel does not use: measured on 1 GiB pools (alternating
   // runs), fewer resident blocks read HBM faster -- 5 a CU for rows under 1
@@ -426,15 +499,39 @@ static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJo
   // 6.59-6.60 with 5, 6.24-6.27 with 3), 3 for longer rows (Q4 gate [768 x
   // 2048]: 6.67-6.72 -> 6.71-6.78, Q8 gate 6.57-6.63 -> 6.68-6.76; 2 a CU
   // alike).
-  size_t pad = 0;
+  pl->pad = 0;
   if (tabs && sh.M == 1) {
     const int cap = sh.rs >= 1024 ? 3 : 5;
-    pad = ((size_t)kLdsPerCU / cap - (size_t)v.mt * kYRows * 4 - 256) / 512 * 512;
+    pl->pad = ((size_t)kLdsPerCU / cap - (size_t)v.mt * kYRows * 4 - 256) / 512 * 512;
   }
+  return true;
+}
+
+// tabs == nullptr: the fused kernel (tables in LDS, lds bytes per block).
+static hipError_t launch_tiled(const QShape& sh, const QJob* jobs_dev, const QJob& one, int njobs,
+                        const uint8_t* tabs, int shared_tabs, size_t lds, hipStream_t stream) {
+  TiledPlan pl;
+  if (!plan_tiled(sh, jobs_dev, one, njobs, tabs, shared_tabs, &pl)) return hipErrorInvalidValue;
   if (tabs)
-    hipLaunchKernelGGL(v.fn, grid, dim3(kBlock), pad, stream, a);
+    hipLaunchKernelGGL(pl.v.fn, pl.grid, dim3(kBlock), pl.pad, stream, pl.a);
   else
-    hipLaunchKernelGGL(v.fused, grid, dim3(kBlock), lds, stream, a);
+    hipLaunchKernelGGL(pl.v.fused, pl.grid, dim3(kBlock), lds, stream, pl.a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_read(const QShape& sh, const QJob* jobs_dev, int njobs, int blocks_per_cu,
+                            uint32_t* sink, hipStream_t stream) {
+  if (sh.M != 1 || blocks_per_cu < 0 || blocks_per_cu > 8) return hipErrorInvalidValue;
+  TiledPlan pl;
+  const QJob none{nullptr, nullptr, nullptr, nullptr};
+  // any non-null tables pointer: the plan of a launch from packed tables
+  if (!plan_tiled(sh, jobs_dev, none, njobs, reinterpret_cast<const uint8_t*>(sink), 1, &pl))
+    return hipErrorInvalidValue;
+  // the GEMV's LDS per block (its output staging plus the cap's padding),
+  // or the padding of another cap
+  size_t lds = pl.pad + (size_t)pl.v.mt * kYRows * 4;
+  if (blocks_per_cu > 0) lds = ((size_t)kLdsPerCU / blocks_per_cu - 256) / 512 * 512;
+  hipLaunchKernelGGL(pl.v.read, pl.grid, dim3(kBlock), lds, stream, pl.a, sink);
   return hipGetLastError();
 }
 

@@ -49,6 +49,13 @@ hipError_t launch_f32gemv(const float* A, const float* W, float* C, int M, int N
 // XOR of all its 32-bit words folded into *sink (the caller zeroes it).
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
 
+// The reads of a batch-1 tiled launch (launch_qgemv_tables' geometry for
+// these jobs: weights and scales, no arithmetic), every word XORed into one
+// of sink[0..3] (the caller zeroes them).  M must be 1; shapes as launch_qgemv_tables.
+// blocks_per_cu: 0 = the GEMV's own cap, else 1..8 blocks a CU (LDS-capped).
+hipError_t launch_rows_read(const QShape& sh, const QJob* jobs_dev, int njobs, int blocks_per_cu,
+                            uint32_t* sink, hipStream_t stream);
+
 // Zero-fill used for unsupported dtypes (kernels.c:172-179).
 hipError_t launch_zero(float* C, size_t n, hipStream_t stream);
 

@@ -83,6 +83,7 @@ _SIGS = {
     "moe_act_table_bytes": (_SZ, [_I]),
     "moe_act_pack_dev": (_I, [_I, _P, _I, _I, _P]),
     "moe_matmul_q_prepacked_dev": (_I, [_I, _P, _I, _I, _I, _I, _P]),
+    "moe_rows_read_dev": (_I, [_I, _P, _I, _I, _I, _I, _P]),
     "moe_silu_mul_dev": (_I, [_P, _P, _P, _SZ]),
     "moe_expf_dev": (_I, [_P, _P, _SZ]),
     "moe_expf_bits_dev": (_I, [ctypes.c_uint32, _P, _SZ]),

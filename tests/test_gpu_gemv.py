@@ -199,3 +199,33 @@ def test_stream_read_ceiling_kernel(moehip, nbytes):
     assert got == int(np.bitwise_xor.reduce(words))
     # sizes that are not whole 16-byte words are rejected
     assert M_.lib().moe_stream_read_dev(d.ptr, nbytes - 4, sink.ptr) != 0
+
+
+@pytest.mark.parametrize("dtype,N,K,nj", [(3, 2048, 768, 1366), (3, 768, 2048, 5), (2, 768, 2048, 683),
+                                          (3, 100, 768, 3), (2, 77, 2048, 9)])
+def test_rows_read_reads_every_word_once(moehip, dtype, N, K, nj):
+    """moe_rows_read_dev (the GEMV launch's reads without its arithmetic,
+    bench.py's read ceiling) reads every weight word and every scale exactly
+    once: the XOR it folds into the sink equals the host's XOR of the pool
+    (a word read twice or skipped would change it).  Job counts include the
+    bench pools' (1366 and 683: 256 / 128-row blocks, 8 row groups a wave)
+    and row counts that leave partial row groups."""
+    L = moehip.lib()
+    rb = K if dtype == 2 else K // 2
+    rng = np.random.default_rng(N * 7 + nj)
+    q = rng.integers(0, 2**32, size=nj * N * rb // 4, dtype=np.uint32)
+    s = rng.integers(0, 2**32, size=nj * N, dtype=np.uint32)
+    dq, ds = moehip.DeviceBuffer.from_array(q), moehip.DeviceBuffer.from_array(s)
+    jobs = (moehip.QJob * nj)()
+    for j in range(nj):
+        jobs[j] = moehip.QJob(dq.ptr + j * N * rb, ds.ptr + j * N * 4, None, None)
+    djobs = moehip.DeviceBuffer(ctypes.sizeof(jobs))
+    moehip.check(L.moe_memcpy_h2d(djobs.ptr, ctypes.addressof(jobs), ctypes.sizeof(jobs)))
+    sink = moehip.DeviceBuffer(16)
+    want = int(np.bitwise_xor.reduce(q) ^ np.bitwise_xor.reduce(s))
+    for cap in (0, 1, 3, 8):   # the GEMV's own blocks-per-CU cap, and others
+        moehip.check(L.moe_memset(sink.ptr, 0, 16), "memset")
+        moehip.check(L.moe_rows_read_dev(dtype, djobs.ptr, nj, N, K, cap, sink.ptr), "rows read")
+        assert int(np.bitwise_xor.reduce(sink.download((4,), np.uint32))) == want, f"cap {cap}"
+    assert L.moe_rows_read_dev(dtype, djobs.ptr, nj, N, 100, 0, sink.ptr) != 0   # no tiled geometry
+    assert L.moe_rows_read_dev(dtype, djobs.ptr, nj, N, K, 9, sink.ptr) != 0     # cap out of range
