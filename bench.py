@@ -154,16 +154,19 @@ def copy_calibration():
 
 
 def measured_traffic(kernel_name):
-    """HBM bytes per launch of `kernel_name` from the committed PMC summary
-    (profiles/traffic.json, written from two rocprofv3 --pmc runs of this
-    script), or None."""
+    """(HBM bytes per launch of `kernel_name`, the commit they were measured
+    at) from the committed PMC summary (profiles/traffic.json, two rocprofv3
+    --pmc runs of this script, FETCH_SIZE and WRITE_SIZE, scaled by what
+    they read for the 256 MiB copy), or (None, None).  rocprofv3 cannot run
+    inside this process, so the figure is not this run's own counter."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
-        return t["kernels"].get(kernel_name, {}).get("traffic_bytes_per_launch")
+        return (t["kernels"].get(kernel_name, {}).get("traffic_bytes_per_launch"),
+                t.get("measured_at"))
     except (OSError, ValueError, KeyError):
-        return None
+        return None, None
 
 
 def host_cores() -> int:
@@ -298,6 +301,7 @@ def run_gemv(args, dtype, shapes, workload):
     ms_step = total_ms / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
     dom = max(per_kernel, key=lambda k: k["avg_launch_us"])
+    traffic, traffic_at = measured_traffic(dom["kernel"])
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
@@ -311,7 +315,8 @@ def run_gemv(args, dtype, shapes, workload):
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(dom["kernel"]), "kernel": dom["kernel"],
+                     "traffic": traffic, "traffic_measured_at_commit": traffic_at,
+                     "kernel": dom["kernel"],
                      "algorithmic_bytes": dom["algorithmic_bytes_per_launch"],
                      # the plain read-only stream over the same pool (moe_stream_read_dev)
                      "read_stream_same_pool": dom["read_stream_GBs"],
