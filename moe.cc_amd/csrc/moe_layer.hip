@@ -122,7 +122,7 @@ struct GateUpArgs {
 // wrapping sum), so no kernel runs between the router and this one.  Block
 // (0, 0) writes the selection and gates (select_gates) and the x table's
 // header.
-template <bool Q4, class G, bool SEL>
+template <bool Q4, class G, bool SEL, bool NT>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   extern __shared__ float hb[];   // [rows_per_block]
   __shared__ int red[2];   // limb count, activation sum
@@ -178,8 +178,8 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     auto epi = mk.e;
     generic_rows_fp32<Q4, 2>(W, a.rb, a.D, xs[0], r0, r1, epi);
   } else {
-    stream_tokens<Q4, G, 2, 1>(W, a.rb, a.D, tabs, xs, 1, r0, r1, mk, x_nl,
-                               x_nl > 0 ? x_sum : nullptr);
+    stream_tokens<Q4, G, 2, 1, NT>(W, a.rb, a.D, tabs, xs, 1, r0, r1, mk, x_nl,
+                                   x_nl > 0 ? x_sum : nullptr);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < r1 - r0; i += blockDim.x) a.h[(size_t)q * a.dff + r0 + i] = hb[i];
@@ -228,7 +228,9 @@ struct DownEpiMaker {
 // down + weighted sum for one token and one row chunk: wave w computes
 // y_j for ranks j = w, w+8, ... into LDS; then out[t, o] = x_resid +
 // (((0 + p0 y0) + p1 y1) + ...) in rank order (test_model_trace.c:502-517).
-template <bool Q4, class G>
+// NT: nontemporal weight loads; false from down_cached_min_tokens() tokens
+// up, where tokens routed to one expert read its rows again.
+template <bool Q4, class G, bool NT>
 __global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs a) {
   extern __shared__ float yb[];   // [topk][rows_per_block]
   int rc, t;
@@ -263,7 +265,7 @@ __global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs 
         nl = on > nl ? on : nl;
         sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
       }
-      stream_row_wave<Q4, G, 1>(W, a.rb, a.dff, tab, x, r0, r1, mk, nl, sum);
+      stream_row_wave<Q4, G, 1, NT>(W, a.rb, a.dff, tab, x, r0, r1, mk, nl, sum);
     }
   }
   __syncthreads();
@@ -424,6 +426,13 @@ int env_int(const char* name, int dflt) {
   return v && *v ? atoi(v) : dflt;
 }
 int gateup_target_blocks() { static const int v = env_int("MOEHIP_GATEUP_BLOCKS", 1024); return v; }
+// Tokens from which the few-token gate/up and down kernels load expert rows
+// with ordinary (cache-allocating) loads instead of nontemporal ones: with
+// many tokens, pairs that share an expert read its rows again (tuning knobs
+// MOEHIP_GATEUP_CACHED_MIN_T, MOEHIP_DOWN_CACHED_MIN_T; 0 = never).
+int gateup_cached_min_tokens() { static const int v = env_int("MOEHIP_GATEUP_CACHED_MIN_T", 12); return v; }
+int down_cached_min_tokens() { static const int v = env_int("MOEHIP_DOWN_CACHED_MIN_T", 12); return v; }
+bool cached_loads(int T, int min_t) { return min_t > 0 && T >= min_t; }
 int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 512); return v; }
 
 template <bool Q4, class G>
@@ -450,9 +459,11 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
   if (sel) {
     a.logits = L->logits; a.xpart = L->xpart; a.nxpart = nxpart; a.E = L->E;
     a.idx_w = L->idx; a.p = L->p; a.idx_user = idx_out; a.p_user = p_out;
-    hipLaunchKernelGGL((gate_up_kernel<Q4, G, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+    hipLaunchKernelGGL((gate_up_kernel<Q4, G, true, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+  } else if (cached_loads(T, gateup_cached_min_tokens())) {
+    hipLaunchKernelGGL((gate_up_kernel<Q4, G, false, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
   } else {
-    hipLaunchKernelGGL((gate_up_kernel<Q4, G, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+    hipLaunchKernelGGL((gate_up_kernel<Q4, G, false, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
   }
 }
 
@@ -469,8 +480,12 @@ void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, floa
              act_table_bytes(L->dff), L->h, L->hpart, nchunks, resid, out, (int)rpb};
   a.nrc = (int)((L->D + rpb - 1) / rpb);
   dim3 grid((unsigned)(a.nrc * T));
-  hipLaunchKernelGGL((down_combine_kernel<Q4, G>), grid, dim3(kCombineThreads),
-                     (size_t)L->topk * rpb * 4, s, a);
+  if (!cached_loads(T, down_cached_min_tokens()))
+    hipLaunchKernelGGL((down_combine_kernel<Q4, G, true>), grid, dim3(kCombineThreads),
+                       (size_t)L->topk * rpb * 4, s, a);
+  else
+    hipLaunchKernelGGL((down_combine_kernel<Q4, G, false>), grid, dim3(kCombineThreads),
+                       (size_t)L->topk * rpb * 4, s, a);
 }
 
 // Row-byte dispatch for the expert GEMVs (same geometries as gemv.hip).

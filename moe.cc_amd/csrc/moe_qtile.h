@@ -212,13 +212,15 @@ struct TileGeom {
 
 // Weight rows are streamed once per launch: nontemporal loads keep them from
 // displacing reused data in the caches (measured ~+15% streaming bandwidth).
-template <class G>
+// NT = false: ordinary loads, for launches in which several blocks read the
+// same rows (the few-token expert kernels: tokens routed to one expert).
+template <class G, bool NT = true>
 __device__ __forceinline__ void load_row_regs(const uint8_t* row, uint32_t (&w)[G::DW]) {
   const int r = (threadIdx.x % kWave) % G::LPR;
 #pragma unroll
   for (int p = 0; p < G::P; ++p) {
-    const u32x4 v = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4*>(row + (size_t)(p * G::LPR + r) * 16));
+    const u32x4* src = reinterpret_cast<const u32x4*>(row + (size_t)(p * G::LPR + r) * 16);
+    const u32x4 v = NT ? __builtin_nontemporal_load(src) : *src;
     w[4 * p + 0] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
   }
 }
@@ -293,7 +295,7 @@ constexpr int pf_for() { return (Q4 && NL > 1) ? 1 : 2; }
 // The epilogue's per-row data (its scales) is fetched with the row's
 // weights: epi.pre(row) at load time, epi(row, tot, pre) at the end, so the
 // scale load's latency hides behind the weight stream.
-template <bool Q4, class G, int NL, int MTI, int NM, class Epi>
+template <bool Q4, class G, int NL, int MTI, int NM, bool NT = true, class Epi>
 __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long rs, int K,
                                             const uint8_t* const* tab, int r0, int r1,
                                             Epi& epi, int wv, int nwv,
@@ -310,7 +312,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t* const* W, long long r
 #pragma unroll
     for (int mat = 0; mat < NM; ++mat) {
       if (row < r1) {
-        load_row_regs<G>(W[mat] + (size_t)row * (size_t)rs, w[mat]);
+        load_row_regs<G, NT>(W[mat] + (size_t)row * (size_t)rs, w[mat]);
       } else {
 #pragma unroll
         for (int i = 0; i < G::DW; ++i) w[mat][i] = 0;
@@ -411,7 +413,7 @@ __device__ void generic_rows_fp32(const uint8_t* const* W, long long rs, int K, 
 // xs[t] are the fp32 activation rows, used only by the exact fallback.
 // nl_in > 0: the limb count of all tokens, and asum_in (per token, may be
 // null) their activation sums, given instead of read from the headers.
-template <bool Q4, class G, int NM, int MT, class MakeEpi>
+template <bool Q4, class G, int NM, int MT, bool NT = true, class MakeEpi>
 __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
                               const uint8_t* const* tabs, const float* const* xs, int ntok, int r0,
                               int r1, MakeEpi& make_epi, int wv, int nwv, int nl_in = 0,
@@ -442,8 +444,8 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
 #pragma unroll
         for (int t = 0; t < MTI; ++t) as[t] = asum_in ? asum_in[t0 + t < ntok ? t0 + t : ntok - 1] : 0u;
         auto epi = make_epi.template at<MTI>(t0);
-        stream_rows<Q4, G, NL, MTI, NM>(W, rs, K, tb, r0, r1, epi, wv, nwv,
-                                        asum_in ? as : nullptr);
+        stream_rows<Q4, G, NL, MTI, NM, NT>(W, rs, K, tb, r0, r1, epi, wv, nwv,
+                                            asum_in ? as : nullptr);
       }
     }
   };
@@ -456,19 +458,19 @@ __device__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
 }
 
 // Whole-block team: every wave of the block shares the rows.
-template <bool Q4, class G, int NM, int MT, class MakeEpi>
+template <bool Q4, class G, int NM, int MT, bool NT = true, class MakeEpi>
 __device__ __forceinline__ void stream_tokens(const uint8_t* const* W, long long rs, int K,
                                               const uint8_t* const* tabs, const float* const* xs,
                                               int ntok, int r0, int r1, MakeEpi& make_epi,
                                               int nl_in = 0, const uint32_t* asum_in = nullptr) {
-  stream_tokens<Q4, G, NM, MT>(W, rs, K, tabs, xs, ntok, r0, r1, make_epi,
+  stream_tokens<Q4, G, NM, MT, NT>(W, rs, K, tabs, xs, ntok, r0, r1, make_epi,
                                (int)(threadIdx.x / kWave), (int)(blockDim.x / kWave), nl_in,
                                asum_in);
 }
 
 // One wave alone streams rows [r0, r1) for one activation row whose limb
 // count nl and activation sum asum are given (the table's header is not read).
-template <bool Q4, class G, int NM, class MakeEpi>
+template <bool Q4, class G, int NM, bool NT = true, class MakeEpi>
 __device__ __forceinline__ void stream_row_wave(const uint8_t* const* W, long long rs, int K,
                                                 const uint8_t* tab, const float* x, int r0,
                                                 int r1, MakeEpi& make_epi, int nl,
@@ -482,7 +484,7 @@ __device__ __forceinline__ void stream_row_wave(const uint8_t* const* W, long lo
       generic_rows_fp32<Q4, NM>(W, rs, K, x, r0, r1, epi, 0, 1);
     } else {
       auto epi = make_epi.template at<1>(0);
-      stream_rows<Q4, G, NL, 1, NM>(W, rs, K, tabs, r0, r1, epi, 0, 1, as);
+      stream_rows<Q4, G, NL, 1, NM, NT>(W, rs, K, tabs, r0, r1, epi, 0, 1, as);
     }
   };
   if (nl <= 1)
