@@ -433,6 +433,7 @@ int gateup_target_blocks() { static const int v = env_int("MOEHIP_GATEUP_BLOCKS"
 int gateup_cached_min_tokens() { static const int v = env_int("MOEHIP_GATEUP_CACHED_MIN_T", 12); return v; }
 int down_cached_min_tokens() { static const int v = env_int("MOEHIP_DOWN_CACHED_MIN_T", 12); return v; }
 bool cached_loads(int T, int min_t) { return min_t > 0 && T >= min_t; }
+
 int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 512); return v; }
 
 template <bool Q4, class G>
@@ -449,6 +450,16 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
   long long rpb = (total + tgt - 1) / tgt;
   rpb = std::max<long long>(unit, (rpb + unit - 1) / unit * unit);
   rpb = std::min<long long>(rpb, 8 * unit);
+  // several tokens: a chunk count that is a multiple of 8, so that every
+  // chunk's pairs run on one XCD (xcd_chunk_item) and pairs sharing an
+  // expert find its rows in that XCD's L2 -- the nearest such count at or
+  // above the target, if its rows per block stay a whole number of units
+  if (npairs > L->topk) {
+    const long long nc0 = (L->dff + rpb - 1) / rpb;
+    const long long nc8 = (nc0 + 7) / 8 * 8;
+    const long long r8 = ((L->dff + nc8 - 1) / nc8 + unit - 1) / unit * unit;
+    if ((L->dff + r8 - 1) / r8 == nc8) rpb = r8;
+  }
   const int nc = (int)((L->dff + rpb - 1) / rpb);
   *nchunks = nc;
   GateUpArgs a{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk, L->idx,
