@@ -53,6 +53,8 @@ struct RouterTileArgs {
   size_t tab_bytes;
   int q4;              // tables for Q4 experts (else Q8)
   uint2* part;         // [token groups][expert groups][16] partial table headers {nl, sum}
+  int* hist_zero = nullptr;   // block 0 zeroes hist_n ints here (the selection's pair counts)
+  int hist_n = 0;
 };
 
 // Router weights reach every lane by DPP row broadcast: within each 16-lane
@@ -296,6 +298,8 @@ __global__ __launch_bounds__(64 * WPB) void router_bcast_kernel(RouterTileArgs a
     if (t < a.T && e < a.E) a.logits[(size_t)t * a.E + e] = a.b ? r.acc[c] + a.b[e] : r.acc[c];
   }
   router_pack<RS::NT>(a, t0, tg, eg, neg);
+  if (a.hist_zero && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < a.hist_n; i += RS::NT) a.hist_zero[i] = 0;
 }
 
 // ---------------------------------------------------------------- select
@@ -311,6 +315,11 @@ struct SelectArgs {
   int neg;             // router blocks per token group
   uint8_t* tabs;       // x unit tables
   size_t tab_bytes;
+  // optional: pairs per expert of each grouping block (block b takes pairs
+  // b * per .. (b + 1) * per - 1), hist[b][E], added here (the router zeroes
+  // it) for group_scatter_kernel
+  int* hist = nullptr;
+  int per = 0;
 };
 
 __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs a) {
@@ -347,6 +356,10 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void select_kernel(SelectArgs
   select_token_any(a.logits + (size_t)t * a.E, a.E, a.topk, reinterpret_cast<uint64_t*>(keys2[wave]),
                    sidx[wave], sval[wave], sexp[wave], a.idx + q, a.p + q,
                    a.idx_user ? a.idx_user + q : nullptr, a.p_user ? a.p_user + q : nullptr);
+  if (a.hist && lane < a.topk) {
+    const int e = sidx[wave][lane];
+    if (e >= 0) atomicAdd(&a.hist[((int)q + lane) / a.per * a.E + e], 1);
+  }
 }
 
 // ---------------------------------------------------------------- group
@@ -453,27 +466,12 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int* __restr
   }
 }
 
-// The same grouping over many pairs in two launches of nb blocks, block b
-// taking pairs b*per .. (b+1)*per - 1 (one atomic per pair on a single
-// block's LDS was the cost of group_kernel): group_count_kernel writes each
-// block's pair counts per expert to hist[b][E]; group_scatter_kernel gives
-// block b the cursor start(e) + sum over b' < b of hist[b'][e] and
-// scatters its pairs; block 0 also writes ecount, eoff and the tasks.
-__global__ __launch_bounds__(kGroupThreads) void group_count_kernel(const int* __restrict__ idx, int npairs,
-                                                                    int E, int per, int* __restrict__ hist) {
-  __shared__ int cnt[kGroupThreads];
-  const int tid = threadIdx.x;
-  cnt[tid] = 0;
-  __syncthreads();
-  const int q0 = blockIdx.x * per, q1 = min(q0 + per, npairs);
-  for (int q = q0 + tid; q < q1; q += kGroupThreads) {
-    const int e = idx[q];
-    if (e >= 0) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  if (tid < E) hist[(size_t)blockIdx.x * E + tid] = cnt[tid];
-}
-
+// The same grouping over many pairs on nb blocks, block b taking pairs
+// b*per .. (b+1)*per - 1 (one atomic per pair on a single block's LDS was
+// the cost of group_kernel): select_kernel has added each block's pair
+// counts per expert into hist[b][E]; block b starts expert e's cursor at
+// start(e) + sum over b' < b of hist[b'][e] and scatters its pairs; block 0
+// also writes ecount, eoff and the tasks.
 __global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
     const int* __restrict__ idx, int npairs, int E, int per, const int* __restrict__ hist, int nb,
     int* __restrict__ ecount, int* __restrict__ eoff, int* __restrict__ perm, int2* __restrict__ tasks,
@@ -621,9 +619,11 @@ moe_status launch_router(const RouterTileArgs& a, hipStream_t s, int* neg) {
 }  // namespace
 
 moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s,
-                         const uint2* xpart, int neg) {
+                         const uint2* xpart, int neg, int* hist, int per) {
   SelectArgs sa{L->logits, T, L->E, L->topk, L->idx, L->p, idx_out, p_out,
                 xpart, neg, L->xtab, act_table_bytes(L->D)};
+  sa.hist = hist;
+  sa.per = per;
   dim3 sg((unsigned)((T + kSelectWaves - 1) / kSelectWaves));
   hipLaunchKernelGGL(select_kernel, sg, dim3(kSelectWaves * kWave), 0, s, sa);
   return check_hip(hipGetLastError(), "select launch");
@@ -642,26 +642,31 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
     return set_error(MOE_ERR_ARG, "grouped forward: arrays must be 16-byte aligned");
   // 1-2. router logits (one sequential chain per lane) and, in the same
   // blocks, the x unit tables of the expert kernels
+  const int npairs = T * L->topk;
+  // many pairs: the grouping runs on nb blocks of `per` pairs; the selection
+  // counts each block's pairs per expert into ghist (zeroed by the router)
+  const bool two = npairs > kGroupOneBlockPairs;
+  const int nb = std::min(kGroupBlocks, (npairs + 255) / 256);
+  const int per = (npairs + nb - 1) / nb;
   RouterTileArgs ra{xn, L->router_w, L->router_b, L->logits, T, L->D, L->E,
                     L->xtab, act_table_bytes(L->D), L->dtype == 3, L->rpart};
+  if (two) {
+    ra.hist_zero = L->ghist;
+    ra.hist_n = nb * L->E;
+  }
   int neg = 0;
   if ((st = launch_router(ra, s, &neg))) return st;
-  // 3. top-k and gates; the x tables' headers
-  if ((st = launch_select(L, T, idx_out, p_out, s, L->rpart, neg))) return st;
+  // 3. top-k and gates; the x tables' headers; the grouping blocks' counts
+  if ((st = launch_select(L, T, idx_out, p_out, s, L->rpart, neg, two ? L->ghist : nullptr, per)))
+    return st;
   // 4. group pairs by expert, tasks of at most one block's pairs
-  const int npairs = T * L->topk;
   const int nt = expert_gemm_tiles(L, T);
   const int split = expert_gemm_split(nt);
   const int ntask_max = npairs / split + L->E + 1;
-  if (npairs <= kGroupOneBlockPairs) {
+  if (!two) {
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, s, L->idx, npairs, L->E,
                        L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
   } else {
-    const int nb = std::min(kGroupBlocks, (npairs + 255) / 256);
-    const int per = (npairs + nb - 1) / nb;
-    hipLaunchKernelGGL(group_count_kernel, dim3((unsigned)nb), dim3(kGroupThreads), 0, s, L->idx, npairs,
-                       L->E, per, L->ghist);
-    if ((st = check_hip(hipGetLastError(), "group count launch"))) return st;
     hipLaunchKernelGGL(group_scatter_kernel, dim3((unsigned)nb), dim3(kGroupThreads), 0, s, L->idx, npairs,
                        L->E, per, L->ghist, nb, L->ecount, L->eoff, L->perm, L->tasks, ntask_max, split);
   }

@@ -59,8 +59,11 @@ struct LayerDev {
 // (and the caller's copies, when given): one wave per token.
 // With xpart set, each token's wave also combines the router blocks'
 // partial x-table headers (neg per token group of 16) into its table.
+// hist (optional): per-grouping-block pair counts, block b taking pairs
+// b * per .. (b + 1) * per - 1, added with atomics (zeroed beforehand).
 moe_status launch_select(const LayerDev* L, int T, int32_t* idx_out, float* p_out, hipStream_t s,
-                         const uint2* xpart = nullptr, int neg = 0);
+                         const uint2* xpart = nullptr, int neg = 0, int* hist = nullptr,
+                         int per = 0);
 
 // Grouped (expert-major) forward for many tokens; requires grouped_ok(L).
 bool grouped_ok(const LayerDev* L);

@@ -334,6 +334,30 @@ def test_grouped_config_shape_T2048(moehip):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def test_grouped_many_pairs_dead_slots(moehip):
+    """More pairs than one grouping block takes (700 tokens x top-8 = 5600
+    pairs: 22 blocks of 255, the last 245) with router rows 6-15 NaN, so
+    that only 6 experts are live and every token's slots 6 and 7 hold -1:
+    the selection's per-block counts skip dead slots and the scatter gets
+    exactly the live pairs."""
+    dtype, T, E, D, dff = 3, 700, 16, 256, 256
+    seed = 9700
+    print("many-pairs dead-slots case", flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    rw[6:, 1] = np.nan
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    assert (widx[:, 6:] == -1).all() and (widx[:, :6] >= 0).all()
+    layer = make_layer(moehip, dtype, ex, rw)
+    layer.set_grouped_min_tokens(1)
+    for _ in range(2):
+        got, idx, p = layer.forward(xn, xn)
+        np.testing.assert_array_equal(idx, widx)
+        np.testing.assert_array_equal(bits(p), bits(wp))
+        np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_grouped_and_decode_agree_ties_nan(moehip):
     """Both paths on the same layer and tokens: tied and NaN router logits."""
     dtype, T, E, D, dff = 2, 12, 32, 256, 128
