@@ -36,7 +36,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGroupThreads = 1024;
 // Pairs up to which one block groups them (group_kernel); above, the
-// two-launch count / scatter over at most kGroupBlocks blocks.
+// selection kernel counts the pairs of at most kGroupBlocks grouping blocks
+// and group_scatter_kernel scatters them.
 constexpr int kGroupOneBlockPairs = 4096;
 constexpr int kGroupBatch = 8;   // pair ids per thread in flight in group_kernel
 constexpr int kSelectWaves = 4;

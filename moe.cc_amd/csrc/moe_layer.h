@@ -16,7 +16,7 @@ constexpr int kMaxTopK = 32;
 constexpr int kEgPairs = 256;
 // The smallest task split (sizes the task list).
 constexpr int kMinSplitPairs = 32;
-// Blocks of the two-launch pair grouping at most (sizes L->ghist).
+// Blocks of the many-pair grouping at most (sizes L->ghist).
 constexpr int kGroupBlocks = 64;
 
 struct LayerDev {

@@ -313,7 +313,7 @@ def test_grouped_mixed_limb_segments(moehip, dtype, T):
 def test_grouped_config_shape_T2048(moehip):
     """The prefill bench's layer shape (configs[3]: Q4, E = 128, D = 2048,
     d_ff = 768, top-8) at T = 2048: eight-wave router blocks, x tables
-    packed by the router blocks, one 256-pair task per expert, the two-launch
+    packed by the router blocks, one 256-pair task per expert, the many-pair
     grouping, two down row tiles per block -- bit for bit against the
     oracle (its threaded build: 77 G multiply-adds)."""
     dtype, T, E, D, dff = 3, 2048, 128, 2048, 768
