@@ -99,12 +99,14 @@ struct GateUpArgs {
   uint32_t* hpart;      // [pair][chunk][2] partial (limbs, sum) of each row chunk of h
   int nchunks, rows_per_block;
   int npairs;           // the launch is nchunks x npairs blocks (xcd_chunk_item)
-  // SEL (one token, E <= kTileBlock): the selection is made here, from the
-  // router logits and the x table's nxpart partial headers; p and the
-  // caller's copies (may be null) get the gates
+  // SEL (E <= kTileBlock): the selection is made here, from the router
+  // logits and the x tables' nxpart partial headers (token t's partial of
+  // slice b at uint2 index t * xp_tok + b * xp_slice); p and the caller's
+  // copies (may be null) get the gates
   const float* logits = nullptr;
   const uint32_t* xpart = nullptr;
   int nxpart = 0, E = 0;
+  int xp_tok = 0, xp_slice = 1;
   int* idx_w = nullptr;
   float* p = nullptr;
   int32_t* idx_user = nullptr;
@@ -116,18 +118,19 @@ struct GateUpArgs {
 // fp32 and, packed, into its rows of the pair's table for the down GEMV; the
 // chunk's limb count and activation sum go to hpart (no atomics).  Row chunks
 // start at multiples of 8, so a chunk owns whole packed dwords.
-// SEL (decode, one token): every block ranks the token's E logits itself
+// SEL (decode): every block ranks its token's E logits itself
 // (block_select_slots) and takes the expert of its slot; it also reduces the
-// router blocks' partial headers of the x table (the largest limb count, the
-// wrapping sum), so no kernel runs between the router and this one.  Block
-// (0, 0) writes the selection and gates (select_gates) and the x table's
-// header.
+// router blocks' partial headers of the token's x table (the largest limb
+// count, the wrapping sum), so no kernel runs between the router and this
+// one.  The block of the token's rank 0 and row chunk 0 writes the token's
+// selection and gates (select_gates) and its x table's header.
 template <bool Q4, class G, bool SEL, bool NT>
 __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
   extern __shared__ float hb[];   // [rows_per_block]
   __shared__ int red[2];   // limb count, activation sum
   int rc, q;
   xcd_chunk_item(a.nchunks, a.npairs, &rc, &q);
+  const int t = q / a.topk;
   int e;
   int x_nl = 0;
   // the token's activation sum, handed to the row streaming by address: in
@@ -141,9 +144,10 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     __shared__ int xred[2];
     const int tid = threadIdx.x;
     // both loads first: the logits and the partial headers
-    const float v = tid < a.E ? a.logits[tid] : -__builtin_inff();
+    const float v = tid < a.E ? a.logits[(size_t)t * a.E + tid] : -__builtin_inff();
     uint2 pp = make_uint2(1u, 0u);
-    if (tid < a.nxpart) pp = reinterpret_cast<const uint2*>(a.xpart)[tid];
+    if (tid < a.nxpart)
+      pp = reinterpret_cast<const uint2*>(a.xpart)[(size_t)t * a.xp_tok + (size_t)tid * a.xp_slice];
     if (tid == 0) { xred[0] = 1; xred[1] = 0; }
     block_select_slots<kTileBlock>(v, a.E, a.topk, keys, part, sidx, sval);
     block_max_sum((int)pp.x, pp.y, xred);
@@ -151,12 +155,15 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     // (no partials: the table's header was written by its own pack kernel)
     x_nl = a.nxpart > 0 ? xred[0] : 0;
     x_sum[0] = (uint32_t)xred[1];   // every thread stores the same value before reading it
-    e = sidx[q];
-    if (rc == 0 && q == 0) {
+    const int j = q - t * a.topk;
+    e = sidx[j];
+    if (rc == 0 && j == 0) {
+      const size_t o = (size_t)t * a.topk;
       if (tid < kWave)
-        select_gates(a.topk, sidx, sval, sexp, a.idx_w, a.p, a.idx_user, a.p_user);
+        select_gates(a.topk, sidx, sval, sexp, a.idx_w + o, a.p + o, a.idx_user ? a.idx_user + o : nullptr,
+                     a.p_user ? a.p_user + o : nullptr);
       if (tid == 0 && a.nxpart > 0) {
-        uint32_t* hh = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(a.xtab));
+        uint32_t* hh = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(a.xtab) + (size_t)t * a.tab_bytes);
         hh[0] = (uint32_t)x_nl;
         hh[1] = (uint32_t)xred[1];
       }
@@ -165,7 +172,6 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
     e = a.idx[q];
   }
   if (e < 0) return;
-  const int t = q / a.topk;
   const int r0 = rc * a.rows_per_block;
   const int r1 = r0 + a.rows_per_block < a.dff ? r0 + a.rows_per_block : a.dff;
   const uint8_t* W[2] = {a.gq + (size_t)e * a.dff * a.rb, a.uq + (size_t)e * a.dff * a.rb};
@@ -439,7 +445,7 @@ int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 51
 template <bool Q4, class G>
 void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s,
                     bool sel = false, int nxpart = 0, int32_t* idx_out = nullptr,
-                    float* p_out = nullptr) {
+                    float* p_out = nullptr, int xp_tok = 0, int xp_slice = 1) {
   // rows per block: a multiple of both the wave-group unit and 8 (whole
   // packed dwords of h), sized for ~1024 blocks
   constexpr int unit0 = kTileWaves * G::WR;
@@ -469,8 +475,12 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
   dim3 grid((unsigned)(nc * npairs));
   if (sel) {
     a.logits = L->logits; a.xpart = L->xpart; a.nxpart = nxpart; a.E = L->E;
+    a.xp_tok = xp_tok; a.xp_slice = xp_slice;
     a.idx_w = L->idx; a.p = L->p; a.idx_user = idx_out; a.p_user = p_out;
-    hipLaunchKernelGGL((gate_up_kernel<Q4, G, true, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+    if (cached_loads(T, gateup_cached_min_tokens()))
+      hipLaunchKernelGGL((gate_up_kernel<Q4, G, true, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
+    else
+      hipLaunchKernelGGL((gate_up_kernel<Q4, G, true, true>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
   } else if (cached_loads(T, gateup_cached_min_tokens())) {
     hipLaunchKernelGGL((gate_up_kernel<Q4, G, false, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
   } else {
@@ -577,20 +587,29 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
     ra.sel_counter = L->sel_counter; ra.sel_topk = L->topk;
     ra.sel_idx = L->idx; ra.sel_p = L->p; ra.sel_idx_user = idx_out; ra.sel_p_user = p_out;
   }
-  // one token through the row kernel: the gate/up blocks select themselves
+  // up to two tokens the gate/up blocks select themselves (no selection
+  // launch) after the row kernel, from each token's x-table partials
+  // [token][row]; the same works after the rows kernel (5-16 tokens,
+  // partials [row][16 tokens]) with MOEHIP_SEL_GU_MAX_T raised, but from 4
+  // tokens on the ranking in every block delays the weight streams by more
+  // than the saved launch (measured T = 4 / 8 / 16: +1 / +2 / +2 us)
   static const bool sel_kernel = getenv("MOEHIP_SELECT_KERNEL") != nullptr;
-  const bool sel_gu = fuse_sel && T == 1 && L->E <= kTileBlock && dense_row_path(ra) && !sel_kernel;
-  ra.sel_defer = sel_gu ? 1 : 0;
-  if ((st = dense_matmul(ra, s))) return st;
+  static const int sel_gu_max_t = env_int("MOEHIP_SEL_GU_MAX_T", 2);
   const bool rows_pack = !fuse_sel && ra.pack_dtype != 0;
-  if (!fuse_sel && (st = launch_select(L, T, idx_out, p_out, s,
-                                       rows_pack ? reinterpret_cast<const uint2*>(L->xpart) : nullptr,
-                                       rows_pack ? L->E : 0)))
+  const bool sel_gu = !sel_kernel && T <= sel_gu_max_t && L->E <= kTileBlock &&
+                      ((fuse_sel && dense_row_path(ra)) || (rows_pack && T <= 16));
+  ra.sel_defer = sel_gu && fuse_sel ? 1 : 0;
+  if ((st = dense_matmul(ra, s))) return st;
+  if (!fuse_sel && !sel_gu &&
+      (st = launch_select(L, T, idx_out, p_out, s,
+                          rows_pack ? reinterpret_cast<const uint2*>(L->xpart) : nullptr,
+                          rows_pack ? L->E : 0)))
     return st;
   const int nxpart = ra.pack_dtype ? L->E : 0;
+  const int xp_tok = rows_pack ? 1 : L->E, xp_slice = rows_pack ? 16 : 1;
   int nchunks = 0;
-  if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out); });
-  else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out); });
+  if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out, xp_tok, xp_slice); });
+  else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out, xp_tok, xp_slice); });
   if ((st = check_hip(hipGetLastError(), "gate_up launch"))) return st;
   if (q4) with_geom<true>(L->rbd, [&](auto g) { launch_down<true, decltype(g)>(L, T, nchunks, resid, out, s); });
   else with_geom<false>(L->rbd, [&](auto g) { launch_down<false, decltype(g)>(L, T, nchunks, resid, out, s); });
