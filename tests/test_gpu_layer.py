@@ -97,6 +97,10 @@ CASES = [  # dtype, T, E, D, d_ff, bias, resid
     (2, 1, 200, 512, 256, True, True),
     (3, 1, 256, 512, 256, False, True),
     (3, 1, 300, 512, 256, True, True),
+    # two tokens: each gate/up block ranks its own token's logits and
+    # reduces that token's x-table partials ([token][router row] layout)
+    (2, 2, 128, 2048, 768, True, True),
+    (3, 2, 60, 512, 256, False, True),
     # few tokens, 8 experts: every token takes all 8, so each expert's
     # gate/up stream serves every token (up to 31 slots)
     (3, 20, 8, 512, 256, False, True),
@@ -123,7 +127,7 @@ def test_layer_vs_oracle(moehip, dtype, T, E, D, dff, bias, resid):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("T", [3, 1])
+@pytest.mark.parametrize("T", [3, 2, 1])
 def test_router_ties_and_nan(moehip, T):
     """Equal logits keep the lower expert first; NaN logits are never chosen."""
     dtype, E, D, dff = 2, 32, 256, 128
@@ -140,6 +144,26 @@ def test_router_ties_and_nan(moehip, T):
     assert 3 not in idx
     np.testing.assert_array_equal(idx, widx)
     assert list(idx[0][:3]) == [5, 9, 17]
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 16])
+def test_decode_dead_slots(moehip, T):
+    """Per-pair kernels with router rows 6-15 NaN (16 experts): every
+    token's slots 6 and 7 hold -1, so their gate/up blocks (which select
+    for themselves up to two tokens) and their down terms drop out."""
+    dtype, E, D, dff = 3, 16, 512, 256
+    seed = 9600 + T
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    rw[6:, 3] = np.nan
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    assert (widx[:, 6:] == -1).all() and (widx[:, :6] >= 0).all()
+    layer = make_layer(moehip, dtype, ex, rw)
+    got, idx, p = layer.forward(xn, xn)
+    np.testing.assert_array_equal(idx, widx)
     np.testing.assert_array_equal(bits(p), bits(wp))
     np.testing.assert_array_equal(bits(got), bits(want))
 
