@@ -497,6 +497,7 @@ struct EgArgs {
   uint8_t* htab; size_t htab_bytes;       // gate/up: h tables out
   uint32_t* hpart; int nseg;              // per-segment h headers: written by gate/up, read by down
   float* y;                               // down: [pairs][D]
+  int16_t* y16;                           // down, Q4: [pairs][D] dots that fit int16, else -32768 and y
   int rtpb;                               // down: row tiles per block (rows % tile == 0 when > 1)
 };
 
@@ -722,7 +723,11 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
 
 // y epilogue of one pass (:502-503): lane (j, h) of wave (rg, pg) holds, for
 // pair pbase + 32 (t PG + pg) + j, the dots of rows rb + 64 rg + 32m + 8q +
-// 4h + r.
+// 4h + r.  Q8: y = ((float)dot / 127) * scale in fp32.  Q4: the int32 dot
+// itself (after the -8 sum correction) as int16 when it lies in [-32767,
+// 32767] -- y is a function of the dot and the row's scale, so the combine
+// forms the same fp32 value from it -- else -32768 there and the fp32 y in
+// a.y: half the bytes written here and read by the combine.
 template <bool Q4, int RG, int PG, int NTW>
 __device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, const v16u (&dots)[2][NTW],
                                          int pbase, int n, int rb, const float* sd) {
@@ -735,20 +740,39 @@ __device__ __forceinline__ void down_epi(const EgArgs& a, const EgPairs& sp, con
     if (i >= n) continue;
     const uint32_t hs = sp.asum[i];
     float* yq = a.y + (size_t)sp.pair[i] * a.rows;
+    int16_t* y16q = Q4 ? a.y16 + (size_t)sp.pair[i] * a.rows : nullptr;
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int lr = 64 * rg + 32 * m + 8 * q + 4 * h;
         if (rb + lr >= a.rows) continue;
-        float yv[4];
+        if constexpr (Q4) {
+          uint32_t d[4];
+          bool fits = true;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          uint32_t d = dots[m][t][4 * q + r];
-          if (Q4) d -= 8u * hs;
-          yv[r] = qdot_epilogue(d, div, sd[lr + r]);
+          for (int r = 0; r < 4; ++r) {
+            d[r] = dots[m][t][4 * q + r] - 8u * hs;
+            fits = fits && d[r] + 32767u <= 65534u;   // (int32)d in [-32767, 32767]
+          }
+          uint2 v;
+          v.x = (d[0] & 0xFFFFu) | (d[1] << 16);
+          v.y = (d[2] & 0xFFFFu) | (d[3] << 16);
+          if (!fits) {
+            // rare: the four outputs go to y, the int16 slots hold the marker
+            float yv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) yv[r] = qdot_epilogue(d[r], div, sd[lr + r]);
+            *reinterpret_cast<float4*>(yq + rb + lr) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+            v.x = v.y = 0x80008000u;
+          }
+          *reinterpret_cast<uint2*>(y16q + rb + lr) = v;
+        } else {
+          float yv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) yv[r] = qdot_epilogue(dots[m][t][4 * q + r], div, sd[lr + r]);
+          *reinterpret_cast<float4*>(yq + rb + lr) = make_float4(yv[0], yv[1], yv[2], yv[3]);
         }
-        *reinterpret_cast<float4*>(yq + rb + lr) = make_float4(yv[0], yv[1], yv[2], yv[3]);
         __builtin_amdgcn_sched_barrier(0);
       }
   }
@@ -884,7 +908,7 @@ moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
   const int nseg = (L->dff + 32 * RG - 1) / (32 * RG);
   EgArgs g{L->gq, L->uq, L->gs, L->us, L->rbg, L->dff, L->D, L->topk, L->perm, L->tasks, ntask,
            L->xtab, act_table_bytes(L->D), L->htab, act_table_bytes(L->dff), L->hpart, nseg,
-           nullptr, 1};
+           nullptr, nullptr, 1};
   hipLaunchKernelGGL((gate_up_eg_kernel<Q4, RG, NTW, D, NW>), dim3(tpad * (unsigned)nseg), dim3(64 * NW),
                      C::BYTES, s, g);
   moe_status st = check_hip(hipGetLastError(), "expert gate/up launch");
@@ -894,7 +918,7 @@ moe_status launch_eg_shape(const LayerDev* L, int ntask, hipStream_t s) {
   const int nrt = (L->D + 64 * RG - 1) / (64 * RG);
   const int rtpb = L->D % (64 * RG) == 0 ? min(RTPB, nrt) : 1;
   EgArgs d{L->dq, nullptr, L->ds, nullptr, L->rbd, L->D, L->dff, L->topk, L->perm, L->tasks, ntask,
-           L->htab, act_table_bytes(L->dff), nullptr, 0, L->hpart, nseg, L->y, rtpb};
+           L->htab, act_table_bytes(L->dff), nullptr, 0, L->hpart, nseg, L->y, L->y16, rtpb};
   hipLaunchKernelGGL((down_eg_kernel<Q4, RG, NTW, D, NW>),
                      dim3(tpad * (unsigned)((nrt + rtpb - 1) / rtpb)), dim3(64 * NW), C::BYTES, s, d);
   return check_hip(hipGetLastError(), "expert down launch");

@@ -590,6 +590,121 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *reinterpret_cast<float4*>(out + oi) = acc;
 }
 
+// One Q4 expert output from the down kernel's int16 dot (y16, -32768: the
+// fp32 value is in y instead): ((float)dot / 7) * scale, the operations of
+// the down epilogue (kernels.c:125).
+__device__ __forceinline__ float y16_value(int16_t v, float s, const float* yrow, int c) {
+  return v != -32768 ? qdot_epilogue((uint32_t)(int32_t)v, 7.0f, s) : yrow[c];
+}
+
+// combine for Q4 layers: y from the int16 dots and the experts' down row
+// scales ds [E][D] (1 MB at E = 128, D = 2048, read from the caches), so
+// half the bytes of fp32 y come from memory; same adds in the same order.
+// Eight columns a thread: one 16-byte load of a rank's dots, two of its
+// scales.  The down kernel marks whole groups of four outputs, so one test
+// per group picks the fp32 values.
+template <int K>
+__global__ __launch_bounds__(256) void combine_y16_k_kernel(const int16_t* __restrict__ y16,
+                                                            const float* __restrict__ y,
+                                                            const float* __restrict__ ds,
+                                                            const int* __restrict__ idx,
+                                                            const float* __restrict__ p,
+                                                            const float* __restrict__ resid,
+                                                            float* __restrict__ out, int D) {
+  const int t = blockIdx.y;
+  const int o = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (o >= D) return;
+  int e[K];
+  float pj[K];
+  uint4 yv[K];
+  float4 s0[K], s1[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    e[j] = idx[t * K + j];
+    pj[j] = p[t * K + j];
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    yv[j] = *reinterpret_cast<const uint4*>(y16 + (size_t)(t * K + j) * D + o);
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float4* sr = reinterpret_cast<const float4*>(ds + (size_t)(e[j] >= 0 ? e[j] : 0) * D + o);
+    s0[j] = sr[0];
+    s1[j] = sr[1];
+  }
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (e[j] < 0) continue;
+    const uint32_t w[4] = {yv[j].x, yv[j].y, yv[j].z, yv[j].w};
+    const float sc[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w, s1[j].x, s1[j].y, s1[j].z, s1[j].w};
+    float v[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int16_t d = (int16_t)((w[c / 2] >> (16 * (c % 2))) & 0xFFFFu);
+      v[c] = qdot_epilogue((uint32_t)(int32_t)d, 7.0f, sc[c]);
+    }
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if (w[2 * g] == 0x80008000u) {
+        const float4 f = *reinterpret_cast<const float4*>(y + (size_t)(t * K + j) * D + o + 4 * g);
+        v[4 * g] = f.x; v[4 * g + 1] = f.y; v[4 * g + 2] = f.z; v[4 * g + 3] = f.w;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float a = pj[j] * v[c];
+      acc[c] = acc[c] + a;
+    }
+  }
+  const size_t oi = (size_t)t * D + o;
+  if (resid) {
+    const float4 r0 = *reinterpret_cast<const float4*>(resid + oi);
+    const float4 r1 = *reinterpret_cast<const float4*>(resid + oi + 4);
+    acc[0] = r0.x + acc[0]; acc[1] = r0.y + acc[1]; acc[2] = r0.z + acc[2]; acc[3] = r0.w + acc[3];
+    acc[4] = r1.x + acc[4]; acc[5] = r1.y + acc[5]; acc[6] = r1.z + acc[6]; acc[7] = r1.w + acc[7];
+  }
+  *reinterpret_cast<float4*>(out + oi) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *reinterpret_cast<float4*>(out + oi + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+__global__ __launch_bounds__(256) void combine_y16_kernel(const int16_t* __restrict__ y16,
+                                                          const float* __restrict__ y,
+                                                          const float* __restrict__ ds,
+                                                          const int* __restrict__ idx,
+                                                          const float* __restrict__ p,
+                                                          const float* __restrict__ resid,
+                                                          float* __restrict__ out, int D, int topk) {
+  const int t = blockIdx.y;
+  const int o = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (o >= D) return;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int jj = 0; jj < topk; ++jj) {
+    const int q = t * topk + jj;
+    const int e = idx[q];
+    if (e < 0) continue;
+    const float pj = p[q];
+    const uint2 yv = *reinterpret_cast<const uint2*>(y16 + (size_t)q * D + o);
+    const float4 sv = *reinterpret_cast<const float4*>(ds + (size_t)e * D + o);
+    const float* yrow = y + (size_t)q * D + o;
+    const float y0 = y16_value((int16_t)(yv.x & 0xFFFFu), sv.x, yrow, 0);
+    const float y1 = y16_value((int16_t)(yv.x >> 16), sv.y, yrow, 1);
+    const float y2 = y16_value((int16_t)(yv.y & 0xFFFFu), sv.z, yrow, 2);
+    const float y3 = y16_value((int16_t)(yv.y >> 16), sv.w, yrow, 3);
+    const float a0 = pj * y0, a1 = pj * y1, a2 = pj * y2, a3 = pj * y3;
+    acc.x = acc.x + a0;
+    acc.y = acc.y + a1;
+    acc.z = acc.z + a2;
+    acc.w = acc.w + a3;
+  }
+  const size_t oi = (size_t)t * D + o;
+  if (resid) {
+    const float4 rv = *reinterpret_cast<const float4*>(resid + oi);
+    acc = make_float4(rv.x + acc.x, rv.y + acc.y, rv.z + acc.z, rv.w + acc.w);
+  }
+  *reinterpret_cast<float4*>(out + oi) = acc;
+}
+
 bool is16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 template <int CE, int KC, int WPB>
@@ -676,7 +791,13 @@ moe_status layer_forward_grouped(LayerDev* L, const float* xn, const float* resi
   if ((st = launch_expert_gemm(L, nt, ntask_max, s))) return st;
   // 7. ordered combine + residual
   dim3 cg((unsigned)((L->D / 4 + 255) / 256), (unsigned)T);
-  if (L->topk == 8)
+  if (L->y16 && L->topk == 8 && L->D % 8 == 0)
+    hipLaunchKernelGGL(combine_y16_k_kernel<8>, dim3((unsigned)((L->D / 8 + 255) / 256), (unsigned)T), dim3(256), 0,
+                       s, L->y16, L->y, L->ds, L->idx, L->p, resid, out, L->D);
+  else if (L->y16)
+    hipLaunchKernelGGL(combine_y16_kernel, cg, dim3(256), 0, s, L->y16, L->y, L->ds, L->idx, L->p, resid, out,
+                       L->D, L->topk);
+  else if (L->topk == 8)
     hipLaunchKernelGGL(combine_k_kernel<8>, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D);
   else
     hipLaunchKernelGGL(combine_kernel, cg, dim3(256), 0, s, L->y, L->idx, L->p, resid, out, L->D,

@@ -49,7 +49,10 @@ struct LayerDev {
   int* perm = nullptr;       // [T*topk]
   int2* tasks = nullptr;     // [T*topk/kMinSplitPairs + E + 1] tasks of the expert kernels:
                              // {expert | pairs << 16, first pair in perm}, x = -1 past the last
-  float* y = nullptr;        // [T*topk][D]
+  float* y = nullptr;        // [T*topk][D] fp32 expert outputs (Q8; Q4: the rows whose dot
+                             // leaves int16, the others read 0x8000 in y16)
+  int16_t* y16 = nullptr;    // Q4: [T*topk][D] down dots (after the -8 sum correction) that fit
+                             // int16; -32768 marks an output held in y instead
   int* ghist = nullptr;      // [kGroupBlocks][E] pairs per expert of each grouping block
   uint2* rpart = nullptr;    // [T/16 + 1][ceil(E/4)][16] the router blocks' partial x-table headers
   unsigned* sel_counter = nullptr;   // block counter of the fused selection

@@ -350,7 +350,7 @@ struct ScratchBuf {
   size_t bytes = 0;
 };
 struct SharedScratch {
-  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, tasks, ghist, rpart;
+  ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, y16, tasks, ghist, rpart;
   unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
 };
 SharedScratch g_scratch;
@@ -389,6 +389,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
   if (grouped_ok(L) &&
       ((st = grow(S.ecount, (size_t)L->E * 4, &synced)) || (st = grow(S.eoff, (size_t)L->E * 4, &synced)) ||
        (st = grow(S.perm, np * 4, &synced)) || (st = grow(S.y, np * L->D * 4, &synced)) ||
+       (L->dtype == 3 && (st = grow(S.y16, np * L->D * 2, &synced))) ||
        (st = grow(S.tasks, (np / kMinSplitPairs + L->E + 1) * 8, &synced)) ||
        (st = grow(S.ghist, (size_t)kGroupBlocks * L->E * 4, &synced)) ||
        (st = grow(S.rpart, ((size_t)T / 16 + 1) * ((L->E + 3) / 4) * 16 * 8, &synced))))
@@ -405,6 +406,7 @@ moe_status ensure_scratch(LayerDev* L, int T) {
     if ((st = check_hip(hipMemsetAsync(S.sel_counter, 0, 4, stream()), "counter init"))) return st;
   }
   L->y = (float*)S.y.p;
+  L->y16 = L->dtype == 3 ? (int16_t*)S.y16.p : nullptr;
   L->sel_counter = S.sel_counter;
   L->capT = T;
   return MOE_OK;
@@ -414,7 +416,7 @@ void release_scratch_all() {
   std::lock_guard<std::mutex> lk(g_layer_mu);
   SharedScratch& S = g_scratch;
   for (ScratchBuf* b : {&S.logits, &S.idx, &S.p, &S.xtab, &S.htab, &S.h, &S.xn, &S.hpart, &S.xpart,
-                        &S.ecount, &S.eoff, &S.perm, &S.y, &S.tasks, &S.ghist, &S.rpart}) {
+                        &S.ecount, &S.eoff, &S.perm, &S.y, &S.y16, &S.tasks, &S.ghist, &S.rpart}) {
     dfree(b->p);
     b->p = nullptr;
     b->bytes = 0;
@@ -897,6 +899,7 @@ moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, cons
   L->rpart = nullptr;
   L->tasks = nullptr;
   L->y = nullptr;
+  L->y16 = nullptr;
   L->capT = T;
   return layer_forward_run(L, x_norm, -1.0f, x_resid, T, out, idx_out, p_out, false);
 }

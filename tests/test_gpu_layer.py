@@ -334,6 +334,61 @@ def test_grouped_mixed_limb_segments(moehip, dtype, T):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def _q4_down_dots(ex, xn, widx):
+    """The Q4 down products' int32 dots of every live (token, rank) pair,
+    from the oracle's expert GEMVs (kernels.c:96-128) and SwiGLU."""
+    D, dff = ex.D, ex.d_ff
+    out = []
+    for t in range(xn.shape[0]):
+        for e in widx[t]:
+            if e < 0:
+                continue
+            g = O.gemv_q4(xn[t:t + 1], ex.gq[e], ex.gs[e], dff, D)
+            u = O.gemv_q4(xn[t:t + 1], ex.uq[e], ex.us[e], dff, D)
+            h = (O.silu(g) * u).astype(np.float32).reshape(-1)
+            a = np.trunc((h * np.float32(7.0)).astype(np.float64)).astype(np.int64)
+            w = ex.dq[e].astype(np.int64)
+            wu = np.empty((D, dff), np.int64)
+            wu[:, 0::2] = (w & 0xF) - 8
+            wu[:, 1::2] = (w >> 4) - 8
+            out.append(wu @ a)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("factor", [40.0, 300.0, 3000.0])
+def test_grouped_q4_int16_down_dots(moehip, factor):
+    """The expert-major Q4 down kernel hands the combine each output's int32
+    dot as int16 when it lies in [-32767, 32767], else a marker and the fp32
+    value: gate/up row scales x factor put the down dots inside int16
+    (1), across its edge within one pair (300) and mostly past it (3000);
+    the host counts the dots of each case from the oracle's own GEMVs so
+    that both paths are known to run, and the layer stays bit-identical."""
+    dtype, E, D, dff, T = 3, 16, 512, 768, 48
+    seed = 8900 + int(factor)
+    print("int16 dots case", factor, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    ex.gs[:] *= np.float32(factor)
+    ex.us[:] *= np.float32(factor)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    xr = O.normal(T * D, seed + 13, 0.0, 1.0).reshape(T, D)
+    want, widx, wp, _ = O.moe_block(xn, xr, rw, None, ex)
+    big = np.abs(_q4_down_dots(ex, xn, widx)) > 32767
+    if factor == 40.0:
+        assert not big.any() and np.abs(_q4_down_dots(ex, xn, widx)).max() > 1000
+    elif factor == 300.0:
+        assert 0.05 < big.mean() < 0.95, big.mean()
+    else:
+        assert big.mean() > 0.95, big.mean()
+    layer = make_layer(moehip, dtype, ex, rw)
+    layer.set_grouped_min_tokens(1)
+    got, idx, p = layer.forward(xn, xr)
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+    layer.close()
+
+
 def test_grouped_config_shape_T2048(moehip):
     """The prefill bench's layer shape (configs[3]: Q4, E = 128, D = 2048,
     d_ff = 768, top-8) at T = 2048: eight-wave router blocks, x tables
