@@ -74,6 +74,25 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 
 // ---------------------------------------------------------------- products
 
+// The product ring's hand-over inside one block, through LDS counters
+// instead of a block barrier per chunk: a producer publishes chunk k by
+// storing k + 1 into full[k % NB] (release, after its product stores), the
+// consumer publishes how many chunks it has summed in `done` (release,
+// after its reads).  A producer waits for done >= k - NB + 1 before reusing
+// a buffer, the consumer for full[c % NB] >= c + 1; neither waits on itself,
+// so every wait ends.  The spin is capped all the same (2^22 polls, about a
+// hundred times a whole product's time), so that the kernel always exits.
+__device__ __forceinline__ void ring_wait(int* ctr, int target, bool nap) {
+  for (int i = 0; i < (1 << 22); ++i) {
+    if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    if (nap) __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void ring_post(int* ctr, int v) {
+  __hip_atomic_store(ctr, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+
 // Few tokens (M <= MM = 64 / RW): a block owns RW output rows; wave 0 is the
 // consumer, waves 1..NP are producers.  The weight rows and the M token rows
 // stream in chunks of KC columns with coalesced 16-byte loads; producer p
@@ -98,10 +117,11 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 // Each block also writes a column slice of the normalized rows and
 // (PACK = 2 / 3) packs the slice into the activation tables; the last block
 // (fused selection) writes the tables' headers.
-template <int RW, bool NORM, int PACK, int NP>
+template <int RW, bool NORM, int PACK, int NP, int MMX = 64 / RW>
 __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) {
   constexpr int KC = RW >= 16 ? 4096 / RW : 256;
-  constexpr int MM = 64 / RW;                // token rows one block can chain
+  constexpr int MM = MMX;                    // token rows one block can chain (<= 64 / RW)
+  static_assert(MM * RW <= 64, "one consumer lane per chain");
   constexpr int V4 = KC / 4;                 // float4 per row chunk (<= 64)
   constexpr int LD = KC + 4;                 // padded LDS row (floats)
   constexpr int RPL = 64 / V4;               // rows one load instruction covers
@@ -113,6 +133,9 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   __shared__ float inv_s[MM];
   __shared__ int pack_scratch[2];
   __shared__ SeqSumScratch seq;
+  __shared__ int ring_full[NP + 1], ring_done;
+  if (threadIdx.x <= NP) ring_full[threadIdx.x] = 0;
+  if (threadIdx.x == 0) ring_done = 0;
   const int M = a.M, N = a.N, K = a.K;
   const int nc = (K + KC - 1) / KC;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -265,25 +288,44 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
   }
   if constexpr (!NORM) {
     if (prod >= 0 && prod < nc) loadW(prod);
+    if constexpr (PACK != 0) {
+      // up to 16 given rows: this block's column slice [c0, c1) of each
+      // token row into its activation table, V columns a thread, while the
+      // first chunks load; the slice's partial header {limbs, sum} goes to
+      // pack_part[block][token] (select_kernel writes the headers)
+      constexpr int V = PACK == 3 ? 8 : 4;
+      __shared__ unsigned pk[16][2];
+      if (threadIdx.x < 16) { pk[threadIdx.x][0] = 1u; pk[threadIdx.x][1] = 0u; }
+      __syncthreads();
+      const int sl = ((K + 7) / 8 + (int)gridDim.x - 1) / (int)gridDim.x * 8;
+      const int c0 = min(K, (int)blockIdx.x * sl), c1 = min(K, c0 + sl);
+      const int G = (c1 - c0 + V - 1) / V;
+      const size_t tb = act_table_bytes(K);
+      for (int i = threadIdx.x; i < M * G; i += NT) {
+        const int m = i / G, g0 = c0 + (i % G) * V;
+        int nl;
+        uint32_t sum;
+        pack_act_cols<PACK == 3>(a.A + (size_t)m * a.lda, K, g0, min(c1, g0 + V), a.pack_tabs + m * tb, 0, 1,
+                                 nl, sum);
+        atomicMax(&pk[m][0], (unsigned)nl);
+        atomicAdd(&pk[m][1], sum);
+      }
+      __syncthreads();
+      if (threadIdx.x < M)
+        reinterpret_cast<uint2*>(a.pack_part)[(size_t)blockIdx.x * 16 + threadIdx.x] =
+            make_uint2(pk[threadIdx.x][0], pk[threadIdx.x][1]);
+    }
   }
+  __syncthreads();   // the ring counters are zero
   if (prod >= 0) {
     if (prod < nc) loadX(prod);
-    if (prod == 0) {
-      produce(0);
-      if (NP < nc) {
-        loadW(NP);
-        loadX(NP);
-      }
-    }
-    for (int c = 0; c < nc; ++c) {
-      __syncthreads();
-      const int k = c + 1;
-      if (k < nc && k % NP == prod) {
-        produce(k);
-        if (k + NP < nc) {
-          loadW(k + NP);
-          loadX(k + NP);
-        }
+    for (int k = prod; k < nc; k += NP) {
+      if (k >= NB) ring_wait(&ring_done, k - NB + 1, true);
+      produce(k);
+      ring_post(&ring_full[k % NB], k + 1);
+      if (k + NP < nc) {
+        loadW(k + NP);
+        loadX(k + NP);
       }
     }
   } else {
@@ -291,8 +333,9 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
     const bool live = m < M;
     float acc = 0.0f;
     for (int c = 0; c < nc; ++c) {
-      __syncthreads();
+      ring_wait(&ring_full[c % NB], c + 1, false);
       if (live) acc = chain_sum(acc, pl + (c % NB) * bufsz + lane * LD, V4);
+      ring_post(&ring_done, c + 1);
     }
     const int n = n0 + r;
     float c = -__builtin_inff();
@@ -1450,12 +1493,12 @@ size_t gemv_lds(int RW, int NP, int M, int K, bool norm) {
   return ((size_t)(NP + 1) * M * RW * (KC + 4) + (norm ? (size_t)M * K : 0)) * 4;
 }
 
-template <int RW, bool NORM, int PACK, int NP>
+template <int RW, bool NORM, int PACK, int NP, int MMX = 64 / RW>
 moe_status launch_gemv(const DenseArgs& a, hipStream_t s) {
   const size_t lds = gemv_lds(RW, NP, a.M, a.K, NORM);
-  moe_status st = set_lds(dense_gemv_kernel<RW, NORM, PACK, NP>, lds, "gemv LDS attribute");
+  moe_status st = set_lds(dense_gemv_kernel<RW, NORM, PACK, NP, MMX>, lds, "gemv LDS attribute");
   if (st) return st;
-  hipLaunchKernelGGL((dense_gemv_kernel<RW, NORM, PACK, NP>), dim3((unsigned)((a.N + RW - 1) / RW)),
+  hipLaunchKernelGGL((dense_gemv_kernel<RW, NORM, PACK, NP, MMX>), dim3((unsigned)((a.N + RW - 1) / RW)),
                      dim3(64 * (NP + 1)), lds, s, a);
   return check_hip(hipGetLastError(), "dense gemv launch");
 }
@@ -1506,6 +1549,13 @@ bool dense_row_ok(const DenseArgs& a, bool vec) {
 bool dense_rows4_ok(const DenseArgs& a, bool vec) {
   return a.M > 4 && a.M <= 16 && !a.norm && !a.sel_counter && !a.amax_part && a.N <= 1024 && vec &&
          a.K <= kRowsMaxK;
+}
+
+// The block-parallel rows kernel instead of the chain kernel for 5-16
+// given rows (MOEHIP_ROUTER_ROWS4=1, for comparison).
+bool rows4_kernel_chosen() {
+  static const bool v = getenv("MOEHIP_ROUTER_ROWS4") != nullptr;
+  return v;
 }
 
 bool dense_rows4_path(const DenseArgs& a) {
@@ -1579,6 +1629,19 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
     if (a.pack_dtype == 2) return launch_row<false, 2>(a, s);
     if (a.pack_dtype == 3) return launch_row<false, 3>(a, s);
     return launch_row<false, 0>(a, s);
+  }
+  if (dense_rows4_ok(a, vec) && !rows4_kernel_chosen()) {
+    // 5-16 given rows against few rows (the router): one block per row, one
+    // consumer lane per token's sequential chain, three producer waves
+    static const bool np7 = getenv("MOEHIP_ROUTER_NP7") != nullptr;
+    if (np7) {
+      if (a.pack_dtype == 2) return launch_gemv<1, false, 2, 7, 16>(a, s);
+      if (a.pack_dtype == 3) return launch_gemv<1, false, 3, 7, 16>(a, s);
+      return launch_gemv<1, false, 0, 7, 16>(a, s);
+    }
+    if (a.pack_dtype == 2) return launch_gemv<1, false, 2, 3, 16>(a, s);
+    if (a.pack_dtype == 3) return launch_gemv<1, false, 3, 3, 16>(a, s);
+    return launch_gemv<1, false, 0, 3, 16>(a, s);
   }
   if (dense_rows4_ok(a, vec)) {
     const size_t lds = (size_t)kRowGroups * a.K * 4;
