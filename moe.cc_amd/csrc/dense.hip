@@ -1633,12 +1633,6 @@ moe_status dense_matmul(const DenseArgs& a, hipStream_t s) {
   if (dense_rows4_ok(a, vec) && !rows4_kernel_chosen()) {
     // 5-16 given rows against few rows (the router): one block per row, one
     // consumer lane per token's sequential chain, three producer waves
-    static const bool np7 = getenv("MOEHIP_ROUTER_NP7") != nullptr;
-    if (np7) {
-      if (a.pack_dtype == 2) return launch_gemv<1, false, 2, 7, 16>(a, s);
-      if (a.pack_dtype == 3) return launch_gemv<1, false, 3, 7, 16>(a, s);
-      return launch_gemv<1, false, 0, 7, 16>(a, s);
-    }
     if (a.pack_dtype == 2) return launch_gemv<1, false, 2, 3, 16>(a, s);
     if (a.pack_dtype == 3) return launch_gemv<1, false, 3, 3, 16>(a, s);
     return launch_gemv<1, false, 0, 3, 16>(a, s);
