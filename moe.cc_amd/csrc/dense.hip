@@ -74,23 +74,6 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 
 // ---------------------------------------------------------------- products
 
-// The product ring's hand-over inside one block, through LDS counters
-// instead of a block barrier per chunk: a producer publishes chunk k by
-// storing k + 1 into full[k % NB] (release, after its product stores), the
-// consumer publishes how many chunks it has summed in `done` (release,
-// after its reads).  A producer waits for done >= k - NB + 1 before reusing
-// a buffer, the consumer for full[c % NB] >= c + 1; neither waits on itself,
-// so every wait ends.  The spin is capped all the same (2^22 polls, about a
-// hundred times a whole product's time), so that the kernel always exits.
-__device__ __forceinline__ void ring_wait(int* ctr, int target, bool nap) {
-  for (int i = 0; i < (1 << 22); ++i) {
-    if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
-    if (nap) __builtin_amdgcn_s_sleep(1);
-  }
-}
-__device__ __forceinline__ void ring_post(int* ctr, int v) {
-  __hip_atomic_store(ctr, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
 
 
 // Few tokens (M <= MM = 64 / RW): a block owns RW output rows; wave 0 is the
@@ -316,6 +299,11 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
             make_uint2(pk[threadIdx.x][0], pk[threadIdx.x][1]);
     }
   }
+  // The ring's hand-over: a producer stores k + 1 into ring_full[k % NB]
+  // after writing chunk k, the consumer the number of chunks it has summed
+  // into ring_done; a producer waits for ring_done >= k - NB + 1 before
+  // reusing a buffer, the consumer for ring_full[c % NB] >= c + 1.  Neither
+  // side waits on itself, so every wait ends.
   __syncthreads();   // the ring counters are zero
   if (prod >= 0) {
     if (prod < nc) loadX(prod);

@@ -149,6 +149,21 @@ __device__ __forceinline__ float expf_glibc_t(float x, const uint64_t* tab) {
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
 
+// Hand-over between the waves of one block through LDS counters instead of
+// a block barrier: the producing side stores or adds to a counter after
+// its data (release), the consuming side polls it (acquire).  The poll is
+// capped (2^22 polls, about a hundred times any kernel's own time) so that a
+// kernel always exits; the users arrange that no wait depends on itself.
+__device__ __forceinline__ void ring_wait(int* ctr, int target, bool nap) {
+  for (int i = 0; i < (1 << 22); ++i) {
+    if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    if (nap) __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void ring_post(int* ctr, int v) {
+  __hip_atomic_store(ctr, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // acc = ((acc + p0) + p1) + ... over 4*n4 values of an LDS row (16-byte
 // aligned): the sequential fp32 sum of the reference, as pure dependent adds
 // (operands formed beforehand, by other lanes); 16 float4 are read ahead of
