@@ -334,6 +334,32 @@ def test_grouped_mixed_limb_segments(moehip, dtype, T):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("dtype,top_k,T,grouped", [(3, 4, 64, True), (2, 6, 48, True), (3, 2, 40, True),
+                                                    (3, 4, 5, False), (2, 6, 3, False), (2, 2, 1, False)])
+def test_layer_other_top_k(moehip, dtype, top_k, T, grouped):
+    """A top-k other than 8 (model.h keeps it a config value): the
+    selection, the gates and the combine over k ranks (the expert-major
+    path's runtime-k combine kernels, fp32 y for Q8 and int16 dots for Q4;
+    the per-pair kernels below 32 tokens), bit for bit against the oracle."""
+    E, D, dff = 32, 512, 256
+    seed = 9100 + dtype * 10 + top_k + T
+    print("top-k case", dtype, top_k, T, grouped, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    ex.gs[:] *= np.float32(60.0)
+    ex.us[:] *= np.float32(60.0)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    xn = O.normal(T * D, seed + 12, 0.0, 1.0).reshape(T, D)
+    xr = O.normal(T * D, seed + 13, 0.0, 1.0).reshape(T, D)
+    want, widx, wp, wlog = O.moe_block(xn, xr, rw, None, ex, top_k)
+    layer = make_layer(moehip, dtype, ex, rw, top_k=top_k)
+    layer.set_grouped_min_tokens(1 if grouped else 1000)
+    got, idx, p = layer.forward(xn, xr)
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+    layer.close()
+
+
 def _q4_down_dots(ex, xn, widx):
     """The Q4 down products' int32 dots of every live (token, rank) pair,
     from the oracle's expert GEMVs (kernels.c:96-128) and SwiGLU."""
