@@ -74,8 +74,6 @@ __device__ __forceinline__ float dense_epilogue(const DenseArgs& a, int m, int n
 
 // ---------------------------------------------------------------- products
 
-
-
 // Few tokens (M <= MM = 64 / RW): a block owns RW output rows; wave 0 is the
 // consumer, waves 1..NP are producers.  The weight rows and the M token rows
 // stream in chunks of KC columns with coalesced 16-byte loads; producer p
@@ -276,6 +274,7 @@ __global__ __launch_bounds__(64 * (NP + 1)) void dense_gemv_kernel(DenseArgs a) 
       // token row into its activation table, V columns a thread, while the
       // first chunks load; the slice's partial header {limbs, sum} goes to
       // pack_part[block][token] (select_kernel writes the headers)
+      static_assert(MM <= 16, "partial headers of up to 16 tokens a block");
       constexpr int V = PACK == 3 ? 8 : 4;
       __shared__ unsigned pk[16][2];
       if (threadIdx.x < 16) { pk[threadIdx.x][0] = 1u; pk[threadIdx.x][1] = 0u; }
