@@ -677,7 +677,7 @@ __global__ __launch_bounds__(64 * NW) void gate_up_eg_kernel(EgArgs a) {
     sp.asum[i] = act_asum(tb);
     sp.red_nl[i] = 1;
     sp.red_sum[i] = 0;
-    const int v = act_nl(tb);
+    const int v = min(act_nl(tb), 4);   // 1, 2 or 4; never past the table's planes
     nl = v > nl ? v : nl;
   }
   if (nl > 1) atomicMax(&sp.nl, nl);
@@ -820,7 +820,9 @@ __global__ __launch_bounds__(64 * NW) void down_eg_kernel(EgArgs a) {
   for (int k = tid; k < n * a.nseg; k += NTH) {
     const int i = k / a.nseg, sg = k - i * a.nseg;
     const uint32_t* pp = a.hpart + ((size_t)sp.pair[i] * a.nseg + sg) * 2;
-    const int v = (int)pp[0];
+    // 1, 2 or 4 limbs (limbs_needed); held to 4 so that no value can send
+    // the limb passes past a table's four planes
+    const int v = min((int)pp[0], 4);
     if (v > 1) {
       atomicMax(&sp.red_nl[i], v);
       for (int l = 1; l < v; ++l) atomicOr(&segmask[(l - 1) * kEgPairs + i], 1u << sg);
