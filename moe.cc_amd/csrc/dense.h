@@ -57,6 +57,9 @@ struct DenseArgs {
   // consecutive outputs also writes its largest value (NaN if it has one)
   // to amax_part[block], for greedy_vec.
   float* amax_part = nullptr;
+  // Optional (row kernel): one thread advances this device word by one
+  // (skipping 0) -- the tag of the launch that follows.
+  uint32_t* epoch_bump = nullptr;
 };
 moe_status dense_matmul(const DenseArgs& a, hipStream_t s);
 bool dense_amax_ok(const DenseArgs& a);

@@ -407,6 +407,10 @@ __global__ __launch_bounds__(kRowThreads) void dense_row_kernel(DenseArgs a) {
   __shared__ int pack_scratch[2];
   __shared__ float inv_s;
   const int tid = threadIdx.x, lane = tid % kWave;
+  if (a.epoch_bump && n == 0 && m == 0 && tid == 0) {
+    const uint32_t e = *a.epoch_bump + 1u;
+    *a.epoch_bump = e ? e : 1u;
+  }
   constexpr int WV = kRowMaxK / 4 / kRowThreads;
   // the token row (and norm weights) into registers first, then the weight
   // row (a wave's loads complete in order: the LDS staging waits only for

@@ -56,6 +56,8 @@ struct LayerDev {
   int* ghist = nullptr;      // [kGroupBlocks][E] pairs per expert of each grouping block
   uint2* rpart = nullptr;    // [T/16 + 1][ceil(E/4)][16] the router blocks' partial x-table headers
   unsigned* sel_counter = nullptr;   // block counter of the fused selection
+  uint64_t* ftag = nullptr;   // one token: tagged words of the gate/up + down launch (or null)
+  uint32_t* epoch = nullptr;  // its tag, advanced by the router launch before it
 };
 
 // Top-k and softmax gates of T tokens from L->logits into L->idx / L->p

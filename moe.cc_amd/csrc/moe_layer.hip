@@ -124,12 +124,24 @@ struct GateUpArgs {
 // count, the wrapping sum), so no kernel runs between the router and this
 // one.  The block of the token's rank 0 and row chunk 0 writes the token's
 // selection and gates (select_gates) and its x table's header.
+// Tagged copies of gate/up's outputs for the one-token gate/up + down
+// launch, and that launch's tag: an epoch that the router launch before it
+// advances (so every launch, graph replays included, has its own tag and a
+// word left from an earlier launch never passes for a current one).
+struct FuseTags {
+  uint64_t* tab = nullptr;     // [pair][4 planes][pw] the h tables' plane dwords
+  uint64_t* h = nullptr;       // [pair][dff] fp32 h (for the exact fallback)
+  uint64_t* part = nullptr;    // [pair][pchunks][2] each row chunk's {limbs}, {sum}
+  const uint32_t* epoch = nullptr;
+  int pw = 0;                  // dwords per plane (act table layout)
+  int pchunks = 0;             // chunk stride of part
+  long long wait_ticks = 0;    // longest wait, wall-clock ticks
+};
+
 template <bool Q4, class G, bool SEL, bool NT>
-__global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
-  extern __shared__ float hb[];   // [rows_per_block]
+__device__ __forceinline__ void gate_up_block(const GateUpArgs& a, int rc, int q, float* hb,
+                                              const FuseTags* ft, uint32_t tag) {
   __shared__ int red[2];   // limb count, activation sum
-  int rc, q;
-  xcd_chunk_item(a.nchunks, a.npairs, &rc, &q);
   const int t = q / a.topk;
   int e;
   int x_nl = 0;
@@ -188,18 +200,34 @@ __global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
                                    x_nl > 0 ? x_sum : nullptr);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < r1 - r0; i += blockDim.x) a.h[(size_t)q * a.dff + r0 + i] = hb[i];
+  for (int i = threadIdx.x; i < r1 - r0; i += blockDim.x) {
+    a.h[(size_t)q * a.dff + r0 + i] = hb[i];
+    if (ft) tag_put(ft->h + (size_t)q * a.dff + r0 + i, tag, __float_as_uint(hb[i]));
+  }
   int nl;
   uint32_t sum;
   pack_act_cols<Q4>(hb - r0, a.dff, r0, r1, a.htab + (size_t)q * a.htab_bytes, threadIdx.x,
-                    blockDim.x, nl, sum);
+                    blockDim.x, nl, sum, ft ? ft->tab + (size_t)q * 4 * ft->pw : nullptr, tag);
   block_max_sum(nl, sum, red);
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t* pp = a.hpart + ((size_t)q * a.nchunks + rc) * 2;
     pp[0] = (uint32_t)red[0];
     pp[1] = (uint32_t)red[1];
+    if (ft) {
+      uint64_t* tp = ft->part + ((size_t)q * ft->pchunks + rc) * 2;
+      tag_put(tp, tag, (uint32_t)red[0]);
+      tag_put(tp + 1, tag, (uint32_t)red[1]);
+    }
   }
+}
+
+template <bool Q4, class G, bool SEL, bool NT>
+__global__ __launch_bounds__(kTileBlock) void gate_up_kernel(GateUpArgs a) {
+  extern __shared__ float hb[];   // [rows_per_block]
+  int rc, q;
+  xcd_chunk_item(a.nchunks, a.npairs, &rc, &q);
+  gate_up_block<Q4, G, SEL, NT>(a, rc, q, hb, nullptr, 0u);
 }
 
 struct DownArgs {
@@ -288,6 +316,230 @@ __global__ __launch_bounds__(kCombineThreads) void down_combine_kernel(DownArgs 
   }
 }
 
+// ---- one token: gate/up and down in one launch ----
+//
+// Blocks [0, ngu) are the gate/up blocks of gate_up_kernel<SEL> (the same
+// selection, rows, tables and partial headers, each also stored as tagged
+// words); blocks [ngu, ngu + nrc) are down blocks of G::WR output rows,
+// 256 threads, wave w taking ranks w and w + 4.  A down block makes the
+// token's selection itself (the gate/up blocks' rule on the same logits),
+// requests its experts' weight rows and scales, and only then waits for
+// the tagged words: each pair's chunk partials (limb count, activation sum),
+// then the table dwords its lanes multiply -- straight into registers -- or,
+// for activations past the register budget, the fp32 h (exact fallback).
+// The combine is down_combine_kernel's (rank order, one rounding per
+// product and sum).  Every down block comes after every gate/up block in
+// the grid, and blocks are dispatched in order, so the blocks it waits on
+// are running or done; a wait still ends at a deadline, and a block that
+// hit one writes NaN rows instead of a result.
+struct FuseArgs {
+  GateUpArgs gu;
+  DownArgs dn;
+  FuseTags ft;
+  int ngu;
+};
+constexpr int kFuseTopK = 8;   // ranks of the fused launch (two a wave)
+constexpr int kFusePlaneWords = 3;   // table dwords a lane per plane: d_ff <= 768
+
+template <bool Q4, class G>
+__device__ void down_fused_block(const FuseArgs& f, int rc, uint32_t tag, float* lds) {
+  const DownArgs& a = f.dn;
+  constexpr int NWV = kTileWaves;
+  constexpr int JP = kFuseTopK / NWV;   // ranks per wave
+  __shared__ __align__(16) uint64_t keys[kTileBlock];
+  __shared__ int part[kTileBlock];
+  __shared__ int sidx[kFuseTopK], gidx[kFuseTopK];
+  __shared__ float sval[kFuseTopK], sexp[kFuseTopK], gp[kFuseTopK];
+  __shared__ int late_any;
+  float* yb = lds;                         // [kFuseTopK][G::WR]
+  uint32_t* tabl = reinterpret_cast<uint32_t*>(lds + kFuseTopK * G::WR);   // [kFuseTopK][2][pw]
+  float* hx = lds + kFuseTopK * G::WR + kFuseTopK * 2 * f.ft.pw;   // [topk][dff] fallback h
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const long long deadline = wall_clock64() + f.ft.wait_ticks;
+  const int r0 = rc * G::WR, r1 = min(r0 + G::WR, a.D);
+  const int g = lane / G::LPR, r = lane % G::LPR;
+  const int row = r0 + g;
+  const float v = tid < f.gu.E ? f.gu.logits[tid] : -__builtin_inff();
+  // the residual rows now, not after the waits
+  const float rv = a.resid && r0 + tid < r1 ? a.resid[r0 + tid] : 0.0f;
+  if (tid == 0) late_any = 0;
+  block_select_slots<kTileBlock>(v, f.gu.E, a.topk, keys, part, sidx, sval);
+  __syncthreads();
+  if (wave == 0) select_gates(a.topk, sidx, sval, sexp, gidx, gp, nullptr, nullptr);
+  // the weight rows and scales of this wave's ranks first
+  uint32_t w[JP][G::DW];
+  float sc[JP];
+  int ej[JP];
+#pragma unroll
+  for (int i = 0; i < JP; ++i) {
+    const int j = wave + NWV * i;
+    ej[i] = j < a.topk ? sidx[j] : -1;
+    if (ej[i] >= 0 && row < r1) {
+      load_row_regs<G, true>(a.dq + ((size_t)ej[i] * a.D + row) * (size_t)a.rb, w[i]);
+      sc[i] = a.ds[(size_t)ej[i] * a.D + row];
+    } else {
+#pragma unroll
+      for (int d = 0; d < G::DW; ++d) w[i][d] = 0;
+      sc[i] = 0.0f;
+    }
+  }
+  // Waiting: first one thread polls a single probe word (the last chunk
+  // partial of one rank) with long sleeps -- the gate/up blocks all run at
+  // once, so when it is there the rest nearly are -- then each wave fetches
+  // both of its ranks' chunk partials and the table dwords its lanes
+  // multiply (Q4 one limb plane, Q8 two) in one batch, polling again only
+  // what is stale.  (Every lane polling everything from the start floods
+  // the memory system under the gate/up weight streams.)
+  bool late = false;
+  const bool any = sidx[0] >= 0;   // rank 0 is live unless every logit is NaN or -inf
+  if (any && tid == 0) {
+    int pj = rc % a.topk;
+    if (sidx[pj] < 0) pj = 0;
+    const uint64_t* pr = f.ft.part + ((size_t)pj * f.ft.pchunks + f.gu.nchunks - 1) * 2;
+    uint32_t pv[1];
+    tag_wait_all<1, 10>([&](int) { return pr; }, pv, tag, deadline, late);
+    if (late) late_any = 1;
+  }
+  __syncthreads();
+  if (late_any) late = true;
+  const int K = a.dff, KW = (K + 7) / 8, pw = f.ft.pw;
+  const int nw = Q4 ? 2 * KW : (K + 3) / 4;   // plane dwords the gate/up blocks write
+  const float div = Q4 ? 7.0f : 127.0f;
+  constexpr int NLF = Q4 ? 1 : 2;                 // limb planes fetched up front
+  constexpr int NWD = 4 + NLF * kFusePlaneWords;  // words a lane per rank
+  uint32_t tv[JP * NWD];
+  if (any) {
+    tag_wait_all<JP * NWD>(
+        [&](int i2) {
+          const int ip = i2 / NWD, u = i2 % NWD;
+          const int jj = ej[ip] >= 0 ? wave + NWV * ip : 0;   // dead rank: rank 0's words, unused
+          if (u < 4) {   // chunks lane and lane + 64 (clamped to the last)
+            const int c = lane + kWave * (u / 2);
+            return f.ft.part + ((size_t)jj * f.ft.pchunks + (c < f.gu.nchunks ? c : f.gu.nchunks - 1)) * 2 +
+                   u % 2;
+          }
+          const int l = (u - 4) / kFusePlaneWords, t = (u - 4) % kFusePlaneWords;
+          const int dw = lane + kWave * t;
+          return f.ft.tab + ((size_t)jj * 4 + l) * pw + (dw < nw ? dw : nw - 1);
+        },
+        tv, tag, deadline, late);
+  }
+  // each rank's limb count and sum; its first NLF table planes into this
+  // wave's LDS (then read back in load_act_regs' layout)
+  int nlr[JP];
+  uint32_t smr[JP];
+  bool one = true;   // every live rank at one limb (the common case)
+#pragma unroll
+  for (int i = 0; i < JP; ++i) {
+    const int j = wave + NWV * i;
+    int n = lane < f.gu.nchunks ? (int)tv[i * NWD] : 1;
+    uint32_t sm = lane < f.gu.nchunks ? tv[i * NWD + 1] : 0u;
+    if (lane + kWave < f.gu.nchunks) {
+      n = (int)tv[i * NWD + 2] > n ? (int)tv[i * NWD + 2] : n;
+      sm += tv[i * NWD + 3];
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const int o = __shfl_xor(n, off, kWave);
+      n = o > n ? o : n;
+      sm += (uint32_t)__shfl_xor((int)sm, off, kWave);
+    }
+    nlr[i] = n <= 1 ? 1 : (n <= 2 ? 2 : 4);
+    smr[i] = sm;
+    if (ej[i] < 0) continue;
+    one = one && nlr[i] == 1;
+    uint32_t* tl = tabl + (size_t)j * NLF * pw;
+#pragma unroll
+    for (int l = 0; l < NLF; ++l)
+#pragma unroll
+      for (int t = 0; t < kFusePlaneWords; ++t) {
+        const int dw = lane + kWave * t;
+        if (dw < nw) tl[l * pw + dw] = tv[i * NWD + 4 + l * kFusePlaneWords + t];
+      }
+  }
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  auto dot_rank = [&](int i, auto nl_tag) {
+    constexpr int NL = decltype(nl_tag)::value;
+    const uint32_t* tl = tabl + (size_t)(wave + NWV * i) * NLF * pw;
+    ActRegs<Q4, G, NL> ar;
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+#pragma unroll
+      for (int p = 0; p < G::P; ++p) {
+        const int d = (p * G::LPR + r) * 4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          ar.a[l][4 * p + u] = tl[l * pw + d + u];
+          if constexpr (Q4) ar.a[l][G::DW + 4 * p + u] = tl[l * pw + KW + d + u];
+        }
+      }
+    const uint32_t v2 = group_sum_dpp<G::LPR>(lane_dot<Q4, G, NL>(w[i], ar));
+    return Q4 ? v2 - 8u * smr[i] : v2;
+  };
+  if (one) {
+    // both ranks' dots side by side (a dead rank's weights are zero; its
+    // result is not stored)
+    uint32_t tot[JP];
+#pragma unroll
+    for (int i = 0; i < JP; ++i) tot[i] = dot_rank(i, std::integral_constant<int, 1>());
+#pragma unroll
+    for (int i = 0; i < JP; ++i)
+      if (ej[i] >= 0 && r == 0 && row < r1)
+        yb[(size_t)(wave + NWV * i) * G::WR + g] = qdot_epilogue(tot[i], div, sc[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < JP; ++i) {
+      const int j = wave + NWV * i;
+      if (ej[i] < 0) continue;
+      if (nlr[i] <= NLF) {
+        const uint32_t tot = nlr[i] == 1 ? dot_rank(i, std::integral_constant<int, 1>())
+                                         : dot_rank(i, std::integral_constant<int, NLF>());
+        if (r == 0 && row < r1) yb[(size_t)j * G::WR + g] = qdot_epilogue(tot, div, sc[i]);
+      } else {
+        // activations past the register budget: the exact fallback on the
+        // fp32 h (its weights reloaded by the wave)
+        float* hj = hx + (size_t)j * K;
+        const uint64_t* th = f.ft.h + (size_t)j * K;
+        for (int k = lane; k < K; k += kWave) hj[k] = __uint_as_float(tag_wait(th + k, tag, deadline, late));
+        __threadfence_block();
+        __builtin_amdgcn_wave_barrier();
+        const uint8_t* W[1] = {a.dq + (size_t)ej[i] * a.D * a.rb};
+        DownEpi epi{a.ds + (size_t)ej[i] * a.D, yb + (size_t)j * G::WR, r0, div};
+        generic_rows_fp32<Q4, 1>(W, a.rb, K, hj, r0, r1, epi, 0, 1);
+      }
+    }
+  }
+  if (late) late_any = 1;
+  __syncthreads();
+  static_assert(G::WR <= kTileBlock, "a thread an output row");
+  if (r0 + tid < r1) {
+    const int o = r0 + tid;
+    float acc = 0.0f;
+    for (int j = 0; j < a.topk; ++j) {
+      if (gidx[j] < 0) continue;
+      const float py = gp[j] * yb[(size_t)j * G::WR + (o - r0)];
+      acc = acc + py;
+    }
+    float res = a.resid ? rv + acc : acc;
+    if (late_any) res = __builtin_nanf("");
+    a.out[o] = res;
+  }
+}
+
+template <bool Q4, class GG, class GD>
+__global__ __launch_bounds__(kTileBlock) void gate_up_down_kernel(FuseArgs f) {
+  extern __shared__ float fl[];
+  const uint32_t tag = *f.ft.epoch;
+  if ((int)blockIdx.x < f.ngu) {
+    int rc, q;
+    xcd_chunk_item(f.gu.nchunks, f.gu.npairs, &rc, &q);
+    gate_up_block<Q4, GG, true, true>(f.gu, rc, q, fl, &f.ft, tag);
+  } else {
+    down_fused_block<Q4, GD>(f, (int)blockIdx.x - f.ngu, tag, fl);
+  }
+}
+
 // rmsnorm (test_model_trace.c:241-255): one block per token; the squares
 // x_i * x_i are formed by all threads into LDS and summed in order by
 // block_seq_sum (msq / D, 1 / sqrtf(msq + eps)).
@@ -351,7 +603,9 @@ struct ScratchBuf {
 };
 struct SharedScratch {
   ScratchBuf logits, idx, p, xtab, htab, h, xn, hpart, xpart, ecount, eoff, perm, y, y16, tasks, ghist, rpart;
+  ScratchBuf ftag;                   // tagged words of the one-token gate/up + down launch
   unsigned* sel_counter = nullptr;   // fused selection's block counter, zero between launches
+  uint32_t* epoch = nullptr;         // the fused launch's tag, advanced by the router launch
 };
 SharedScratch g_scratch;
 std::mutex g_layer_mu;
@@ -405,6 +659,25 @@ moe_status ensure_scratch(LayerDev* L, int T) {
     if ((st = dev_alloc(&S.sel_counter, 1))) return st;
     if ((st = check_hip(hipMemsetAsync(S.sel_counter, 0, 4, stream()), "counter init"))) return st;
   }
+  if (T == 1 && L->topk <= kFuseTopK) {
+    // zero-filled when (re)allocated: tag 0 is never an epoch
+    const size_t words = (size_t)kFuseTopK * (4 * (((size_t)L->dff + 15) / 16 * 4) + L->dff +
+                                              2 * (((size_t)L->dff + 7) / 8));
+    const void* old = S.ftag.p;
+    if ((st = grow(S.ftag, words * 8, &synced))) return st;
+    if (S.ftag.p != old &&
+        (st = check_hip(hipMemsetAsync(S.ftag.p, 0, S.ftag.bytes, stream()), "tag buffer init")))
+      return st;
+    if (!S.epoch) {
+      if ((st = dev_alloc(&S.epoch, 1))) return st;
+      if ((st = check_hip(hipMemsetAsync(S.epoch, 0, 4, stream()), "epoch init"))) return st;
+    }
+    L->ftag = (uint64_t*)S.ftag.p;
+    L->epoch = S.epoch;
+  } else {
+    L->ftag = nullptr;
+    L->epoch = nullptr;
+  }
   L->y = (float*)S.y.p;
   L->y16 = L->dtype == 3 ? (int16_t*)S.y16.p : nullptr;
   L->sel_counter = S.sel_counter;
@@ -416,13 +689,16 @@ void release_scratch_all() {
   std::lock_guard<std::mutex> lk(g_layer_mu);
   SharedScratch& S = g_scratch;
   for (ScratchBuf* b : {&S.logits, &S.idx, &S.p, &S.xtab, &S.htab, &S.h, &S.xn, &S.hpart, &S.xpart,
-                        &S.ecount, &S.eoff, &S.perm, &S.y, &S.y16, &S.tasks, &S.ghist, &S.rpart}) {
+                        &S.ecount, &S.eoff, &S.perm, &S.y, &S.y16, &S.tasks, &S.ghist, &S.rpart,
+                        &S.ftag}) {
     dfree(b->p);
     b->p = nullptr;
     b->bytes = 0;
   }
   dfree(S.sel_counter);
   S.sel_counter = nullptr;
+  dfree(S.epoch);
+  S.epoch = nullptr;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
@@ -444,10 +720,9 @@ bool cached_loads(int T, int min_t) { return min_t > 0 && T >= min_t; }
 
 int down_target_blocks() { static const int v = env_int("MOEHIP_DOWN_BLOCKS", 512); return v; }
 
-template <bool Q4, class G>
-void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s,
-                    bool sel = false, int nxpart = 0, int32_t* idx_out = nullptr,
-                    float* p_out = nullptr, int xp_tok = 0, int xp_slice = 1) {
+template <class G>
+GateUpArgs gate_up_args(const LayerDev* L, const float* xn, int T, bool sel, int nxpart,
+                        int32_t* idx_out, float* p_out, int xp_tok, int xp_slice) {
   // rows per block: a multiple of both the wave-group unit and 8 (whole
   // packed dwords of h), sized for ~1024 blocks
   constexpr int unit0 = kTileWaves * G::WR;
@@ -469,16 +744,27 @@ void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hip
     if ((L->dff + r8 - 1) / r8 == nc8) rpb = r8;
   }
   const int nc = (int)((L->dff + rpb - 1) / rpb);
-  *nchunks = nc;
   GateUpArgs a{L->gq, L->gs, L->uq, L->us, L->rbg, L->D, L->dff, L->topk, L->idx,
                L->xtab, act_table_bytes(L->D), xn, L->h, L->htab, act_table_bytes(L->dff),
                L->hpart, nc, (int)rpb};
   a.npairs = npairs;
-  dim3 grid((unsigned)(nc * npairs));
   if (sel) {
     a.logits = L->logits; a.xpart = L->xpart; a.nxpart = nxpart; a.E = L->E;
     a.xp_tok = xp_tok; a.xp_slice = xp_slice;
     a.idx_w = L->idx; a.p = L->p; a.idx_user = idx_out; a.p_user = p_out;
+  }
+  return a;
+}
+
+template <bool Q4, class G>
+void launch_gate_up(const LayerDev* L, const float* xn, int T, int* nchunks, hipStream_t s,
+                    bool sel = false, int nxpart = 0, int32_t* idx_out = nullptr,
+                    float* p_out = nullptr, int xp_tok = 0, int xp_slice = 1) {
+  const GateUpArgs a = gate_up_args<G>(L, xn, T, sel, nxpart, idx_out, p_out, xp_tok, xp_slice);
+  const size_t rpb = (size_t)a.rows_per_block;
+  *nchunks = a.nchunks;
+  dim3 grid((unsigned)(a.nchunks * a.npairs));
+  if (sel) {
     if (cached_loads(T, gateup_cached_min_tokens()))
       hipLaunchKernelGGL((gate_up_kernel<Q4, G, true, false>), grid, dim3(kTileBlock), (size_t)rpb * 4, s, a);
     else
@@ -511,6 +797,48 @@ void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, floa
                        (size_t)L->topk * rpb * 4, s, a);
 }
 
+// Wall-clock ticks a fused launch's down block may wait for its inputs
+// (20 ms; the clock rate is the device's, read once).
+long long fuse_wait_ticks() {
+  static const long long v = [] {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+      khz = 100000;
+    return (long long)khz * 20;
+  }();
+  return v;
+}
+
+size_t fuse_lds(const LayerDev* L, int rpb_gu, int wr) {
+  const size_t pw = ((size_t)L->dff + 15) / 16 * 4;
+  const size_t dn = ((size_t)kFuseTopK * wr + (size_t)kFuseTopK * 2 * pw + (size_t)L->topk * L->dff) * 4;
+  const size_t gu = (size_t)rpb_gu * 4;
+  return dn > gu ? dn : gu;
+}
+
+template <bool Q4, class GG, class GD>
+void launch_gate_up_down(const LayerDev* L, const float* xn, const float* resid, float* out,
+                         int nxpart, int32_t* idx_out, float* p_out, int xp_tok, int xp_slice,
+                         hipStream_t s) {
+  FuseArgs f;
+  f.gu = gate_up_args<GG>(L, xn, 1, true, nxpart, idx_out, p_out, xp_tok, xp_slice);
+  f.dn = DownArgs{L->dq, L->ds, L->rbd, 1, L->D, L->dff, L->topk, L->idx, L->p, L->htab,
+                  act_table_bytes(L->dff), L->h, L->hpart, f.gu.nchunks, resid, out, GD::WR};
+  f.dn.nrc = (L->D + GD::WR - 1) / GD::WR;
+  const size_t pw = ((size_t)L->dff + 15) / 16 * 4;   // dwords per act-table plane
+  f.ft.pw = (int)pw;
+  f.ft.pchunks = (L->dff + 7) / 8;
+  f.ft.tab = L->ftag;
+  f.ft.h = L->ftag + (size_t)kFuseTopK * 4 * pw;
+  f.ft.part = f.ft.h + (size_t)kFuseTopK * L->dff;
+  f.ft.epoch = L->epoch;
+  f.ft.wait_ticks = fuse_wait_ticks();
+  f.ngu = f.gu.nchunks * f.gu.npairs;
+  hipLaunchKernelGGL((gate_up_down_kernel<Q4, GG, GD>), dim3((unsigned)(f.ngu + f.dn.nrc)),
+                     dim3(kTileBlock), fuse_lds(L, f.gu.rows_per_block, GD::WR), s, f);
+}
+
 // Row-byte dispatch for the expert GEMVs (same geometries as gemv.hip).
 template <bool Q4, class F>
 void with_geom(long long rb, F&& f) {
@@ -527,6 +855,24 @@ void with_geom(long long rb, F&& f) {
     case 4096: f(TileGeom<4, 64>()); return;
     default: f(GenericGeom()); return;
   }
+}
+
+// The fused one-token launch is built for Q4 at D = 2048, d_ff = 768 (the
+// model's layers).  Q8 at that shape measured slower fused (29.7 -> 33.6 us
+// a layer): its 768 gate/up blocks fill every slot, so the down blocks
+// start only as gate/up ends, with their selection still ahead of them.
+using FuseGG = TileGeom<4, 16>;
+using FuseGD = TileGeom<3, 8>;
+bool fuse_geoms(const LayerDev* L) { return L->dtype == 3 && L->rbg == 1024 && L->rbd == 384; }
+
+// The down blocks read two gate/up chunk partials a lane: at most 128 chunks.
+bool fuse_chunks_ok(const LayerDev* L) {
+  return gate_up_args<FuseGG>(L, nullptr, 1, true, 0, nullptr, nullptr, 0, 1).nchunks <= 2 * kWave;
+}
+
+void launch_fused(const LayerDev* L, const float* xn, const float* resid, float* out, int nxpart,
+                  int32_t* idx_out, float* p_out, int xp_tok, int xp_slice, hipStream_t s) {
+  launch_gate_up_down<true, FuseGG, FuseGD>(L, xn, resid, out, nxpart, idx_out, p_out, xp_tok, xp_slice, s);
 }
 
 }  // namespace
@@ -601,6 +947,13 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
   const bool sel_gu = !sel_kernel && T <= sel_gu_max_t && L->E <= kTileBlock &&
                       ((fuse_sel && dense_row_path(ra)) || (rows_pack && T <= 16));
   ra.sel_defer = sel_gu && fuse_sel ? 1 : 0;
+  // one token: gate/up and down in one launch, where its geometries are built
+  static const bool no_fuse_gd = getenv("MOEHIP_NO_FUSE_GD") != nullptr;
+  const bool fuse_gd = !no_fuse_gd && T == 1 && sel_gu && fuse_sel && ra.sel_defer && L->ftag &&
+                       L->epoch && L->topk <= kFuseTopK && fuse_geoms(L) && fuse_chunks_ok(L) &&
+                       ((size_t)L->dff + 15) / 16 * 4 <= (size_t)kWave * kFusePlaneWords &&
+                       fuse_lds(L, 0, 64) <= 64 * 1024;
+  if (fuse_gd) ra.epoch_bump = L->epoch;
   if ((st = dense_matmul(ra, s))) return st;
   if (!fuse_sel && !sel_gu &&
       (st = launch_select(L, T, idx_out, p_out, s,
@@ -609,6 +962,10 @@ moe_status layer_forward_run(LayerDev* L, const float* x, float norm_eps, const 
     return st;
   const int nxpart = ra.pack_dtype ? L->E : 0;
   const int xp_tok = rows_pack ? 1 : L->E, xp_slice = rows_pack ? 16 : 1;
+  if (fuse_gd) {
+    launch_fused(L, xn, resid, out, nxpart, idx_out, p_out, xp_tok, xp_slice, s);
+    return check_hip(hipGetLastError(), "gate_up/down launch");
+  }
   int nchunks = 0;
   if (q4) with_geom<true>(L->rbg, [&](auto g) { launch_gate_up<true, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out, xp_tok, xp_slice); });
   else with_geom<false>(L->rbg, [&](auto g) { launch_gate_up<false, decltype(g)>(L, xn, T, &nchunks, s, sel_gu, nxpart, idx_out, p_out, xp_tok, xp_slice); });
@@ -900,6 +1257,8 @@ moe_status moe_layer_forward_noalloc(moe_layer* layer, const float* x_norm, cons
   L->tasks = nullptr;
   L->y = nullptr;
   L->y16 = nullptr;
+  L->ftag = nullptr;   // the no-allocation forward keeps two launches for gate/up and down
+  L->epoch = nullptr;
   L->capT = T;
   return layer_forward_run(L, x_norm, -1.0f, x_resid, T, out, idx_out, p_out, false);
 }

@@ -136,13 +136,73 @@ __device__ void pack_act_row(const float* __restrict__ x, int K, uint8_t* __rest
   }
 }
 
+// ---- tagged words: hand-overs between the blocks of one launch ----
+//
+// A 64-bit word {tag, value} stored and loaded with relaxed agent-scope
+// atomics: a load sees the stores to its own address in order (per-location
+// coherence, across the XCDs' L2s), so a reader that finds the current
+// launch's tag has that launch's value -- no fence, no flag, no release
+// (a device-scope release is an L2 write-back per block on gfx950).
+__device__ __forceinline__ uint64_t tag_word(uint32_t tag, uint32_t v) {
+  return ((uint64_t)tag << 32) | v;
+}
+__device__ __forceinline__ void tag_put(uint64_t* p, uint32_t tag, uint32_t v) {
+  __hip_atomic_store(p, tag_word(tag, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value at p once it carries `tag`; past `deadline` (wall clock) it
+// stops waiting and sets `late` (the caller then poisons its results), so
+// every wait ends.
+__device__ __forceinline__ uint32_t tag_wait(const uint64_t* p, uint32_t tag, long long deadline,
+                                             bool& late) {
+  uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while ((uint32_t)(w >> 32) != tag) {
+    if (late || wall_clock64() > deadline) {
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return (uint32_t)w;
+}
+
+// N tagged words at once (addr(i) gives word i's address): every load
+// issued first, then only the stale words polled again, so the wait costs
+// one round trip when the words are there.  Same deadline rule as tag_wait.
+template <int N, int SLEEP = 2, class Addr>
+__device__ __forceinline__ void tag_wait_all(Addr addr, uint32_t (&v)[N], uint32_t tag,
+                                             long long deadline, bool& late) {
+  uint64_t w[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = __hip_atomic_load(addr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ok = ok && (uint32_t)(w[i] >> 32) == tag;
+    if (ok || late) break;
+    if (wall_clock64() > deadline) {
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(SLEEP);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((uint32_t)(w[i] >> 32) != tag)
+        w[i] = __hip_atomic_load(addr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = (uint32_t)w[i];
+}
+
 // Packs columns [c0, c1) of one activation row (x points at column 0) into
 // the table's planes; c0 is a multiple of 8.  Returns this thread's limb
 // count and activation sum over the columns it packed; threads of a team
-// (tid in [0, nthr)) split the work.
+// (tid in [0, nthr)) split the work.  ttab (optional): every plane dword
+// also as a tagged word, plane l's dword i at ttab[l * plane dwords + i].
 template <bool Q4>
 __device__ void pack_act_cols(const float* x, int K, int c0, int c1, uint8_t* tab, int tid,
-                              int nthr, int& nl_out, uint32_t& sum_out) {
+                              int nthr, int& nl_out, uint32_t& sum_out,
+                              uint64_t* ttab = nullptr, uint32_t tag = 0) {
   const float mult = Q4 ? 7.0f : 127.0f;
   constexpr int V = Q4 ? 8 : 4;
   const size_t plane = (((size_t)K + 15) / 16) * 16;
@@ -166,11 +226,20 @@ __device__ void pack_act_cols(const float* x, int K, int c0, int c1, uint8_t* ta
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
       uint32_t* pl = p0 + (size_t)l * (plane / 4);
+      uint64_t* tl = ttab ? ttab + (size_t)l * (plane / 4) : nullptr;
       if constexpr (!Q4) {
-        pl[d] = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+        const uint32_t v = pack4(b[0][l], b[1][l], b[2][l], b[3][l]);
+        pl[d] = v;
+        if (tl) tag_put(tl + d, tag, v);
       } else {
-        pl[d] = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
-        pl[KW + d] = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
+        const uint32_t ve = pack4(b[0][l], b[2][l], b[4][l], b[6][l]);
+        const uint32_t vo = pack4(b[1][l], b[3][l], b[5][l], b[7][l]);
+        pl[d] = ve;
+        pl[KW + d] = vo;
+        if (tl) {
+          tag_put(tl + d, tag, ve);
+          tag_put(tl + KW + d, tag, vo);
+        }
       }
     }
   }

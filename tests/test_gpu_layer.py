@@ -168,6 +168,45 @@ def test_decode_dead_slots(moehip, T):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("case", ["plain", "two_limb_rows", "dead_slots", "top4"])
+def test_fused_one_token_gate_up_down(moehip, case):
+    """One token at the Q4 shape whose gate/up and down share one launch
+    (E = 128, D = 2048, d_ff = 768): the down blocks select for themselves
+    and take h's tables, limb counts and sums from the gate/up blocks'
+    tagged words.  two_limb_rows: gate/up row scales of d_ff rows 0-63 x
+    1000, so h needs two limbs there and the down blocks take the exact
+    fallback on the tagged fp32 h; dead_slots: router rows 5-127 NaN, so
+    ranks 5-7 hold -1 (their down terms drop out, waves 1-3's second rank is
+    dead); top4: top-k 4 (every wave's second rank is past k).  Each case
+    runs twice, the first call on 1000x larger activations (every h value
+    two limbs), so that a word left by an earlier launch would show."""
+    dtype, E, D, dff = 3, 128, 2048, 768
+    seed = {"plain": 9700, "two_limb_rows": 9710, "dead_slots": 9720, "top4": 9730}[case]
+    top_k = 4 if case == "top4" else 8
+    print("fused one-token case", case, flush=True)
+    ex = random_experts(dtype, E, D, dff, seed)
+    if case == "two_limb_rows":
+        ex.gs[:, :64] *= 1000.0
+        ex.us[:, :64] *= 1000.0
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    if case == "dead_slots":
+        rw[5:, 7] = np.nan
+    xn = O.normal(D, seed + 12, 0.0, 1.0).reshape(1, D)
+    big = np.ascontiguousarray(xn * np.float32(1000.0))
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex, top_k=top_k)
+    want_big, widx_big, _, _ = O.moe_block(big, xn, rw, None, ex, top_k=top_k)
+    if case == "dead_slots":
+        assert (widx[:, 5:] == -1).all() and (widx[:, :5] >= 0).all()
+    layer = make_layer(moehip, dtype, ex, rw, top_k=top_k)
+    got_big, idx_big, _ = layer.forward(big, xn)
+    np.testing.assert_array_equal(idx_big, widx_big)
+    np.testing.assert_array_equal(bits(got_big), bits(want_big))
+    got, idx, p = layer.forward(xn, xn)
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_rmsnorm_dev(moehip):
     for T, D in ((3, 2048), (2, 100)):
         x = O.normal(T * D, 5 + D, 0.0, 2.0).reshape(T, D)
