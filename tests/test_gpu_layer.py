@@ -207,6 +207,40 @@ def test_fused_one_token_gate_up_down(moehip, case):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def test_router_block_sum_special_rows(moehip):
+    """The one-token router's product sums at D = 2048 (block-parallel
+    candidate segments) against the oracle's loop, bit for bit, on rows
+    built to stress them: partial sums that cross zero often (alternating
+    +-c pairs with a small drift, where segment estimates miss and the
+    sequential fallback runs), exact cancellation to zero, 1e30 / 1e-30
+    terms side by side, an overflow to inf and then NaN, a NaN term,
+    all-zero and all-equal rows, and plain random rows."""
+    dtype, E, D, dff = 3, 16, 2048, 256
+    seed = 9800
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    k = np.arange(D)
+    rw[0] = np.where(k % 2 == 0, 1.0, -1.0) * (1.0 + 1e-3 * (k % 7))
+    rw[1, : D // 2] = 0.5
+    rw[1, D // 2:] = -0.5
+    rw[2] = np.where(k % 3 == 0, 1e30, np.where(k % 3 == 1, 1e-30, -1e30))
+    rw[3, :] = 3e38
+    rw[3, D // 2:] = -3e38
+    rw[4, 1000] = np.nan
+    rw[5] = 0.0
+    rw[6] = 0.25
+    rw[7] = np.sin(k * 0.37) * np.exp(-k / 700.0)
+    xn = np.abs(O.normal(D, seed + 12, 0.0, 1.0)).reshape(1, D) + np.float32(0.5)
+    want, widx, wp, wlog = O.moe_block(xn, xn, rw.astype(np.float32), None, ex)
+    layer = make_layer(moehip, dtype, ex, rw.astype(np.float32))
+    got, idx, p = layer.forward(xn, xn)
+    dbg = layer.debug(1)
+    np.testing.assert_array_equal(bits(dbg["logits"]), bits(wlog))
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(bits(p), bits(wp))
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_rmsnorm_dev(moehip):
     for T, D in ((3, 2048), (2, 100)):
         x = O.normal(T * D, 5 + D, 0.0, 2.0).reshape(T, D)
