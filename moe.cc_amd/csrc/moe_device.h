@@ -218,7 +218,7 @@ constexpr int kSeqCands = 64;
 
 struct SeqSumScratch {
   double part[kSeqSegs];
-  float cand[kSeqSegs][kSeqCands];
+  uint32_t base[kSeqSegs];   // key of each segment's first candidate
   float out[kSeqSegs][kSeqCands];
   float result;
 };
@@ -290,9 +290,11 @@ __device__ __forceinline__ float group_seq_sum(const float* p, int n, SeqSumScra
 #pragma unroll
     for (int q = 0; q < S - 1; ++q)
       if (q < j) est += sc.part[q];
-    const int32_t base = seq_key((float)est) - kSeqCands / 2 + i * CPT;
+    // candidate c = i * CPT + u has key base + c (keys wrap as uint32)
+    const uint32_t base = (uint32_t)seq_key((float)est) - (uint32_t)(kSeqCands / 2);
+    if (i == 0) sc.base[j] = base;
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) c[u] = seq_unkey(base + u);
+    for (int u = 0; u < CPT; ++u) c[u] = seq_unkey((int32_t)(base + (uint32_t)(i * CPT + u)));
   } else {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) c[u] = 0.0f;   // segment 0 starts at +0
@@ -328,28 +330,28 @@ __device__ __forceinline__ float group_seq_sum(const float* p, int n, SeqSumScra
     }
   }
 #pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    sc.cand[j][i * CPT + u] = c[u];
-    sc.out[j][i * CPT + u] = acc[u];
-  }
+  for (int u = 0; u < CPT; ++u) sc.out[j][i * CPT + u] = acc[u];
   __syncthreads();
   // 5. stitch the segments in order (wave 0, lane l <-> candidate l; all
-  // candidates and outputs read up front)
+  // outputs read up front).  Segment 0's chains all start at +0.  A true
+  // start t is candidate key(t) - base of its segment when that index is
+  // below kSeqCands (key is a bijection, candidates are consecutive keys):
+  // one subtraction and a readlane per segment, no search.
   if (tid < 64) {
     const int lane = tid;
-    uint32_t cb[S];
+    uint32_t bs[S];
     float ob[S];
 #pragma unroll
     for (int q = 0; q < S; ++q) {
-      cb[q] = __float_as_uint(sc.cand[q][lane]);
+      bs[q] = sc.base[q];
       ob[q] = sc.out[q][lane];
     }
-    float t = 0.0f;
+    float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ob[0]), 0));
 #pragma unroll
-    for (int q = 0; q < S; ++q) {
-      const unsigned long long m = __ballot(cb[q] == __float_as_uint(t));
-      if (m) {
-        t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ob[q]), __ffsll((long long)m) - 1));
+    for (int q = 1; q < S; ++q) {
+      const uint32_t idx = (uint32_t)seq_key(t) - bs[q];
+      if (idx < (uint32_t)kSeqCands) {
+        t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ob[q]), (int)idx));
       } else {
         const int q0 = min(n, q * L), q1 = min(n, q0 + L);
         int k = q0;
