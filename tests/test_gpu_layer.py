@@ -168,24 +168,26 @@ def test_decode_dead_slots(moehip, T):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("case", ["plain", "two_limb_rows", "dead_slots", "top4"])
-def test_fused_one_token_gate_up_down(moehip, case):
-    """One token at the Q4 shape whose gate/up and down share one launch
-    (E = 128, D = 2048, d_ff = 768): the down blocks select for themselves
-    and take h's tables, limb counts and sums from the gate/up blocks'
-    tagged words.  two_limb_rows: gate/up row scales of d_ff rows 0-63 x
-    1000, so h needs two limbs there and the down blocks take the exact
-    fallback on the tagged fp32 h; dead_slots: router rows 5-127 NaN, so
-    ranks 5-7 hold -1 (their down terms drop out, waves 1-3's second rank is
-    dead); top4: top-k 4 (every wave's second rank is past k).  Each case
-    runs twice, the first call on 1000x larger activations (every h value
-    two limbs), so that a word left by an earlier launch would show."""
-    dtype, E, D, dff = 3, 128, 2048, 768
-    seed = {"plain": 9700, "two_limb_rows": 9710, "dead_slots": 9720, "top4": 9730}[case]
+@pytest.mark.parametrize("dtype", [3, 2])
+@pytest.mark.parametrize("case", ["plain", "big_rows", "dead_slots", "top4"])
+def test_fused_one_token_gate_up_down(moehip, dtype, case):
+    """One token at E = 128, D = 2048, d_ff = 768.  Q4: gate/up and down
+    share one launch -- the down blocks select for themselves and take h's
+    tables, limb counts and sums from the gate/up blocks' tagged words; Q8
+    (two launches at this shape) as the per-pair reference point.  big_rows:
+    gate/up row scales of d_ff rows 0-63 x 1000, so h needs two limbs there
+    (Q4: the down blocks' exact fallback on the tagged fp32 h; Q8: two
+    planes, or four where |h| passes 257); dead_slots: router rows 5-127
+    NaN, so ranks 5-7 hold -1 (their down terms drop out, waves 1-3's
+    second rank is dead); top4: top-k 4 (every wave's second rank is past
+    k).  Each case runs twice, the first call on 1000x larger activations,
+    so that a word left by an earlier launch would show."""
+    E, D, dff = 128, 2048, 768
+    seed = {"plain": 9700, "big_rows": 9710, "dead_slots": 9720, "top4": 9730}[case] + dtype
     top_k = 4 if case == "top4" else 8
-    print("fused one-token case", case, flush=True)
+    print("fused one-token case", dtype, case, flush=True)
     ex = random_experts(dtype, E, D, dff, seed)
-    if case == "two_limb_rows":
+    if case == "big_rows":
         ex.gs[:, :64] *= 1000.0
         ex.us[:, :64] *= 1000.0
     rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
