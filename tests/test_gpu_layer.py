@@ -209,6 +209,28 @@ def test_fused_one_token_gate_up_down(moehip, dtype, case):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def test_fused_one_token_between_other_paths(moehip):
+    """The fused one-token launch between calls on the other paths (T = 1,
+    3, 1, 40, 1, 2, 1 at the Q4 fused shape: per-pair kernels at 2-3 tokens,
+    expert-major at 40): its tags come from an epoch only its own router
+    launches advance, so the words the earlier fused calls left are never
+    current in a later one; each call against the oracle."""
+    dtype, E, D, dff = 3, 128, 2048, 768
+    seed = 9750
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    layer = make_layer(moehip, dtype, ex, rw)
+    for i, T in enumerate((1, 3, 1, 40, 1, 2, 1)):
+        print("fused-shape sequence call", i, "T", T, flush=True)
+        xn = O.normal(T * D, seed + 20 + i, 0.0, 1.0).reshape(T, D)
+        xr = O.normal(T * D, seed + 40 + i, 0.0, 1.0).reshape(T, D)
+        want, widx, wp, _ = O.moe_block(xn, xr, rw, None, ex)
+        got, idx, p = layer.forward(xn, xr)
+        np.testing.assert_array_equal(idx, widx)
+        np.testing.assert_array_equal(bits(p), bits(wp))
+        np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_router_block_sum_special_rows(moehip):
     """The one-token router's product sums at D = 2048 (block-parallel
     candidate segments) against the oracle's loop, bit for bit, on rows
