@@ -107,6 +107,9 @@ struct AttnArgs {
   int fuse_heads = 0;
   const float* q_norm = nullptr; const float* k_norm = nullptr; float eps = 0.0f;
   const float* rope_cos = nullptr; const float* rope_sin = nullptr;
+  // set by attention_rows: the one-row kernels' blocks of one KV head group
+  // share an XCD (attn_xcd_map)
+  int xcd_map = 0;
 };
 moe_status attention_rows(const AttnArgs& a, hipStream_t s);
 

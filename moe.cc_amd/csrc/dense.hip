@@ -818,6 +818,26 @@ __global__ __launch_bounds__(64) void heads_kernel(HeadArgs a) {
 // caches.  All global loads are issued first.
 constexpr int kRegHd = 128;
 
+// (x, y) work indices of this block in a 2-D grid, permuted so that blocks
+// with consecutive y (heads of one KV group) share an XCD: blocks are dealt
+// to the 8 XCDs in turn, so XCD k runs the blocks whose linear index is k
+// mod 8, and those get logical indices k n/8 .. k n/8 + n/8 - 1 (x fastest).
+// The K and V rows a KV head's blocks read then come from one XCD's L2
+// instead of every XCD's.  The identity when n is not a multiple of 8 or
+// with MOEHIP_ATTN_NO_XCD set.
+__device__ __forceinline__ void attn_xcd_map(bool on, int* bx, int* by) {
+  const int gx = (int)gridDim.x, n = gx * (int)gridDim.y;
+  const int L = (int)blockIdx.x + gx * (int)blockIdx.y;
+  if (!on || n % 8) {
+    *bx = (int)blockIdx.x;
+    *by = (int)blockIdx.y;
+    return;
+  }
+  const int Lg = (L % 8) * (n / 8) + L / 8;
+  *bx = Lg % gx;
+  *by = Lg / gx;
+}
+
 template <bool REG>
 __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   extern __shared__ float lds[];
@@ -833,9 +853,11 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(AttnArgs a) {
   float* sn = cs + hdp;                 // [hd/2]
   float* sq = sn + hdp;                 // [2][hd]
   __shared__ float inv_s[2];
-  const int t = blockIdx.z, h = blockIdx.y, lane = threadIdx.x;
+  int bx, h;
+  attn_xcd_map(a.xcd_map, &bx, &h);
+  const int t = blockIdx.z, lane = threadIdx.x;
   const int P = a.pos0 + t;
-  const int tk0 = blockIdx.x * 64;
+  const int tk0 = bx * 64;
   if (tk0 > P) return;
   const int group = a.nq / a.nkv;
   const int kvh = h / group;
@@ -990,7 +1012,9 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   constexpr int LDT = CH + 4;
   extern __shared__ float lds[];
   const int hd = a.hd;
-  const int t = blockIdx.z, h = blockIdx.y;
+  int bx, h;
+  attn_xcd_map(a.xcd_map, &bx, &h);
+  const int t = blockIdx.z;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int n = a.pos0 + t + 1;
   float* es = lds;                                  // [max_seq, rounded up to 4]
@@ -998,7 +1022,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   __shared__ float red[kPvThreads / kWave];
   __shared__ SeqSumScratch seq;
   const int kvh = h / (a.nq / a.nkv);
-  const int d0 = DPB * blockIdx.x;
+  const int d0 = DPB * bx;
   const int dl = min(DPB, hd - d0);
   const float* vbase = a.vc + (size_t)kvh * a.max_seq * hd + d0;
   const int nch = (n + CH - 1) / CH;
@@ -1717,15 +1741,18 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
   }
   const int nmax = a.pos0 + a.T;   // positions of the last row
   const size_t hdp = (size_t)((a.hd + 3) & ~3);
+  static const bool no_xcd = getenv("MOEHIP_ATTN_NO_XCD") != nullptr;
+  AttnArgs ax = a;
+  ax.xcd_map = no_xcd ? 0 : 1;
   const dim3 sgrid((unsigned)((nmax + 63) / 64), (unsigned)a.nq, (unsigned)a.T);
   moe_status st;
   if (a.hd <= kRegHd) {
     const size_t lds_s = 10 * hdp * 4;
-    hipLaunchKernelGGL(attn_scores_kernel<true>, sgrid, dim3(64), lds_s, s, a);
+    hipLaunchKernelGGL(attn_scores_kernel<true>, sgrid, dim3(64), lds_s, s, ax);
   } else {
     const size_t lds_s = (9 * hdp + 64 * (size_t)(a.hd + 4)) * 4;
     if ((st = set_lds(attn_scores_kernel<false>, lds_s, "scores LDS attribute"))) return st;
-    hipLaunchKernelGGL(attn_scores_kernel<false>, sgrid, dim3(64), lds_s, s, a);
+    hipLaunchKernelGGL(attn_scores_kernel<false>, sgrid, dim3(64), lds_s, s, ax);
   }
   if ((st = check_hip(hipGetLastError(), "scores launch"))) return st;
   const size_t es_f = (size_t)((a.max_seq + 3) & ~3);
@@ -1733,12 +1760,12 @@ moe_status attention_rows(const AttnArgs& a, hipStream_t s) {
     const size_t lds_p = (es_f + 16 * (16384 / 16 + 4)) * 4;
     if ((st = set_lds(attn_softmax_pv_kernel<16>, lds_p, "softmax/pv LDS attribute"))) return st;
     hipLaunchKernelGGL(attn_softmax_pv_kernel<16>, dim3((unsigned)((a.hd + 15) / 16), (unsigned)a.nq, (unsigned)a.T),
-                       dim3(kPvThreads), lds_p, s, a);
+                       dim3(kPvThreads), lds_p, s, ax);
   } else {
     const size_t lds_p = (es_f + 128 * (16384 / 128 + 4)) * 4;
     if ((st = set_lds(attn_softmax_pv_kernel<128>, lds_p, "softmax/pv LDS attribute"))) return st;
     hipLaunchKernelGGL(attn_softmax_pv_kernel<128>, dim3((unsigned)((a.hd + 127) / 128), (unsigned)a.nq, (unsigned)a.T),
-                       dim3(kPvThreads), lds_p, s, a);
+                       dim3(kPvThreads), lds_p, s, ax);
   }
   return check_hip(hipGetLastError(), "softmax/pv launch");
 }
