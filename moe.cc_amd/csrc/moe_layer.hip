@@ -799,15 +799,19 @@ void launch_down(const LayerDev* L, int T, int nchunks, const float* resid, floa
 
 // Wall-clock ticks a fused launch's down block may wait for its inputs
 // (20 ms; the clock rate is the device's, read once).
+// MOEHIP_FUSE_WAIT_US (read at every launch; tests set 0 to drive the
+// deadline path from the host) overrides the 20 ms.
 long long fuse_wait_ticks() {
-  static const long long v = [] {
-    int dev = 0, khz = 0;
+  static const long long khz = [] {
+    int dev = 0, k = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
-      khz = 100000;
-    return (long long)khz * 20;
+        hipDeviceGetAttribute(&k, hipDeviceAttributeWallClockRate, dev) != hipSuccess || k <= 0)
+      k = 100000;
+    return (long long)k;
   }();
-  return v;
+  const char* us = getenv("MOEHIP_FUSE_WAIT_US");
+  const long long wait_us = us && *us ? atoll(us) : 20000;
+  return khz * (wait_us < 0 ? 0 : wait_us) / 1000;
 }
 
 size_t fuse_lds(const LayerDev* L, int rpb_gu, int wr) {

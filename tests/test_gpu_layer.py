@@ -209,6 +209,33 @@ def test_fused_one_token_gate_up_down(moehip, dtype, case):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+def test_fused_one_token_deadline(moehip, monkeypatch):
+    """The fused launch's bounded waits, forced from the host: with a wait
+    limit of 0 a down block that does not find its words at the first look
+    gives up and writes NaN for its rows.  Every output row is then either
+    the oracle's bits or NaN -- never a wrong number -- and the launch
+    completes; with the limit back every row is exact again."""
+    dtype, E, D, dff = 3, 128, 2048, 768
+    seed = 9770
+    ex = random_experts(dtype, E, D, dff, seed)
+    rw = O.normal(E * D, seed + 10, 0.0, 0.02).reshape(E, D)
+    layer = make_layer(moehip, dtype, ex, rw)
+    xn = O.normal(D, seed + 12, 0.0, 1.0).reshape(1, D)
+    want, widx, wp, _ = O.moe_block(xn, xn, rw, None, ex)
+    monkeypatch.setenv("MOEHIP_FUSE_WAIT_US", "0")
+    nan_rows = 0
+    for _ in range(4):
+        got, idx, p = layer.forward(xn, xn)
+        np.testing.assert_array_equal(idx, widx)
+        bad = ~np.isnan(got[0])
+        np.testing.assert_array_equal(bits(got[0][bad]), bits(want[0][bad]))
+        nan_rows += int(np.isnan(got[0]).sum())
+    print("outputs given up at the deadline:", nan_rows, "of", 4 * D, flush=True)
+    monkeypatch.delenv("MOEHIP_FUSE_WAIT_US")
+    got, idx, p = layer.forward(xn, xn)
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
 def test_fused_one_token_between_other_paths(moehip):
     """The fused one-token launch between calls on the other paths (T = 1,
     3, 1, 40, 1, 2, 1 at the Q4 fused shape: per-pair kernels at 2-3 tokens,
