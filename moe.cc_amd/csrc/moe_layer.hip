@@ -663,9 +663,11 @@ moe_status ensure_scratch(LayerDev* L, int T) {
     // zero-filled when (re)allocated: tag 0 is never an epoch
     const size_t words = (size_t)kFuseTopK * (4 * (((size_t)L->dff + 15) / 16 * 4) + L->dff +
                                               2 * (((size_t)L->dff + 7) / 8));
+    // (zeroed on every reallocation, even one at the same address)
     const void* old = S.ftag.p;
+    const size_t old_bytes = S.ftag.bytes;
     if ((st = grow(S.ftag, words * 8, &synced))) return st;
-    if (S.ftag.p != old &&
+    if ((S.ftag.p != old || S.ftag.bytes != old_bytes) &&
         (st = check_hip(hipMemsetAsync(S.ftag.p, 0, S.ftag.bytes, stream()), "tag buffer init")))
       return st;
     if (!S.epoch) {
