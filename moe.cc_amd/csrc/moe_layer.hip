@@ -127,7 +127,9 @@ struct GateUpArgs {
 // Tagged copies of gate/up's outputs for the one-token gate/up + down
 // launch, and that launch's tag: an epoch that the router launch before it
 // advances (so every launch, graph replays included, has its own tag and a
-// word left from an earlier launch never passes for a current one).
+// word left from an earlier launch never passes for a current one -- the
+// 32-bit epoch would come round again only after 2^32 launches, ~4 days of
+// continuous decode, and every launch rewrites the words it reads).
 struct FuseTags {
   uint64_t* tab = nullptr;     // [pair][4 planes][pw] the h tables' plane dwords
   uint64_t* h = nullptr;       // [pair][dff] fp32 h (for the exact fallback)
