@@ -110,7 +110,16 @@ struct AttnArgs {
   // set by attention_rows: the one-row kernels' blocks of one KV head group
   // share an XCD (attn_xcd_map)
   int xcd_map = 0;
+  // Optional, T == 1: the matrix of the product that follows (the O
+  // projection, pf_n rows of leading dimension pf_ld).  Block b of the
+  // softmax launch requests the first kAttnPfCols columns of rows
+  // kAttnPfRows b .. kAttnPfRows b + kAttnPfRows - 1 while it waits for
+  // its scores, so that the product's first chunks come from the
+  // memory-side cache; the values are not used.
+  const float* pf_w = nullptr;
+  int pf_ld = 0, pf_n = 0;
 };
+constexpr int kAttnPfRows = 8, kAttnPfCols = 512;
 moe_status attention_rows(const AttnArgs& a, hipStream_t s);
 
 // The reference's next token over n logits (test_model_trace.c:735-746):

@@ -1111,15 +1111,36 @@ __global__ __launch_bounds__(kPvThreads) void attn_softmax_pv_kernel(AttnArgs a)
   for (int i = tid; i < n; i += kPvThreads) es[i] = es[i] * inv;
   __syncthreads();
   float out = 0.0f;
+  // the next product's first chunks toward the memory-side cache (values
+  // unused), requested once the V tile is in LDS so that no wait for V or
+  // the scores counts them
+  constexpr int PFN = kAttnPfRows * kAttnPfCols / 4 / kPvThreads;
+  float4 pfv[PFN];
+  const bool pf = a.pf_w && t == 0 && DPB == 16;
   for (int c = 0; c < nch; ++c) {
     store(c);
     if (c + 1 < nch) load(c + 1);
+    if (c == 0 && pf) {
+      const int b = (int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y;
+#pragma unroll
+      for (int u = 0; u < PFN; ++u) {
+        const int i = tid + kPvThreads * u;
+        const int row = kAttnPfRows * b + i / (kAttnPfCols / 4), c4 = i % (kAttnPfCols / 4);
+        pfv[u] = row < a.pf_n && 4 * c4 + 4 <= a.pf_ld
+                     ? *reinterpret_cast<const float4*>(a.pf_w + (size_t)row * a.pf_ld + 4 * c4)
+                     : zero4();
+      }
+    }
     __syncthreads();
     const int np = min(CH, n - c * CH);
     if (tid < dl) out = chain_sum(out, pt + tid * LDT, (np + 3) / 4);
     __syncthreads();
   }
   if (tid < dl) a.H[(size_t)t * a.nq * hd + (size_t)h * hd + d0 + tid] = out;
+  if (pf) {
+#pragma unroll
+    for (int u = 0; u < PFN; ++u) asm volatile("" ::"v"(pfv[u].x));   // keeps the requests
+  }
 }
 
 // ---- many query rows (prefill): several rows share each staged K / V tile ----

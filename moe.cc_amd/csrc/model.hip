@@ -230,6 +230,10 @@ moe_status forward_dev(moe_model* m, const int32_t* ids_d, int T, float* logits_
       aa.fuse_heads = 1;
       aa.q_norm = L.q_norm; aa.k_norm = L.k_norm; aa.eps = eps;
       aa.rope_cos = m->rope_cos; aa.rope_sin = m->rope_sin;
+      static const bool no_pf = getenv("MOEHIP_NO_WO_PREFETCH") != nullptr;
+      if (!no_pf) {
+        aa.pf_w = L.wo; aa.pf_ld = m->Dq; aa.pf_n = D;
+      }
     } else {
       HeadArgs ha{qkv, m->nqkv, T, m->pos, c.n_q, c.n_kv, hd, m->max_seq, L.q_norm, L.k_norm,
                   eps, m->rope_cos, m->rope_sin, kc, vc};
